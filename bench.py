@@ -1,0 +1,310 @@
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Headline (BASELINE.json metric, configs[1]): one decode step's Q8_0 matvec
+set of a dense 9B-class layer (q, k, v, o 4096->4096; gate, up 4096->12288;
+down 12288->4096) plus the lm_head matvec 4096->151936, batch 1, FP32
+activations.  value = algorithmic bytes (weights + x + y) / time, GB/s, with
+all inputs resident in HBM.  Distinct weight copies are rotated so the
+256 MB Infinity Cache cannot serve them.  The other configurations are
+reported under "configs" (matvec GB/s, GEMM TFLOP/s, MoE).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-configs] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-configs", action="store_true", help="headline only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def mv_bytes(m) -> int:
+    return m.nbytes + 4 * m.cols + 4 * m.rows
+
+
+def copies_for(total_bytes: int) -> int:
+    """Distinct copies so that a full rotation is >= 4x the Infinity Cache."""
+    return max(2, -(-4 * MALL_BYTES // total_bytes))
+
+
+def capture(torch, fn):
+    """Capture fn's launches (all on the current stream) into a HIP graph."""
+    fn()  # eager warm-up outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def check_replays(torch, graph, eager, outputs, times=3):
+    """Every replay must reproduce the eager result bit for bit (the kernels are
+    deterministic); eager work runs between the replays."""
+    eager()
+    torch.cuda.synchronize()
+    want = [o.clone() for o in outputs]
+    for _ in range(times):
+        for o in outputs:
+            o.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, w in zip(outputs, want):
+            if not torch.equal(o.view(torch.int32), w.view(torch.int32)):
+                raise RuntimeError("graph replay differs from the eager result")
+        eager()
+        torch.cuda.synchronize()
+
+
+def headline(torch, q3x, wl, steps, warmup):
+    mats = wl.dense_matrices(1)
+    layer = [m for m in mats if m.name != "lm_head"]
+    lm = [m for m in mats if m.name == "lm_head"][0]
+    layer_bytes = sum(m.nbytes for m in layer)
+    n_layer = copies_for(layer_bytes)
+    n_lm = copies_for(lm.nbytes)
+    layer_sets = [layer] + [[wl.Matrix(m.name, m.type, m.rows, m.cols, m.weight.clone()) for m in layer]
+                            for _ in range(n_layer - 1)]
+    lm_set = [lm] + [wl.Matrix(lm.name, lm.type, lm.rows, lm.cols, lm.weight.clone()) for _ in range(n_lm - 1)]
+    x = wl.activations(1, 1, 12288)[0].contiguous()
+    ys = {m.name: torch.empty(m.rows, dtype=torch.float32, device="cuda") for m in mats}
+    step_bytes = sum(mv_bytes(m) for m in mats)
+
+    def run_layer(r):
+        for m in layer_sets[r]:
+            q3x.mv(m.linear, x, ys[m.name])
+
+    def run_lm(r):
+        q3x.mv(lm_set[r].linear, x, ys["lm_head"])
+
+    # The layer set (seven launches) is replayed as a HIP graph; lm_head is
+    # launched directly between two events.  The host queues it while the GPU
+    # still runs the layer graph, so the events bracket the lm_head kernel
+    # itself (the dominant kernel of the step, timed for the roofline).
+    layer_graphs = [capture(torch, lambda r=r: run_layer(r)) for r in range(n_layer)]
+    check_replays(torch, layer_graphs[1], lambda: run_layer(1), [ys[m.name] for m in layer])
+
+    for i in range(warmup):
+        layer_graphs[i % n_layer].replay()
+        run_lm(i % n_lm)
+    events = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        layer_graphs[i % n_layer].replay()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run_lm(i % n_lm)
+        e1.record()
+        events.append((e0, e1))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1e3 / steps
+    lm_ms = statistics.fmean(a.elapsed_time(b) for a, b in events)
+    lm_alg = mv_bytes(lm)
+    return {
+        "value": step_bytes / (ms * 1e-3) / 1e9,
+        "ms_per_step": ms,
+        "step_bytes": step_bytes,
+        "copies": {"layer_set": n_layer, "lm_head": n_lm},
+        "lm_head": {"bytes": lm_alg, "ms": lm_ms, "GBps": lm_alg / (lm_ms * 1e-3) / 1e9},
+        "mats": mats,
+    }
+
+
+def time_graph(torch, fn, calls, replays, warmup=2):
+    """Mean ms per call of fn(i), i = 0..calls-1 captured in one graph."""
+    g = capture(torch, lambda: [fn(i) for i in range(calls)])
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (replays * calls)
+
+
+def extra_configs(torch, q3x, wl):
+    out = {}
+    # config 0: one Q8_0 4096x4096 matvec, copies rotated
+    m = wl.dense_matrices(0)[0]
+    n = copies_for(m.nbytes)
+    ws = [m.weight] + [m.weight.clone() for _ in range(n - 1)]
+    x = wl.activations(0, 1, 4096)[0].contiguous()
+    y = torch.empty(4096, dtype=torch.float32, device="cuda")
+    ms = time_graph(torch, lambda i: q3x.mv(q3x.Linear(ws[i % n], 4096, 4096, m.type), x, y), 4 * n, 20)
+    out["cfg0_q8_mv_4096"] = {"GBps": mv_bytes(m) / (ms * 1e-3) / 1e9, "us": ms * 1e3, "copies": n}
+    del ws
+    # config 2: Q8_0 prefill GEMM, N in {512, 4096}
+    mats = wl.dense_matrices(2)
+    for count in (512, 4096):
+        X = wl.activations(2, count, 4096)
+        H = wl.activations(2, count, 12288, salt=1)
+        Ys = {mm.name: torch.empty((count, mm.rows), dtype=torch.float32, device="cuda") for mm in mats}
+
+        def run(i):
+            for mm in mats:
+                q3x.batch_mv(mm.linear, H if mm.name == "down" else X, Ys[mm.name], count)
+        ms = time_graph(torch, run, 1, 4 if count == 4096 else 10)
+        flops = sum(2.0 * count * mm.rows * mm.cols for mm in mats)
+        out[f"cfg2_q8_gemm_N{count}"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
+                                         "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+        del X, H, Ys
+    del mats
+    # config 3: Q4_0 27B FFN at N = 1 (matvec) and N = 512 (GEMM)
+    mats = wl.dense_matrices(3)
+    total = sum(mm.nbytes for mm in mats)
+    n = copies_for(total)
+    sets = [mats] + [[wl.Matrix(mm.name, mm.type, mm.rows, mm.cols, mm.weight.clone()) for mm in mats]
+                     for _ in range(n - 1)]
+    x = wl.activations(3, 1, 17408)[0].contiguous()
+    ys = {mm.name: torch.empty(mm.rows, dtype=torch.float32, device="cuda") for mm in mats}
+
+    def run_mv(i):
+        for mm in sets[i % n]:
+            q3x.mv(mm.linear, x, ys[mm.name])
+    ms = time_graph(torch, run_mv, 2 * n, 10)
+    alg = sum(mv_bytes(mm) for mm in mats)
+    out["cfg3_q4_mv_27b_ffn"] = {"GBps": alg / (ms * 1e-3) / 1e9, "us": ms * 1e3, "copies": n}
+    del sets
+    X = wl.activations(3, 512, 5120)
+    H = wl.activations(3, 512, 17408, salt=1)
+    Ys = {mm.name: torch.empty((512, mm.rows), dtype=torch.float32, device="cuda") for mm in mats}
+
+    def run_gemm(i):
+        for mm in mats:
+            q3x.batch_mv(mm.linear, H if mm.name == "down" else X, Ys[mm.name], 512)
+    ms = time_graph(torch, run_gemm, 1, 10)
+    flops = sum(2.0 * 512 * mm.rows * mm.cols for mm in mats)
+    out["cfg3_q4_gemm_N512"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
+                                "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+    del mats, X, H, Ys
+    # config 4: Q4_0 routed MoE (router + experts), decode and 2048-token prefill
+    moe = wl.moe_weights(4)
+    cfg = wl.CONFIGS[4]
+    k = cfg["top_k"]
+    for T in (1, 2048):
+        logits = wl.router_logits(4, T, moe.experts)
+        X = wl.activations(4, T, moe.H)
+        ids = torch.empty((T, k), dtype=torch.int32, device="cuda")
+        wts = torch.empty((T, k), dtype=torch.float32, device="cuda")
+        Y = torch.empty((T, moe.H), dtype=torch.float32, device="cuda")
+        wsb = torch.empty(q3x.moe_workspace_bytes(T, moe.experts, k, moe.H, moe.I), dtype=torch.uint8,
+                          device="cuda")
+
+        def run_moe(i):
+            q3x.router_top_k(logits, T, moe.experts, k, ids, wts)
+            q3x.moe_routed(moe.gate_up_linear, moe.down_linear, X, T, ids, wts, k, Y, workspace=wsb)
+        ms = time_graph(torch, run_moe, 1, 50 if T == 1 else 5)
+        if T == 1:
+            per_expert = (moe.gate_up.numel() + moe.down.numel()) // moe.experts
+            alg = k * per_expert
+            out["cfg4_q4_moe_decode"] = {"GBps": alg / (ms * 1e-3) / 1e9, "us": ms * 1e3,
+                                         "note": "router + 8 experts per call; the same token's 14 MB of "
+                                                 "expert weights repeat, so the Infinity Cache serves them"}
+        else:
+            flops = 2.0 * T * k * (2 * moe.I * moe.H + moe.H * moe.I)
+            out["cfg4_q4_moe_prefill_T2048"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
+                                                "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+        del logits, X, ids, wts, Y, wsb
+    return out
+
+
+def cpu_baseline(mats, seconds):
+    """The reference CPU path (single thread) over the same matvec set."""
+    import numpy as np
+    import oracle
+    ref = oracle.ref()
+    hosts = [(m, np.ascontiguousarray(m.weight.cpu().numpy())) for m in mats]
+    x = np.random.default_rng(1).normal(0, 1, 12288).astype(np.float32)
+    kind = "reference" if ref is not None else "port"
+
+    def one_pass():
+        t0 = time.perf_counter()
+        for m, w in hosts:
+            y = np.empty(m.rows, np.float32)
+            if ref is not None:
+                ref.q3xr_try_mv(w.ctypes.data, m.type, m.rows, m.cols, x.ctypes.data, y.ctypes.data)
+            else:
+                oracle.lib().q3xo_mv_rows(w.ctypes.data, m.type, 0, m.rows, m.cols, x.ctypes.data, y.ctypes.data)
+        return time.perf_counter() - t0
+
+    times = [one_pass()]
+    while sum(times) < seconds and len(times) < 25:
+        times.append(one_pass())
+    t = statistics.median(times)
+    total = sum(mv_bytes(m) for m in mats)
+    return {"value": total / t / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"the full config-1 matvec set ({total} B) per pass, median of {len(times)} passes "
+                      f"({t * 1e3:.0f} ms each), single thread; host nproc={os.cpu_count()}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the matvec/GEMM shard by output rows with an all-gather, not measured here.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import qwen3x_amd as q3x
+    from qwen3x_amd import workloads as wl
+
+    torch.cuda.set_device(0)
+    head = headline(torch, q3x, wl, args.steps, args.warmup)
+    lm = head["lm_head"]
+    result = {
+        "metric": "Q8/Q4 matvec HBM GB/s (% of peak) at N=1; prefill GEMM FP32 TFLOP/s",
+        "value": round(head["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) weights quantised to Q8_0; N(0,1) activations)",
+        "config": {"workload": "config 1: Q8_0 decode matvec set of one 9B-class layer "
+                               "(q/k/v/o 4096->4096, gate/up 4096->12288, down 12288->4096) + lm_head "
+                               "4096->151936, batch 1", "step_bytes": head["step_bytes"],
+                   "weight_copies_rotated": head["copies"], "frac_of_hbm_peak": round(head["value"] / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(lm["GBps"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(lm["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "mv_stream_kernel<Q8_0, 64 lanes/row, 4-row batches, x in LDS> on lm_head 151936x4096",
+                     "algorithmic_bytes_per_launch": lm["bytes"], "avg_launch_ms": round(lm["ms"], 5)},
+    }
+    if not args.no_configs:
+        result["configs"] = extra_configs(torch, q3x, wl)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(head["mats"], args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

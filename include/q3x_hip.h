@@ -1,0 +1,128 @@
+/*
+ * q3x_hip.h -- C ABI of the MI355X (gfx950) quantized-matmul backend.
+ *
+ * Drop-in boundary for qwen3x's quantized weight matmul.  Weights keep the
+ * reference's llama.cpp-compatible 32-element block layouts:
+ *   Q8_0 block (34 B): uint16 fp16 scale d, int8 q[32];  w = d * q
+ *     (reference q8.h:10-15, arch/cpu.cpp:55-63)
+ *   Q4_0 block (18 B): uint16 fp16 scale d, uint8 nib[16]; element j < 16 is
+ *     the low nibble of nib[j], element j >= 16 the high nibble of nib[j-16];
+ *     w = d * (nibble - 8)  (reference q4.h:10-23, arch/cpu.cpp:81-90)
+ * A matrix W[rows, cols] is row-major, each row cols/32 contiguous blocks with
+ * no padding; an expert pool W[E, rows, cols] is E such matrices back to back
+ * (stride quantized_bytes(rows, cols); reference engine.cpp:214-224).
+ * Activations, accumulators and outputs are FP32.
+ *
+ * Conventions (all entry points):
+ *   - every pointer except `bytes` outputs is a DEVICE pointer;
+ *   - calls are asynchronous on `stream` (0 = the null stream) and enqueue
+ *     nothing when they return an error;
+ *   - no entry point allocates, frees, synchronises or keeps state; the MoE
+ *     workspace is caller-owned; calls are reentrant;
+ *   - results are deterministic: no atomics on accumulation paths, fixed
+ *     reduction order per shape;
+ *   - return Q3X_HIP_OK, or a negative code (arguments are validated before
+ *     any device work, so invalid calls touch no memory).
+ * The reference's CUDA backend aborts on error (engine.cu:48-56); this ABI
+ * returns codes instead so a caller may wrap them in its own assert.
+ */
+#ifndef Q3X_HIP_H
+#define Q3X_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Matrix type numbering of the reference's model_config.h:16-20. */
+enum {
+    Q3X_HIP_MATRIX_BF16 = 0,
+    Q3X_HIP_MATRIX_Q8_0 = 1,
+    Q3X_HIP_MATRIX_Q4_0 = 2,
+};
+
+enum {
+    Q3X_HIP_OK = 0,
+    Q3X_HIP_EINVAL = -1,   /* bad pointer, shape, type or size */
+    Q3X_HIP_ERUNTIME = -2, /* a HIP launch or query failed */
+    Q3X_HIP_ENOTSUP = -3,  /* valid request this backend does not handle
+                              (BF16 matrices: the caller keeps its own path,
+                              as with arch/cpu.cpp try_mv returning false) */
+};
+
+/* Human-readable name of a return code (static string). */
+const char* q3x_hip_strerror(int code);
+
+/* Exact byte size of a Q8_0/Q4_0 matrix.  Mirrors arch/cpu.cpp:161-179
+ * (quantized_bytes): rejects BF16/unknown types, rows <= 0, cols <= 0,
+ * cols % 32 != 0 and size_t overflow with Q3X_HIP_EINVAL, leaving *bytes
+ * untouched. */
+int q3x_hip_quantized_bytes(uint32_t type, int rows, int cols, size_t* bytes);
+
+/* y[rows] = W[rows, cols] x[cols]        (accumulate == 0)
+ * y[rows] += W[rows, cols] x[cols]       (accumulate != 0)
+ * Replaces the CUDA backend's mv() and mv_add() (arch/cuda/engine.cu:1531,
+ * 1547; kernels mv_q8_kernel / mv_add_q8_kernel / mv_q4_kernel /
+ * mv_add_q4_kernel :574-612) and the CPU try_mv (arch/cpu.cpp:192). */
+int q3x_hip_mv(const void* w, uint32_t type, int rows, int cols,
+               const float* x, float* y, int accumulate, hipStream_t stream);
+
+/* Y[count, rows] (+)= X[count, cols] W[rows, cols]^T, row-major X and Y.
+ * Replaces batch_mv() (arch/cuda/engine.cu:1568; batch_mv_q8_kernel :761),
+ * and adds the Q4_0 case the CUDA backend lacks (engine.cu:1580).  `count`
+ * is unbounded (the reference chunks prefill at 256 tokens, engine.cu:45). */
+int q3x_hip_gemm(const void* w, uint32_t type, int rows, int cols,
+                 const float* X, int count, float* Y, int accumulate,
+                 hipStream_t stream);
+
+/* out[nrows, cols] = dequantised rows [row0, row0 + nrows) of W, bit-exact
+ * with the reference's embed (arch/cpu.cpp:55-63, 81-90; CUDA embed_q8_kernel
+ * / embed_q4_kernel engine.cu:490-517, batch_embed_q8_kernel :701). */
+int q3x_hip_dequant(const void* w, uint32_t type, int cols, int row0, int nrows,
+                    float* out, hipStream_t stream);
+
+/* Per-token router: softmax over `experts` logits, top_k sequential argmax
+ * (strict '>', lowest index wins ties), weights renormalised over the
+ * selection.  logits [tokens, experts]; ids, weights [tokens, top_k].
+ * Replaces router_top_k (engine.cpp:377-405; router_top_k_kernel
+ * engine.cu:1153-1184, which runs one thread for one token).
+ * Requires 1 <= top_k <= min(experts, 8) and experts <= 1024. */
+int q3x_hip_router_topk(const float* logits, int tokens, int experts, int top_k,
+                        int* ids, float* weights, hipStream_t stream);
+
+/* Bytes of caller-owned workspace q3x_hip_moe_routed needs. */
+size_t q3x_hip_moe_workspace_bytes(int tokens, int experts, int top_k, int H, int I);
+
+/* Routed experts: for every token t,
+ *   Y[t] (+)= sum_{slot < top_k} weights[t, slot] * Down_e (silu(G_e X[t]) * U_e X[t])
+ * with e = ids[t, slot], G_e / U_e rows [0, I) / [I, 2I) of gate_up[e], in
+ * slot order from zero (engine.cpp:406-420; CUDA expert_gate_up_q4_kernel,
+ * expert_swiglu_kernel, expert_down_weighted_q4_kernel engine.cu:1186-1250).
+ * gate_up: [experts, 2I, H], down: [experts, H, I], type Q4_0 or Q8_0.
+ * tokens == 1 runs fused matvecs (decode); tokens > 1 groups the (token,
+ * slot) pairs by expert and runs one grouped FP32-MFMA GEMM per expert.
+ * ids outside [0, experts) contribute nothing (as engine.cu:1198, 1235). */
+int q3x_hip_moe_routed(const void* gate_up, const void* down, uint32_t type,
+                       int experts, int H, int I, const float* X, int tokens,
+                       const int* ids, const float* weights, int top_k, float* Y,
+                       int accumulate, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+
+/* dst = Q8_0/Q4_0 blocks of src[rows, cols] (FP32), the quantizers of the
+ * reference's packer (scripts/pack_weights.py:299-343) applied to FP32 input:
+ * Q8_0 d = max|w|/127, q = clip(copysign(floor(|w/d| + 0.5)), +-127);
+ * Q4_0 d = w[argmax|w|] / -8, nibble = min(15, trunc(w/d + 8.5)); d stored as
+ * fp16 round-to-nearest-even; 1/d taken in FP32.  Non-finite input is the
+ * caller's responsibility (the packer rejects it; here it yields the same
+ * arithmetic on IEEE specials). */
+int q3x_hip_quantize(uint32_t type, const float* src, int rows, int cols, void* dst,
+                     hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,175 @@
+"""CPU parity oracle for qwen3x's quantized matmul path -- TEST INFRASTRUCTURE ONLY.
+
+Python access to ``liboracle.so`` (this repository's C restatement of the
+reference CPU path, q3x_oracle.c) and, when it was built, to
+``_ref/libq3x_ref.so`` (the reference's own CPU sources compiled where they
+lie).  Only tests/, ``__graft_entry__.smoke()`` and bench.py's cpu_baseline
+leg may use this package; the product library never does.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_DIR, "liboracle.so")
+REF_PATH = os.path.join(_DIR, "_ref", "libq3x_ref.so")
+
+Q8_0 = 1
+Q4_0 = 2
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18}
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_U = ctypes.c_uint32
+_S = ctypes.c_size_t
+_F = ctypes.c_float
+_SIGS = {
+    "q3xo_f16": (_F, [ctypes.c_uint16]),
+    "q3xo_quantized_bytes": (_I, [_U, _I, _I, ctypes.POINTER(_S)]),
+    "q3xo_embed": (_I, [_P, _U, _I, _I, _P]),
+    "q3xo_mv_rows": (_I, [_P, _U, _I, _I, _I, _P, _P]),
+    "q3xo_mv": (_I, [_P, _U, _I, _I, _P, _P, _I]),
+    "q3xo_gemm": (_I, [_P, _U, _I, _I, _P, _I, _P, _I]),
+    "q3xo_sigmoid": (_F, [_F]),
+    "q3xo_silu": (_F, [_F]),
+    "q3xo_router_top_k": (_I, [_P, _I, _I, _P, _P, _P]),
+    "q3xo_moe_routed": (_I, [_P, _P, _U, _I, _I, _I, _P, _I, _P, _P, _I, _P, _I]),
+    "q3xo_quantize": (_I, [_U, _P, _S, _P]),
+}
+_REF_SIGS = {
+    "q3xr_quantized_bytes": (_I, [_U, _I, _I, ctypes.POINTER(_S)]),
+    "q3xr_try_embed": (_I, [_P, _U, _I, _I, _P]),
+    "q3xr_try_mv": (_I, [_P, _U, _I, _I, _P, _P]),
+    "q3xr_router_top_k": (None, [_P, _I, _I, _P, _P]),
+    "q3xr_sigmoid": (_F, [_F]),
+    "q3xr_silu": (_F, [_F]),
+    "q3xr_moe_q4": (None, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P]),
+}
+
+_lib = None
+_ref = None
+
+
+def _bind(path, sigs):
+    handle = ctypes.CDLL(path)
+    for name, (restype, argtypes) in sigs.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return handle
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C {_DIR}`")
+        _lib = _bind(LIB_PATH, _SIGS)
+    return _lib
+
+
+def ref():
+    """The reference build, or None when it was not built (no reference tree)."""
+    global _ref
+    if _ref is None and os.path.exists(REF_PATH):
+        _ref = _bind(REF_PATH, _REF_SIGS)
+    return _ref
+
+
+def default_threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def f16(bits: int) -> float:
+    return float(lib().q3xo_f16(bits))
+
+
+def quantized_bytes(type_: int, rows: int, cols: int):
+    out = ctypes.c_size_t(123)
+    ok = lib().q3xo_quantized_bytes(type_, rows, cols, ctypes.byref(out))
+    return out.value if ok else None
+
+
+def embed(w: np.ndarray, type_: int, cols: int, row: int) -> np.ndarray:
+    out = np.empty(cols, np.float32)
+    assert lib().q3xo_embed(_p(w), type_, cols, row, _p(out))
+    return out
+
+
+def dequant(w: np.ndarray, type_: int, rows: int, cols: int) -> np.ndarray:
+    out = np.empty((rows, cols), np.float32)
+    for r in range(rows):
+        assert lib().q3xo_embed(_p(w), type_, cols, r, _p(out[r]))
+    return out
+
+
+def mv(w: np.ndarray, type_: int, rows: int, cols: int, x: np.ndarray, threads: int | None = None) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows, np.float32)
+    assert lib().q3xo_mv(_p(w), type_, rows, cols, _p(x), _p(y), threads or default_threads())
+    return y
+
+
+def mv_serial(w: np.ndarray, type_: int, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows, np.float32)
+    assert lib().q3xo_mv_rows(_p(w), type_, 0, rows, cols, _p(x), _p(y))
+    return y
+
+
+def gemm(w: np.ndarray, type_: int, rows: int, cols: int, X: np.ndarray, threads: int | None = None) -> np.ndarray:
+    X = np.ascontiguousarray(X, np.float32)
+    count = X.shape[0]
+    Y = np.empty((count, rows), np.float32)
+    assert lib().q3xo_gemm(_p(w), type_, rows, cols, _p(X), count, _p(Y), threads or default_threads())
+    return Y
+
+
+def sigmoid(x: float) -> float:
+    return float(lib().q3xo_sigmoid(x))
+
+
+def silu(x: float) -> float:
+    return float(lib().q3xo_silu(x))
+
+
+def router_top_k(logits: np.ndarray, top_k: int):
+    """Per token (rows of ``logits``): ids [T, k], weights [T, k], probabilities [T, E]."""
+    logits = np.ascontiguousarray(np.atleast_2d(logits), np.float32)
+    T, E = logits.shape
+    ids = np.empty((T, top_k), np.int32)
+    weights = np.empty((T, top_k), np.float32)
+    probs = np.empty((T, E), np.float32)
+    for t in range(T):
+        assert lib().q3xo_router_top_k(_p(logits[t]), E, top_k, _p(ids[t]), _p(weights[t]), _p(probs[t]))
+    return ids, weights, probs
+
+
+def moe_routed(gate_up: np.ndarray, down: np.ndarray, type_: int, experts: int, H: int, I: int,
+               X: np.ndarray, ids: np.ndarray, weights: np.ndarray, threads: int | None = None) -> np.ndarray:
+    X = np.ascontiguousarray(np.atleast_2d(X), np.float32)
+    ids = np.ascontiguousarray(np.atleast_2d(ids), np.int32)
+    weights = np.ascontiguousarray(np.atleast_2d(weights), np.float32)
+    T = X.shape[0]
+    top_k = ids.shape[1]
+    Y = np.empty((T, H), np.float32)
+    assert lib().q3xo_moe_routed(_p(gate_up), _p(down), type_, experts, H, I, _p(X), T, _p(ids), _p(weights),
+                                 top_k, _p(Y), threads or default_threads())
+    return Y
+
+
+def quantize(type_: int, values: np.ndarray) -> np.ndarray:
+    values = np.ascontiguousarray(values, np.float32).reshape(-1)
+    out = np.empty(values.size // 32 * BLOCK_BYTES[type_], np.uint8)
+    ok = lib().q3xo_quantize(type_, _p(values), values.size, _p(out))
+    if not ok:
+        raise ValueError("quantize: partial block or non-finite input")
+    return out

@@ -1,0 +1,81 @@
+// ref_shim.cpp -- C entry points into the reference CPU engine, compiled from
+// the reference sources where they lie (TEST INFRASTRUCTURE ONLY).
+//
+// Like the reference's own tests (tests/q8_cpu_test.cpp:11,
+// tests/q4_cpu_test.cpp), this file includes engine.cpp to reach its
+// internal functions, and exports them with plain C signatures so the parity
+// tests can compare this repository's oracle against the reference bit for bit.
+// Built by `make -C oracle ref` into oracle/_ref/ (git-ignored).
+#include "engine.cpp"
+#include "q4.h"
+
+#include <vector>
+
+extern "C" {
+
+int q3xr_quantized_bytes(uint32_t type, int rows, int cols, size_t* bytes) {
+    return q3x_cpu::quantized_bytes(static_cast<q3x_model::MatrixType>(type), rows, cols,
+                                    bytes) ? 1 : 0;
+}
+
+// arch/cpu.cpp:181-190
+int q3xr_try_embed(const void* weights, uint32_t type, int cols, int row, float* out) {
+    if (type > q3x_model::MATRIX_Q4_0) return 0;
+    return q3x_cpu::try_embed(weights, static_cast<q3x_model::MatrixType>(type), cols, row,
+                              out) ? 1 : 0;
+}
+
+// arch/cpu.cpp:192-226 (serial on x86)
+int q3xr_try_mv(const void* weights, uint32_t type, int rows, int cols, const float* x,
+                float* y) {
+    if (type > q3x_model::MATRIX_Q4_0) return 0;
+    return q3x_cpu::try_mv(weights, static_cast<q3x_model::MatrixType>(type), rows, cols, x,
+                           y) ? 1 : 0;
+}
+
+// engine.cpp:377-405 (probabilities[ids[slot]] holds the renormalised weight)
+void q3xr_router_top_k(const float* logits, int experts, int top_k, int* ids,
+                       float* probabilities) {
+    q3x_backend::router_top_k(logits, experts, top_k, ids, probabilities);
+}
+
+float q3xr_sigmoid(float x) { return q3x_backend::sigmoid(x); }
+float q3xr_silu(float x) { return q3x_backend::silu(x); }
+
+// engine.cpp:406-430 for one token: BF16 router [E, H], Q4_0 experts
+// gate_up [E, 2I, H] and down [E, H, I].  The shared expert is given all-zero
+// Q4_0 blocks (scale 0) so it adds exactly zero; `logits` receives the router
+// output the reference computed, `ids` the selected experts.
+void q3xr_moe_q4(const uint16_t* router, const void* gate_up, const void* down,
+                 int experts, int H, int I, int top_k, const float* input,
+                 float* logits, int* ids, float* out) {
+    // Work (engine.cpp:84-110) sizes delta_output, which moe() reuses for the
+    // expert down output of H floats, as VH * VD: take VD = H.
+    const q3x_model::ModelConfig config {
+        1, "synthetic-MoE", 64, H, I, 1,
+        1, 1, 1, 32, 16, 1, 1, 32, H, 4,
+        experts, top_k, 32, q3x_model::MATRIX_Q4_0, false,
+    };
+    const int shared_I = 32;
+    std::vector<q3x_q4::Block> shared_gate(static_cast<size_t>(shared_I) * H / 32);
+    std::vector<q3x_q4::Block> shared_up(shared_gate.size());
+    std::vector<q3x_q4::Block> shared_down(static_cast<size_t>(H) * shared_I / 32);
+    std::vector<uint16_t> shared_scale(H, 0);
+    for (auto* pool : {&shared_gate, &shared_up, &shared_down})
+        for (auto& block : *pool) { block.scale = 0; std::memset(block.values, 0x88, 16); }
+    q3x_backend::MoeWeights weights {
+        {router, experts, H, q3x_model::MATRIX_BF16},
+        {gate_up, experts, 2 * I, H, q3x_model::MATRIX_Q4_0},
+        {down, experts, H, I, q3x_model::MATRIX_Q4_0},
+        {shared_gate.data(), shared_I, H, q3x_model::MATRIX_Q4_0},
+        {shared_up.data(), shared_I, H, q3x_model::MATRIX_Q4_0},
+        {shared_down.data(), H, shared_I, q3x_model::MATRIX_Q4_0},
+        {shared_scale.data(), 1, H, q3x_model::MATRIX_BF16},
+    };
+    q3x_backend::Work work(config);
+    q3x_backend::mv(weights.router, input, logits);
+    q3x_backend::moe(weights, input, work, out, config);
+    for (int slot = 0; slot < top_k; ++slot) ids[slot] = work.expert_ids[slot];
+}
+
+}  // extern "C"

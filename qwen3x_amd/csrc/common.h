@@ -1,0 +1,112 @@
+// common.h -- block formats, argument checks and device helpers shared by the
+// gfx950 kernels of the quantized-matmul backend.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "q3x_hip.h"
+
+namespace q3x {
+
+constexpr int kBlock = 32;        // weights per block (q8.h:8, q4.h:8)
+constexpr int kQ8Bytes = 34;      // uint16 scale + int8[32]   (q8.h:10-15)
+constexpr int kQ4Bytes = 18;      // uint16 scale + uint8[16]  (q4.h:12-15)
+constexpr int kWave = 64;         // CDNA wavefront
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__host__ __device__ constexpr int block_bytes(uint32_t type) {
+    return type == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
+}
+
+// arch/cpu.cpp:161-179 with the same rejection rules.
+inline bool quantized_size(uint32_t type, int rows, int cols, size_t* bytes) {
+    size_t bb;
+    if (type == Q3X_HIP_MATRIX_Q8_0) bb = kQ8Bytes;
+    else if (type == Q3X_HIP_MATRIX_Q4_0) bb = kQ4Bytes;
+    else return false;
+    if (rows <= 0 || cols <= 0 || cols % kBlock != 0) return false;
+    const size_t blocks = static_cast<size_t>(cols) / kBlock;
+    const size_t maximum = SIZE_MAX;
+    if (blocks > maximum / bb) return false;
+    const size_t row_bytes = blocks * bb;
+    if (static_cast<size_t>(rows) > maximum / row_bytes) return false;
+    *bytes = static_cast<size_t>(rows) * row_bytes;
+    return true;
+}
+
+inline bool is_quant_type(uint32_t type) {
+    return type == Q3X_HIP_MATRIX_Q8_0 || type == Q3X_HIP_MATRIX_Q4_0;
+}
+
+inline bool aligned(const void* p, size_t a) {
+    return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+// Launch-error check after an asynchronous kernel launch.
+inline int launch_status() {
+    return hipGetLastError() == hipSuccess ? Q3X_HIP_OK : Q3X_HIP_ERUNTIME;
+}
+
+// Exact IEEE binary16 -> binary32 by bit manipulation, identical bit for bit
+// to the reference's f16() (arch/cpu.cpp:31-52), NaN payloads included.  Used
+// where dequantised values are returned to the caller.
+__device__ __forceinline__ float f16_exact(uint32_t value) {
+    const uint32_t sign = (value & 0x8000u) << 16;
+    const uint32_t exponent = (value >> 10) & 0x1fu;
+    const uint32_t mantissa = value & 0x03ffu;
+    uint32_t bits;
+    if (exponent == 0) {
+        if (mantissa == 0) {
+            bits = sign;
+        } else {
+            // Normalise the subnormal: shift the leading one to bit 10.
+            const int lead = __clz(mantissa) - 21;  // 1..10 shifts
+            bits = sign | ((113u - lead) << 23) | (((mantissa << lead) & 0x03ffu) << 13);
+        }
+    } else if (exponent == 31) {
+        bits = sign | 0x7f800000u | (mantissa << 13);
+    } else {
+        bits = sign | ((exponent + 112u) << 23) | (mantissa << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+// Hardware half -> float (v_cvt_f32_f16): exact for every finite value and
+// infinity, subnormals included (f16 denormals are preserved on gfx950).
+// Used inside the dot-product kernels.
+__device__ __forceinline__ float f16_fast(uint32_t value) {
+    _Float16 h;
+    const uint16_t bits = static_cast<uint16_t>(value);
+    __builtin_memcpy(&h, &bits, sizeof(h));
+    return static_cast<float>(h);
+}
+
+// Signed byte k of a dword as float (one v_cvt_f32_i32_sdwa with sext).
+template <int K>
+__device__ __forceinline__ float sbyte(uint32_t v) {
+    return static_cast<float>(static_cast<int8_t>(v >> (8 * K)));
+}
+
+// Sum over groups of `width` consecutive lanes (width a power of two <= 64).
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int offset = WIDTH / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, WIDTH);
+    return v;
+}
+
+// Orders LDS traffic of one wavefront: every lane's earlier LDS writes are
+// visible to every lane's later LDS reads (LDS executes a wave's operations
+// in issue order; this keeps the compiler from moving them across).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+}  // namespace q3x

@@ -1,0 +1,220 @@
+// gemm.h -- FP32-MFMA GEMM with on-the-fly Q8_0 / Q4_0 weight dequantisation
+// (prefill), shared by the dense prefill entry point and the MoE grouped GEMM.
+//
+// C[m, n] = sum_k A[m, k] * B[k, n] with A = activations (tokens x cols, FP32,
+// row-major) and B = W^T (W = weight rows x cols, quantised).  MFMA's M
+// dimension carries tokens and N carries weight rows, so a 32x32 accumulator
+// tile stores 32 consecutive output features per token: coalesced writes of
+// the row-major [tokens, rows] output.
+//
+// Per K stage (one 32-column block): the workgroup loads its A tile
+// (BM x 32 FP32) and its weight blocks (BN rows x 1 block), dequantises the
+// weights to FP32 (d * q is exact in FP32: an 11-bit significand times an
+// 8-bit integer), writes both to a double-buffered LDS tile, and each wave
+// runs 16 MFMA k-steps per 32x32 tile.  The 32 k values of a block are fed
+// in the order k = 16*(lane/32) + s (s = 0..15), the same permutation for A
+// and B, so a lane reads 16 consecutive floats of each operand row with four
+// ds_read_b128.
+#pragma once
+
+#include "common.h"
+
+namespace q3x {
+
+constexpr int kGemmPad = 4;            // floats of padding per LDS tile row
+constexpr int kGemmLd = 32 + kGemmPad; // LDS row pitch (floats)
+
+struct GemmTile {
+    int m0;      // first A row of the tile (policy-defined numbering)
+    int mcount;  // valid A rows in the tile (<= BM)
+    int group;   // policy-defined (expert of a grouped tile)
+};
+
+// Raw halfwords of part `part` of PARTS of one block: raw[0] = fp16 scale,
+// raw[1..RAW_HALVES] = the part's value bytes two at a time.  Q8_0: elements
+// [part*N, part*N + N), N = 32/PARTS.  Q4_0: nibble bytes
+// [NB*part, NB*part + NB), NB = 16/PARTS, i.e. elements NB*part + j (low
+// nibbles) and 16 + NB*part + j (high nibbles).  `blk` is 2-byte aligned.
+template <uint32_t QT, int PARTS>
+struct BlockPart {
+    static constexpr int N = 32 / PARTS;                    // elements
+    static constexpr int HALVES = QT == Q3X_HIP_MATRIX_Q8_0 ? N / 2 : N / 4;
+    __device__ static __forceinline__ void load(const uint8_t* blk, int part, uint32_t* raw) {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
+        raw[0] = h[0];
+#pragma unroll
+        for (int i = 0; i < HALVES; ++i) raw[1 + i] = h[1 + HALVES * part + i];
+    }
+    // out[e] for e < N, in the column order of column().
+    __device__ static __forceinline__ void dequant(const uint32_t* raw, float* out) {
+        const float d = f16_fast(raw[0]);
+#pragma unroll
+        for (int i = 0; i < HALVES; ++i) {
+            const uint32_t two = raw[1 + i];
+            if (QT == Q3X_HIP_MATRIX_Q8_0) {
+                out[2 * i + 0] = d * static_cast<float>(static_cast<int8_t>(two & 0xffu));
+                out[2 * i + 1] = d * static_cast<float>(static_cast<int8_t>(two >> 8));
+            } else {
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const uint32_t byte = (two >> (8 * b)) & 0xffu;
+                    out[2 * i + b] = d * static_cast<float>(static_cast<int>(byte & 15u) - 8);
+                    out[N / 2 + 2 * i + b] = d * static_cast<float>(static_cast<int>(byte >> 4) - 8);
+                }
+            }
+        }
+    }
+    // Column within the block of output element e.
+    __device__ static __forceinline__ int column(int part, int e) {
+        if (QT == Q3X_HIP_MATRIX_Q8_0) return part * N + e;
+        constexpr int NB = N / 2;
+        return e < NB ? part * NB + e : 16 + part * NB + (e - NB);
+    }
+};
+
+// WM x WN waves, each TM x TN tiles of 32x32.  Policy supplies the tile
+// geometry, A rows, weight rows and the output store (see dense / grouped
+// policies).  Grid: x = weight-row tiles (BN), y = A-row tiles (BM).
+template <uint32_t QT, int WM, int WN, int TM, int TN, class Policy>
+__global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, int rows, int cols) {
+    constexpr int NT = WM * WN * kWave;   // threads
+    constexpr int BM = WM * TM * 32;
+    constexpr int BN = WN * TN * 32;
+    constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
+    // A tile load: BM rows x 8 float4 per stage.
+    constexpr int A_VEC = BM * 8;
+    constexpr int A_PER_T = (A_VEC + NT - 1) / NT;
+    // B tile load: BN rows, PARTS threads per row.
+    constexpr int PARTS = NT / BN >= 2 ? 2 : 1;
+    constexpr int B_ROWS_PER_PASS = NT / PARTS;
+    constexpr int B_PASSES = (BN + B_ROWS_PER_PASS - 1) / B_ROWS_PER_PASS;
+    constexpr int PER_PART = 32 / PARTS;
+    static_assert(PARTS * B_ROWS_PER_PASS == NT, "thread split");
+
+    __shared__ __attribute__((aligned(16))) float As[2][BM * kGemmLd];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BN * kGemmLd];
+
+    GemmTile tile;
+    if (!pol.tile(blockIdx.y, BM, tile)) return;
+    const int n0 = blockIdx.x * BN;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int wm = wave / WN, wn = wave % WN;
+    const int li = lane & 31, kh = lane >> 5;
+
+    // Per-thread source pointers, fixed over K.
+    const float* a_src[A_PER_T];
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+        const int idx = tid + i * NT;
+        const int m = idx >> 3;
+        a_src[i] = (idx < A_VEC && m < tile.mcount) ? pol.a_row(tile, m) + 4 * (idx & 7) : nullptr;
+    }
+    const uint8_t* b_src[B_PASSES];
+    const int b_part = tid % PARTS;
+#pragma unroll
+    for (int p = 0; p < B_PASSES; ++p) {
+        const int n = tid / PARTS + p * B_ROWS_PER_PASS;
+        b_src[p] = (n < BN && n0 + n < rows) ? pol.b_row(tile, n0 + n) : nullptr;
+    }
+
+    using Part = BlockPart<QT, PARTS>;
+    f32x4 a_reg[A_PER_T];
+    uint32_t b_raw[B_PASSES][1 + Part::HALVES];
+    auto load_stage = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < A_PER_T; ++i)
+            a_reg[i] = a_src[i] ? *reinterpret_cast<const f32x4*>(a_src[i] + 32 * kb)
+                                : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int p = 0; p < B_PASSES; ++p) {
+            if (b_src[p]) {
+                Part::load(b_src[p] + static_cast<size_t>(kb) * BB, b_part, b_raw[p]);
+            } else {
+#pragma unroll
+                for (int e = 0; e <= Part::HALVES; ++e) b_raw[p][e] = 0u;
+            }
+        }
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < A_PER_T; ++i) {
+            const int idx = tid + i * NT;
+            if (idx < A_VEC)
+                *reinterpret_cast<f32x4*>(&As[buf][(idx >> 3) * kGemmLd + 4 * (idx & 7)]) = a_reg[i];
+        }
+#pragma unroll
+        for (int p = 0; p < B_PASSES; ++p) {
+            const int n = tid / PARTS + p * B_ROWS_PER_PASS;
+            if (n < BN) {
+                float vals[PER_PART];
+                Part::dequant(b_raw[p], vals);
+#pragma unroll
+                for (int e = 0; e < PER_PART; e += 4) {
+                    const int c = Part::column(b_part, e);
+                    *reinterpret_cast<f32x4*>(&Bs[buf][n * kGemmLd + c]) =
+                        f32x4{vals[e], vals[e + 1], vals[e + 2], vals[e + 3]};
+                }
+            }
+        }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int nblk = cols / kBlock;
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    for (int kb = 0; kb < nblk; ++kb) {
+        const int buf = kb & 1;
+        if (kb + 1 < nblk) load_stage(kb + 1);
+        f32x4 af[TM][4], bf[TN][4];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const float* src = &As[buf][((wm * TM + i) * 32 + li) * kGemmLd + 16 * kh];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) af[i][q] = *reinterpret_cast<const f32x4*>(src + 4 * q);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const float* src = &Bs[buf][((wn * TN + j) * 32 + li) * kGemmLd + 16 * kh];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) bf[j][q] = *reinterpret_cast<const f32x4*>(src + 4 * q);
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s >> 2][s & 3],
+                                                                     bf[j][s >> 2][s & 3],
+                                                                     acc[i][j], 0, 0, 0);
+        if (kb + 1 < nblk) store_stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Accumulator layout of v_mfma_f32_32x32x2f32: register r of lane l holds
+    // C[8*(r/4) + 4*(l/32) + r%4][l%32].
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = n0 + (wn * TN + j) * 32 + li;
+            if (n >= rows) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = (wm * TM + i) * 32 + 8 * (r >> 2) + 4 * kh + (r & 3);
+                if (m < tile.mcount) pol.store(tile, m, n, acc[i][j][r]);
+            }
+        }
+}
+
+}  // namespace q3x

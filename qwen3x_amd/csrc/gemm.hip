@@ -1,0 +1,98 @@
+// gemm.hip -- q3x_hip_gemm: dense prefill GEMM Y[count, rows] (+)= X W^T
+// with Q8_0 / Q4_0 weights on FP32 MFMA (kernel in gemm.h).
+//
+// Replaces the reference's batch_mv (arch/cuda/engine.cu:1568-1597), whose Q8
+// path is an FP32 SIMT kernel (batch_mv_q8_kernel :761, 64 rows x 128 tokens
+// per CTA) and which has no Q4_0 GEMM (it asserts, :1580).
+#include "gemm.h"
+#include "matvec.h"
+
+namespace q3x {
+
+// Token rows X[count, cols] against one weight matrix.
+struct DenseGemm {
+    const float* X;
+    int cols;
+    int count;
+    const uint8_t* w;
+    size_t row_bytes;
+    float* Y;
+    int rows;
+    bool accumulate;
+    __device__ bool tile(int ty, int bm, GemmTile& t) const {
+        t.m0 = ty * bm;
+        t.mcount = min(bm, count - t.m0);
+        t.group = 0;
+        return t.mcount > 0;
+    }
+    __device__ const float* a_row(const GemmTile& t, int m) const {
+        return X + static_cast<size_t>(t.m0 + m) * cols;
+    }
+    __device__ const uint8_t* b_row(const GemmTile&, int n) const {
+        return w + static_cast<size_t>(n) * row_bytes;
+    }
+    __device__ void store(const GemmTile& t, int m, int n, float v) const {
+        float* p = Y + static_cast<size_t>(t.m0 + m) * rows + n;
+        if (accumulate) *p += v;
+        else *p = v;
+    }
+};
+
+// Large tiles: 2x2 waves of 2x2 32x32 tiles = 128 tokens x 128 weight rows.
+// Small tiles (2x2 waves of one 32x32 tile = 64 x 64) when large tiles would
+// give fewer than two workgroups per CU (256 CUs).
+constexpr int kMaxGridY = 65535;
+constexpr int kFillWorkgroups = 512;
+
+template <uint32_t QT, int TM, int TN>
+int launch_dense_gemm_tiles(const DenseGemm& base, hipStream_t stream) {
+    constexpr int BM = 2 * TM * 32, BN = 2 * TN * 32;
+    // Chunk the token dimension so grid.y stays within the launch limit.
+    const int chunk = kMaxGridY * BM;
+    for (int start = 0; start < base.count; start += chunk) {
+        DenseGemm part = base;
+        part.X = base.X + static_cast<size_t>(start) * base.cols;
+        part.Y = base.Y + static_cast<size_t>(start) * base.rows;
+        part.count = min(chunk, base.count - start);
+        const dim3 grid((base.rows + BN - 1) / BN, (part.count + BM - 1) / BM);
+        hipLaunchKernelGGL((gemm_mfma_kernel<QT, 2, 2, TM, TN, DenseGemm>), grid, dim3(4 * kWave), 0, stream,
+                           part, base.rows, base.cols);
+        const int status = launch_status();
+        if (status != Q3X_HIP_OK) return status;
+    }
+    return Q3X_HIP_OK;
+}
+
+template <uint32_t QT>
+int launch_dense_gemm(const DenseGemm& g, hipStream_t stream) {
+    const long long large = static_cast<long long>((g.rows + 127) / 128) * ((g.count + 127) / 128);
+    if (large >= kFillWorkgroups) return launch_dense_gemm_tiles<QT, 2, 2>(g, stream);
+    return launch_dense_gemm_tiles<QT, 1, 1>(g, stream);
+}
+
+}  // namespace q3x
+
+using namespace q3x;
+
+extern "C" int q3x_hip_gemm(const void* w, uint32_t type, int rows, int cols, const float* X,
+                            int count, float* Y, int accumulate, hipStream_t stream) {
+    if (type == Q3X_HIP_MATRIX_BF16) return Q3X_HIP_ENOTSUP;
+    size_t bytes;
+    if (!w || !X || !Y || count <= 0 || !quantized_size(type, rows, cols, &bytes))
+        return Q3X_HIP_EINVAL;
+    const int bpr = cols / kBlock;
+    const size_t row_bytes = static_cast<size_t>(bpr) * block_bytes(type);
+    if (!aligned(w, 2) || !aligned(X, 16) || !aligned(Y, 4)) {
+        // Unaligned operands: one matvec per token (the reference CPU prefill
+        // is exactly this, engine.cpp:580-583).
+        for (int t = 0; t < count; ++t) {
+            const int status = q3x_hip_mv(w, type, rows, cols, X + static_cast<size_t>(t) * cols,
+                                          Y + static_cast<size_t>(t) * rows, accumulate, stream);
+            if (status != Q3X_HIP_OK) return status;
+        }
+        return Q3X_HIP_OK;
+    }
+    DenseGemm g{X, cols, count, static_cast<const uint8_t*>(w), row_bytes, Y, rows, accumulate != 0};
+    return type == Q3X_HIP_MATRIX_Q8_0 ? launch_dense_gemm<Q3X_HIP_MATRIX_Q8_0>(g, stream)
+                                       : launch_dense_gemm<Q3X_HIP_MATRIX_Q4_0>(g, stream);
+}

@@ -1,0 +1,183 @@
+// misc.hip -- sizes, error strings, dequantisation and the device quantizer.
+#include <math.h>
+
+#include "common.h"
+
+namespace q3x {
+
+// out[r, c] = f16(d) * q (Q8_0) or f16(d) * (nibble - 8) (Q4_0): the
+// reference's embed (arch/cpu.cpp:55-63, 81-90), bit for bit.  The scale is
+// decoded with the reference's own bit manipulation, and the product of an
+// 11-bit significand with an integer of at most 8 bits is exact in FP32.
+template <uint32_t QT>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ w, int cols, int row0,
+                                                      int nrows, float* __restrict__ out) {
+    constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
+    const size_t total = static_cast<size_t>(nrows) * cols;
+    const int bpr = cols / kBlock;
+    for (size_t idx = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; idx < total;
+         idx += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const size_t r = idx / cols;
+        const int c = static_cast<int>(idx % cols);
+        const uint8_t* blk = w + ((row0 + r) * bpr + c / kBlock) * BB;
+        const float scale = f16_exact(blk[0] | (blk[1] << 8));
+        const int within = c % kBlock;
+        int q;
+        if (QT == Q3X_HIP_MATRIX_Q8_0) {
+            q = static_cast<int8_t>(blk[2 + within]);
+        } else {
+            const uint32_t packed = blk[2 + within % 16];
+            q = static_cast<int>(within < 16 ? (packed & 15u) : (packed >> 4)) - 8;
+        }
+        out[idx] = scale * static_cast<float>(q);
+    }
+}
+
+// IEEE binary32 -> binary16, round to nearest even (numpy's astype("<f2")),
+// in integer arithmetic so the sign of zero and every rounding are explicit
+// (the compiler may otherwise fold the conversion into a mixed-precision FMA
+// with a +0 addend, which turns -0 into +0).
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float value) {
+    const uint32_t bits = __float_as_uint(value);
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const uint32_t exponent = (bits >> 23) & 0xffu;
+    uint32_t mantissa = bits & 0x7fffffu;
+    if (exponent == 0xffu)  // inf / nan (quiet the nan, keep its top payload bits)
+        return static_cast<uint16_t>(sign | 0x7c00u | (mantissa ? 0x200u | (mantissa >> 13) : 0u));
+    const int e = static_cast<int>(exponent) - 127 + 15;
+    if (e >= 31) return static_cast<uint16_t>(sign | 0x7c00u);
+    if (e <= 0) {  // half subnormal or zero
+        if (e < -10) return static_cast<uint16_t>(sign);
+        mantissa |= 0x800000u;
+        const int shift = 14 - e;
+        uint32_t half = mantissa >> shift;
+        const uint32_t rest = mantissa & ((1u << shift) - 1u);
+        const uint32_t halfway = 1u << (shift - 1);
+        if (rest > halfway || (rest == halfway && (half & 1u))) ++half;
+        return static_cast<uint16_t>(sign | half);
+    }
+    uint32_t half = (static_cast<uint32_t>(e) << 10) | (mantissa >> 13);
+    const uint32_t rest = mantissa & 0x1fffu;
+    if (rest > 0x1000u || (rest == 0x1000u && (half & 1u))) ++half;  // may carry into inf
+    return static_cast<uint16_t>(sign | half);
+}
+
+// One thread per 32-value block: scripts/pack_weights.py:299-343 on FP32
+// values.  Q8_0: d = max|v| / 127 (FP32), inverse = 1/d (0 when d == 0),
+// q = clip(copysign(floor(|v * inverse| + 0.5), v * inverse), -127, 127).
+// Q4_0: m = the first value of largest magnitude, d = m / -8, inverse as
+// above, nibble = min(15, trunc(v * inverse + 8.5)); low nibbles hold
+// elements 0..15.  Both store d as fp16.
+template <uint32_t QT>
+__global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ src, size_t blocks,
+                                                       uint8_t* __restrict__ dst) {
+    // The packer rounds every operation separately (numpy): no FMA contraction.
+#pragma clang fp contract(off)
+    constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
+    for (size_t b = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; b < blocks;
+         b += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        float v[32];
+        const float4* s4 = reinterpret_cast<const float4*>(src + b * 32);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 t = s4[i];
+            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+        }
+        uint8_t* out = dst + b * BB;
+        if (QT == Q3X_HIP_MATRIX_Q8_0) {
+            float maximum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) maximum = fabsf(v[i]) > maximum ? fabsf(v[i]) : maximum;
+            const float scale = maximum / 127.0f;
+            const float inverse = scale != 0.0f ? 1.0f / scale : 0.0f;
+            const uint16_t h = f32_to_f16_rne(scale);
+            out[0] = static_cast<uint8_t>(h & 0xff);
+            out[1] = static_cast<uint8_t>(h >> 8);
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const float normalized = v[i] * inverse;
+                float rounded = copysignf(floorf(fabsf(normalized) + 0.5f), normalized);
+                rounded = fminf(fmaxf(rounded, -127.0f), 127.0f);
+                out[2 + i] = static_cast<uint8_t>(static_cast<int8_t>(static_cast<int>(rounded)));
+            }
+        } else {
+            int largest = 0;
+#pragma unroll
+            for (int i = 1; i < 32; ++i) largest = fabsf(v[i]) > fabsf(v[largest]) ? i : largest;
+            float maximum = v[0];
+#pragma unroll
+            for (int i = 1; i < 32; ++i) maximum = i == largest ? v[i] : maximum;
+            const float scale = maximum / -8.0f;
+            const float inverse = scale != 0.0f ? 1.0f / scale : 0.0f;
+            const uint16_t h = f32_to_f16_rne(scale);
+            out[0] = static_cast<uint8_t>(h & 0xff);
+            out[1] = static_cast<uint8_t>(h >> 8);
+            uint32_t q[32];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const float normalized = v[i] * inverse;
+                const float t = truncf(normalized + 8.5f);
+                q[i] = static_cast<uint32_t>(static_cast<int>(fminf(t, 15.0f)));
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) out[2 + i] = static_cast<uint8_t>(q[i] | (q[16 + i] << 4));
+        }
+    }
+}
+
+}  // namespace q3x
+
+using namespace q3x;
+
+extern "C" const char* q3x_hip_strerror(int code) {
+    switch (code) {
+    case Q3X_HIP_OK: return "ok";
+    case Q3X_HIP_EINVAL: return "invalid argument";
+    case Q3X_HIP_ERUNTIME: return "HIP runtime error";
+    case Q3X_HIP_ENOTSUP: return "matrix type not handled by this backend";
+    default: return "unknown error";
+    }
+}
+
+extern "C" int q3x_hip_quantized_bytes(uint32_t type, int rows, int cols, size_t* bytes) {
+    size_t value;
+    if (!bytes || !quantized_size(type, rows, cols, &value)) return Q3X_HIP_EINVAL;
+    *bytes = value;
+    return Q3X_HIP_OK;
+}
+
+extern "C" int q3x_hip_dequant(const void* w, uint32_t type, int cols, int row0, int nrows, float* out,
+                               hipStream_t stream) {
+    if (type == Q3X_HIP_MATRIX_BF16) return Q3X_HIP_ENOTSUP;
+    size_t bytes;
+    if (!w || !out || row0 < 0 || !quantized_size(type, nrows, cols, &bytes)) return Q3X_HIP_EINVAL;
+    if (static_cast<long long>(row0) + nrows > 0x7fffffffLL) return Q3X_HIP_EINVAL;
+    const size_t total = static_cast<size_t>(nrows) * cols;
+    const unsigned grid = static_cast<unsigned>(std::min<size_t>((total + 255) / 256, 1u << 20));
+    const uint8_t* src = static_cast<const uint8_t*>(w);
+    if (type == Q3X_HIP_MATRIX_Q8_0)
+        hipLaunchKernelGGL(dequant_kernel<Q3X_HIP_MATRIX_Q8_0>, dim3(grid), dim3(256), 0, stream, src, cols,
+                           row0, nrows, out);
+    else
+        hipLaunchKernelGGL(dequant_kernel<Q3X_HIP_MATRIX_Q4_0>, dim3(grid), dim3(256), 0, stream, src, cols,
+                           row0, nrows, out);
+    return launch_status();
+}
+
+extern "C" int q3x_hip_quantize(uint32_t type, const float* src, int rows, int cols, void* dst,
+                                hipStream_t stream) {
+    if (type == Q3X_HIP_MATRIX_BF16) return Q3X_HIP_ENOTSUP;
+    size_t bytes;
+    if (!src || !dst || !quantized_size(type, rows, cols, &bytes) || !aligned(src, 16))
+        return Q3X_HIP_EINVAL;
+    const size_t blocks = static_cast<size_t>(rows) * (cols / kBlock);
+    const unsigned grid = static_cast<unsigned>(std::min<size_t>((blocks + 255) / 256, 1u << 20));
+    uint8_t* out = static_cast<uint8_t*>(dst);
+    if (type == Q3X_HIP_MATRIX_Q8_0)
+        hipLaunchKernelGGL(quantize_kernel<Q3X_HIP_MATRIX_Q8_0>, dim3(grid), dim3(256), 0, stream, src, blocks,
+                           out);
+    else
+        hipLaunchKernelGGL(quantize_kernel<Q3X_HIP_MATRIX_Q4_0>, dim3(grid), dim3(256), 0, stream, src, blocks,
+                           out);
+    return launch_status();
+}

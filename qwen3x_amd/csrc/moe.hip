@@ -1,0 +1,463 @@
+// moe.hip -- router top-k and the routed-expert matmul of the MoE layer.
+//
+// Reference: engine.cpp:377-420 (CPU router_top_k and routed loop of moe())
+// and arch/cuda/engine.cu:1153-1250, 1709-1726 (router_top_k_kernel runs one
+// thread for one token; expert_gate_up_q4_kernel / expert_swiglu_kernel /
+// expert_down_weighted_q4_kernel run per token, so the reference has no
+// grouped expert GEMM and its prefill is token by token).
+//
+// Here the router runs one wavefront per token.  The routed matmul has two
+// shapes:
+//   decode (tokens == 1): the selected experts are one tall virtual matrix
+//     for the staged matvec (matvec.h), then SwiGLU, the down matvec, and a
+//     combine in slot order;
+//   prefill (tokens > 1): the (token, slot) pairs are grouped by expert with
+//     a stable counting sort (deterministic positions), each expert's group is
+//     cut into 32-token tiles, and one grouped FP32-MFMA GEMM launch (gemm.h)
+//     runs gate_up for every tile of every expert, then SwiGLU, then one for
+//     down; a combine sums the slots of each token in slot order from zero.
+// No atomics touch any accumulated value, so results are deterministic.
+#include "gemm.h"
+#include "matvec.h"
+
+namespace q3x {
+
+constexpr int kRouterMaxExperts = 1024;
+constexpr int kRouterMaxTopK = 8;          // q3x_model::MAX_TOP_K (model_config.h:14)
+constexpr int kGroupThreads = 1024;
+constexpr int kChunk = 1024;               // pairs per grouping chunk
+// Grouped GEMM: 1 x 4 waves of one 32x32 tile -> 32 pairs x 128 weight rows
+// (experts average 64 pairs at 2048 tokens, so short tiles waste little).
+constexpr int kGrpWM = 1, kGrpWN = 4, kGrpTM = 1, kGrpTN = 1;
+constexpr int kGrpBM = kGrpWM * kGrpTM * 32;
+constexpr int kGrpBN = kGrpWN * kGrpTN * 32;
+
+// ---------------------------------------------------------------- router ----
+
+// One wavefront per token.  Softmax with the maximum subtracted, then top_k
+// passes of a wave-wide argmax (larger probability wins; equal values go to
+// the lower expert index, as the reference's strict '>' scan does), then
+// weights = p / (sum of the selected p, added in slot order).
+__global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int tokens,
+                                                          int experts, int top_k, int* __restrict__ ids,
+                                                          float* __restrict__ weights) {
+    constexpr int PER_LANE = kRouterMaxExperts / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int token = blockIdx.x * 4 + threadIdx.x / kWave;
+    if (token >= tokens) return;
+    const float* row = logits + static_cast<size_t>(token) * experts;
+    float p[PER_LANE];
+    float maximum = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) {
+        const int e = lane + kWave * j;
+        p[j] = e < experts ? row[e] : -INFINITY;
+        maximum = maximum < p[j] ? p[j] : maximum;  // std::max(maximum, logit)
+    }
+#pragma unroll
+    for (int offset = kWave / 2; offset > 0; offset >>= 1) {
+        const float other = __shfl_xor(maximum, offset);
+        maximum = maximum < other ? other : maximum;
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) {
+        const int e = lane + kWave * j;
+        p[j] = e < experts ? expf(p[j] - maximum) : 0.0f;
+        total += p[j];
+    }
+    total = group_sum<kWave>(total);
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) {
+        const int e = lane + kWave * j;
+        p[j] = e < experts ? p[j] / total : -1.0f;  // -1: never selected
+    }
+    float chosen[kRouterMaxTopK];
+    int chosen_id[kRouterMaxTopK];
+#pragma unroll
+    for (int slot = 0; slot < kRouterMaxTopK; ++slot) {
+        chosen[slot] = 0.0f;
+        chosen_id[slot] = 0;
+        if (slot >= top_k) continue;
+        float best = -1.0f;
+        int best_id = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < PER_LANE; ++j) {
+            if (p[j] > best) { best = p[j]; best_id = lane + kWave * j; }
+        }
+#pragma unroll
+        for (int offset = kWave / 2; offset > 0; offset >>= 1) {
+            const float ov = __shfl_xor(best, offset);
+            const int oi = __shfl_xor(best_id, offset);
+            if (ov > best || (ov == best && oi < best_id)) { best = ov; best_id = oi; }
+        }
+        chosen[slot] = best;
+        chosen_id[slot] = best_id;
+#pragma unroll
+        for (int j = 0; j < PER_LANE; ++j)
+            if (lane + kWave * j == best_id) p[j] = -1.0f;
+    }
+    float selected_total = 0.0f;
+#pragma unroll
+    for (int slot = 0; slot < kRouterMaxTopK; ++slot)
+        if (slot < top_k) selected_total += chosen[slot];
+    float mine = 0.0f;
+    int mine_id = 0;
+#pragma unroll
+    for (int slot = 0; slot < kRouterMaxTopK; ++slot)
+        if (slot == lane) { mine = chosen[slot]; mine_id = chosen_id[slot]; }
+    if (lane < top_k) {
+        ids[static_cast<size_t>(token) * top_k + lane] = mine_id;
+        weights[static_cast<size_t>(token) * top_k + lane] = mine / selected_total;
+    }
+}
+
+// ------------------------------------------------------------ workspace ----
+
+struct MoeLayout {
+    size_t ntiles, nvalid, tile_expert, tile_start, tile_count, pos_of_pair, src_token;
+    size_t chunk_counts, chunk_base;
+    int chunks;
+    size_t gu, h, d, total;
+    int max_tiles;
+};
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+inline MoeLayout moe_layout(int tokens, int experts, int top_k, int H, int I) {
+    MoeLayout L{};
+    const size_t P = static_cast<size_t>(tokens) * top_k;
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t at = off; off = align_up(off + bytes, 256); return at; };
+    if (tokens > 1) {
+        L.max_tiles = static_cast<int>(P / kGrpBM + std::min<size_t>(experts, P) + 1);
+        L.ntiles = take(sizeof(int));
+        L.nvalid = take(sizeof(int));
+        L.tile_expert = take(sizeof(int) * L.max_tiles);
+        L.tile_start = take(sizeof(int) * L.max_tiles);
+        L.tile_count = take(sizeof(int) * L.max_tiles);
+        L.pos_of_pair = take(sizeof(int) * P);
+        L.src_token = take(sizeof(int) * P);
+        L.chunks = static_cast<int>((P + kChunk - 1) / kChunk);
+        L.chunk_counts = take(sizeof(int) * static_cast<size_t>(L.chunks) * experts);
+        L.chunk_base = take(sizeof(int) * static_cast<size_t>(L.chunks) * experts);
+    }
+    L.gu = take(sizeof(float) * P * 2 * I);
+    L.h = take(sizeof(float) * P * I);
+    L.d = take(sizeof(float) * P * H);
+    L.total = off;
+    return L;
+}
+
+// ------------------------------------------------------------- grouping ----
+
+// Inclusive-to-exclusive block scan of v over kGroupThreads threads.
+__device__ int block_exclusive_scan(int v, int* buf) {
+    const int t = threadIdx.x;
+    buf[t] = v;
+    __syncthreads();
+    for (int offset = 1; offset < kGroupThreads; offset <<= 1) {
+        const int add = t >= offset ? buf[t - offset] : 0;
+        __syncthreads();
+        buf[t] += add;
+        __syncthreads();
+    }
+    const int inclusive = buf[t];
+    __syncthreads();
+    return inclusive - v;
+}
+
+// Stable counting sort of the (token, slot) pairs by expert, in three steps:
+// a per-chunk expert histogram (moe_count_kernel), one workgroup that turns
+// the histograms into group starts, per-chunk bases and the tile table
+// (moe_scan_kernel), and a per-chunk scatter where each pair's rank is the
+// number of earlier pairs of its chunk with the same expert
+// (moe_scatter_kernel).  Every expert's group therefore lists its pairs in
+// (token, slot) order and positions are identical on every run.  Pairs with
+// an id outside [0, experts) get position -1.
+__global__ __launch_bounds__(kChunk) void moe_count_kernel(const int* __restrict__ ids, int P, int experts,
+                                                           int* __restrict__ chunk_counts) {
+    __shared__ int hist[kRouterMaxExperts];
+    for (int e = threadIdx.x; e < experts; e += kChunk) hist[e] = 0;
+    __syncthreads();
+    const int p = blockIdx.x * kChunk + threadIdx.x;
+    if (p < P) {
+        const int e = ids[p];
+        if (e >= 0 && e < experts) atomicAdd(&hist[e], 1);  // integer count: order-free
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < experts; e += kChunk)
+        chunk_counts[static_cast<size_t>(blockIdx.x) * experts + e] = hist[e];
+}
+
+__global__ __launch_bounds__(kGroupThreads) void moe_scan_kernel(
+    const int* __restrict__ chunk_counts, int chunks, int experts, int bm, int* __restrict__ chunk_base,
+    int* __restrict__ tile_expert, int* __restrict__ tile_start, int* __restrict__ tile_count,
+    int* __restrict__ ntiles, int* __restrict__ nvalid) {
+    __shared__ int buf[kGroupThreads];
+    const int e = threadIdx.x;
+    const bool owner = e < experts;
+    int total = 0;
+    if (owner) {
+#pragma unroll 8
+        for (int c = 0; c < chunks; ++c) total += chunk_counts[static_cast<size_t>(c) * experts + e];
+    }
+    const int start = block_exclusive_scan(total, buf);
+    if (owner) {
+        int run = start;
+        for (int c = 0; c < chunks; ++c) {
+            const size_t at = static_cast<size_t>(c) * experts + e;
+            chunk_base[at] = run;
+            run += chunk_counts[at];
+        }
+    }
+    const int tiles = owner ? (total + bm - 1) / bm : 0;
+    const int tile0 = block_exclusive_scan(tiles, buf);
+    for (int j = 0; j < tiles; ++j) {
+        tile_expert[tile0 + j] = e;
+        tile_start[tile0 + j] = start + j * bm;
+        tile_count[tile0 + j] = min(bm, total - j * bm);
+    }
+    if (e == kGroupThreads - 1) { *ntiles = tile0 + tiles; *nvalid = start + total; }
+}
+
+__global__ __launch_bounds__(kChunk) void moe_scatter_kernel(const int* __restrict__ ids, int P, int top_k,
+                                                             int experts, const int* __restrict__ chunk_base,
+                                                             int* __restrict__ pos_of_pair,
+                                                             int* __restrict__ src_token) {
+    __shared__ int chunk_ids[kChunk];
+    const int t = threadIdx.x;
+    const int p = blockIdx.x * kChunk + t;
+    const int e = p < P ? ids[p] : -1;
+    chunk_ids[t] = e;
+    __syncthreads();
+    if (p >= P) return;
+    if (e < 0 || e >= experts) { pos_of_pair[p] = -1; return; }
+    int rank = 0;
+    for (int u = 0; u < t; ++u) rank += chunk_ids[u] == e;
+    const int pos = chunk_base[static_cast<size_t>(blockIdx.x) * experts + e] + rank;
+    pos_of_pair[p] = pos;
+    src_token[pos] = p / top_k;
+}
+
+// Grouped GEMM policy: tile ty is the tile table's entry; A rows are
+// gathered (a_index[position] = source row) or taken in position order; the
+// weights are expert tile_expert[ty] of the pool; out[position, n].
+struct GroupedGemm {
+    const float* A;
+    int a_cols;
+    const int* a_index;
+    const uint8_t* pool;
+    size_t expert_bytes;
+    size_t row_bytes;
+    const int* tile_expert;
+    const int* tile_start;
+    const int* tile_count;
+    const int* ntiles;
+    float* out;
+    int out_cols;
+    __device__ bool tile(int ty, int, GemmTile& t) const {
+        if (ty >= *ntiles) return false;
+        t.group = tile_expert[ty];
+        t.m0 = tile_start[ty];
+        t.mcount = tile_count[ty];
+        return true;
+    }
+    __device__ const float* a_row(const GemmTile& t, int m) const {
+        const int pos = t.m0 + m;
+        const int row = a_index ? a_index[pos] : pos;
+        return A + static_cast<size_t>(row) * a_cols;
+    }
+    __device__ const uint8_t* b_row(const GemmTile& t, int n) const {
+        return pool + static_cast<size_t>(t.group) * expert_bytes + static_cast<size_t>(n) * row_bytes;
+    }
+    __device__ void store(const GemmTile& t, int m, int n, float v) const {
+        out[static_cast<size_t>(t.m0 + m) * out_cols + n] = v;
+    }
+};
+
+// h[pos, j] = silu(gu[pos, j]) * gu[pos, I + j] for pos < *count
+// (engine.cpp:415-416).  count == nullptr: `limit` rows.
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ gu, float* __restrict__ h,
+                                                     int I, int limit, const int* __restrict__ count) {
+    const int rows = count ? *count : limit;
+    const size_t total = static_cast<size_t>(rows) * I;
+    for (size_t idx = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; idx < total;
+         idx += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const size_t pos = idx / I, j = idx % I;
+        const float g = gu[pos * 2 * I + j];
+        const float u = gu[pos * 2 * I + I + j];
+        h[idx] = silu_ref(g) * u;
+    }
+}
+
+// Y[t, i] (+)= sum over slots, in slot order from zero, of
+// weights[t, slot] * d[pos, i] (engine.cpp:411, 418-419: out = 0 then
+// out += w * d per slot).  pos = pos_of_pair[t*top_k + slot] (grouped) or the
+// slot itself (decode); slots with an out-of-range expert id are skipped.
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ d, const int* __restrict__ pos_of_pair,
+                                                      const int* __restrict__ ids, int experts,
+                                                      const float* __restrict__ weights, int tokens, int top_k,
+                                                      int H, float* __restrict__ Y, int accumulate) {
+    const size_t idx = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    if (idx >= static_cast<size_t>(tokens) * H) return;
+    const int t = static_cast<int>(idx / H), i = static_cast<int>(idx % H);
+    float acc = 0.0f;
+    for (int slot = 0; slot < top_k; ++slot) {
+        const int pair = t * top_k + slot;
+        int pos;
+        if (pos_of_pair) {
+            pos = pos_of_pair[pair];
+        } else {
+            const int e = ids[pair];
+            pos = (e >= 0 && e < experts) ? slot : -1;
+        }
+        if (pos < 0) continue;
+        acc = fmaf(weights[pair], d[static_cast<size_t>(pos) * H + i], acc);
+    }
+    if (accumulate) Y[idx] += acc;
+    else Y[idx] = acc;
+}
+
+template <uint32_t QT>
+int moe_decode(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
+               const int* ids, const float* weights, int top_k, float* Y, int accumulate,
+               uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
+    constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
+    float* gu = reinterpret_cast<float*>(ws + L.gu);
+    float* h = reinterpret_cast<float*>(ws + L.h);
+    float* d = reinterpret_cast<float*>(ws + L.d);
+    const size_t gu_row = static_cast<size_t>(H / kBlock) * BB;
+    const size_t down_row = static_cast<size_t>(I / kBlock) * BB;
+    ExpertRows<true> gate{gate_up, gu_row * 2 * I, gu_row, 2 * I, experts, ids, X, 0, gu};
+    const bool gate_staged = aligned(gate_up, 16) && aligned(X, 16) && gu_row % 16 == 0;
+    int status = launch_mv<QT>(gate, top_k * 2 * I, H / kBlock, gate_staged, stream);
+    if (status != Q3X_HIP_OK) return status;
+    const int sw = top_k * I;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((sw + 255) / 256), dim3(256), 0, stream, gu, h, I, top_k,
+                       nullptr);
+    if ((status = launch_status()) != Q3X_HIP_OK) return status;
+    ExpertRows<false> dn{down, down_row * H, down_row, H, experts, ids, h, static_cast<size_t>(I), d};
+    const bool down_staged = aligned(down, 16) && down_row % 16 == 0;
+    status = launch_mv<QT>(dn, top_k * H, I / kBlock, down_staged, stream);
+    if (status != Q3X_HIP_OK) return status;
+    hipLaunchKernelGGL(combine_kernel, dim3((H + 255) / 256), dim3(256), 0, stream, d, nullptr, ids,
+                       experts, weights, 1, top_k, H, Y, accumulate);
+    return launch_status();
+}
+
+template <uint32_t QT>
+int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
+                int tokens, const int* ids, const float* weights, int top_k, float* Y, int accumulate,
+                uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
+    constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
+    const int P = tokens * top_k;
+    int* ntiles = reinterpret_cast<int*>(ws + L.ntiles);
+    int* nvalid = reinterpret_cast<int*>(ws + L.nvalid);
+    int* tile_expert = reinterpret_cast<int*>(ws + L.tile_expert);
+    int* tile_start = reinterpret_cast<int*>(ws + L.tile_start);
+    int* tile_count = reinterpret_cast<int*>(ws + L.tile_count);
+    int* pos_of_pair = reinterpret_cast<int*>(ws + L.pos_of_pair);
+    int* src_token = reinterpret_cast<int*>(ws + L.src_token);
+    float* gu = reinterpret_cast<float*>(ws + L.gu);
+    float* h = reinterpret_cast<float*>(ws + L.h);
+    float* d = reinterpret_cast<float*>(ws + L.d);
+
+    int* chunk_counts = reinterpret_cast<int*>(ws + L.chunk_counts);
+    int* chunk_base = reinterpret_cast<int*>(ws + L.chunk_base);
+    hipLaunchKernelGGL(moe_count_kernel, dim3(L.chunks), dim3(kChunk), 0, stream, ids, P, experts, chunk_counts);
+    int status = launch_status();
+    if (status != Q3X_HIP_OK) return status;
+    hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(kGroupThreads), 0, stream,
+                       static_cast<const int*>(chunk_counts), L.chunks, experts, kGrpBM, chunk_base, tile_expert,
+                       tile_start, tile_count, ntiles, nvalid);
+    if ((status = launch_status()) != Q3X_HIP_OK) return status;
+    hipLaunchKernelGGL(moe_scatter_kernel, dim3(L.chunks), dim3(kChunk), 0, stream, ids, P, top_k, experts,
+                       static_cast<const int*>(chunk_base), pos_of_pair, src_token);
+    if ((status = launch_status()) != Q3X_HIP_OK) return status;
+
+    const size_t gu_row = static_cast<size_t>(H / kBlock) * BB;
+    const size_t down_row = static_cast<size_t>(I / kBlock) * BB;
+    const int tiles_bound = L.max_tiles;
+    GroupedGemm g1{X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
+                   ntiles, gu, 2 * I};
+    hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm>),
+                       dim3((2 * I + kGrpBN - 1) / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0,
+                       stream, g1, 2 * I, H);
+    if ((status = launch_status()) != Q3X_HIP_OK) return status;
+    const size_t sw = static_cast<size_t>(P) * I;
+    const int sw_blocks = static_cast<int>(std::min<size_t>((sw + 255) / 256, 65536));
+    hipLaunchKernelGGL(swiglu_kernel, dim3(sw_blocks), dim3(256), 0, stream, gu, h, I, 0,
+                       static_cast<const int*>(nvalid));
+    if ((status = launch_status()) != Q3X_HIP_OK) return status;
+    GroupedGemm g2{h, I, nullptr, down, down_row * H, down_row, tile_expert, tile_start, tile_count,
+                   ntiles, d, H};
+    hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm>),
+                       dim3((H + kGrpBN - 1) / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0,
+                       stream, g2, H, I);
+    if ((status = launch_status()) != Q3X_HIP_OK) return status;
+    const size_t outs = static_cast<size_t>(tokens) * H;
+    hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0,
+                       stream, d, pos_of_pair, ids, experts, weights, tokens, top_k, H, Y, accumulate);
+    return launch_status();
+}
+
+}  // namespace q3x
+
+using namespace q3x;
+
+extern "C" int q3x_hip_router_topk(const float* logits, int tokens, int experts, int top_k, int* ids,
+                                   float* weights, hipStream_t stream) {
+    if (!logits || !ids || !weights || tokens <= 0 || experts <= 0 || experts > kRouterMaxExperts ||
+        top_k <= 0 || top_k > experts || top_k > kRouterMaxTopK)
+        return Q3X_HIP_EINVAL;
+    hipLaunchKernelGGL(router_topk_kernel, dim3((tokens + 3) / 4), dim3(256), 0, stream, logits, tokens,
+                       experts, top_k, ids, weights);
+    return launch_status();
+}
+
+static bool moe_shape_ok(uint32_t type, int experts, int H, int I, int tokens, int top_k) {
+    size_t bytes;
+    if (experts <= 0 || experts > kRouterMaxExperts || tokens <= 0 || top_k <= 0 || top_k > experts)
+        return false;
+    if (!quantized_size(type, 2 * I, H, &bytes) || !quantized_size(type, H, I, &bytes)) return false;
+    // Pool sizes and pair counts must fit the kernels' index types.
+    const long long pairs = static_cast<long long>(tokens) * top_k;
+    if (pairs > 0x7fffffffLL) return false;
+    // Grouped tiles index grid.y (<= 65535).
+    if (tokens > 1 && pairs / kGrpBM + std::min<long long>(experts, pairs) + 1 > 65535) return false;
+    return true;
+}
+
+extern "C" size_t q3x_hip_moe_workspace_bytes(int tokens, int experts, int top_k, int H, int I) {
+    if (tokens <= 0 || experts <= 0 || top_k <= 0 || H <= 0 || I <= 0) return 0;
+    return moe_layout(tokens, experts, top_k, H, I).total;
+}
+
+extern "C" int q3x_hip_moe_routed(const void* gate_up, const void* down, uint32_t type, int experts, int H,
+                                  int I, const float* X, int tokens, const int* ids, const float* weights,
+                                  int top_k, float* Y, int accumulate, void* workspace, size_t workspace_bytes,
+                                  hipStream_t stream) {
+    if (type == Q3X_HIP_MATRIX_BF16) return Q3X_HIP_ENOTSUP;
+    if (!gate_up || !down || !X || !ids || !weights || !Y || !workspace || !is_quant_type(type) ||
+        !moe_shape_ok(type, experts, H, I, tokens, top_k))
+        return Q3X_HIP_EINVAL;
+    const MoeLayout L = moe_layout(tokens, experts, top_k, H, I);
+    if (workspace_bytes < L.total || !aligned(workspace, 256)) return Q3X_HIP_EINVAL;
+    if (!aligned(gate_up, 2) || !aligned(down, 2) || !aligned(X, 16)) return Q3X_HIP_EINVAL;
+    const uint8_t* gu = static_cast<const uint8_t*>(gate_up);
+    const uint8_t* dn = static_cast<const uint8_t*>(down);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    if (tokens == 1) {
+        return type == Q3X_HIP_MATRIX_Q8_0
+                   ? moe_decode<Q3X_HIP_MATRIX_Q8_0>(gu, dn, experts, H, I, X, ids, weights, top_k, Y,
+                                                     accumulate, ws, L, stream)
+                   : moe_decode<Q3X_HIP_MATRIX_Q4_0>(gu, dn, experts, H, I, X, ids, weights, top_k, Y,
+                                                     accumulate, ws, L, stream);
+    }
+    return type == Q3X_HIP_MATRIX_Q8_0
+               ? moe_grouped<Q3X_HIP_MATRIX_Q8_0>(gu, dn, experts, H, I, X, tokens, ids, weights, top_k, Y,
+                                                  accumulate, ws, L, stream)
+               : moe_grouped<Q3X_HIP_MATRIX_Q4_0>(gu, dn, experts, H, I, X, tokens, ids, weights, top_k, Y,
+                                                  accumulate, ws, L, stream);
+}

@@ -1,0 +1,67 @@
+// hip_ops.cpp -- see hip_ops.h.
+#include "hip_ops.h"
+
+#include <cstdio>
+#include <cstdlib>
+
+namespace qwen3x_hip {
+namespace {
+
+void check(int status, const char* what, const char* file, int line) {
+    if (status == Q3X_HIP_OK) return;
+    std::fprintf(stderr, "%s:%d: %s failed: %s (%d)\n", file, line, what, q3x_hip_strerror(status), status);
+    std::abort();
+}
+
+#define Q3X_HIP_CHECK(call) check((call), #call, __FILE__, __LINE__)
+
+}  // namespace
+
+void mv(const Linear& linear, const float* input, float* output, hipStream_t stream) {
+    Q3X_HIP_CHECK(q3x_hip_mv(linear.weight, linear.type, linear.rows, linear.columns, input, output, 0,
+                             stream));
+}
+
+void mv_add(const Linear& linear, const float* input, float* output, hipStream_t stream) {
+    Q3X_HIP_CHECK(q3x_hip_mv(linear.weight, linear.type, linear.rows, linear.columns, input, output, 1,
+                             stream));
+}
+
+void batch_mv(const Linear& linear, const float* input, float* output, int count, bool add,
+              hipStream_t stream) {
+    Q3X_HIP_CHECK(q3x_hip_gemm(linear.weight, linear.type, linear.rows, linear.columns, input, count,
+                               output, add ? 1 : 0, stream));
+}
+
+void embed(const Linear& table, int token, float* output, hipStream_t stream) {
+    if (token < 0 || token >= table.rows) {
+        std::fprintf(stderr, "embedding token=%d rows=%d\n", token, table.rows);
+        std::abort();
+    }
+    Q3X_HIP_CHECK(q3x_hip_dequant(table.weight, table.type, table.columns, token, 1, output, stream));
+}
+
+void router_top_k(const float* logits, int tokens, int experts, int top_k, int* ids, float* weights,
+                  hipStream_t stream) {
+    Q3X_HIP_CHECK(q3x_hip_router_topk(logits, tokens, experts, top_k, ids, weights, stream));
+}
+
+size_t moe_workspace_bytes(int tokens, int experts, int top_k, int H, int I) {
+    return q3x_hip_moe_workspace_bytes(tokens, experts, top_k, H, I);
+}
+
+void moe_routed(const ExpertLinear& gate_up, const ExpertLinear& down, const float* input, int tokens,
+                const int* ids, const float* weights, int top_k, float* output, bool add, void* workspace,
+                size_t workspace_bytes, hipStream_t stream) {
+    if (gate_up.type != down.type || gate_up.experts != down.experts || gate_up.columns != down.rows ||
+        gate_up.rows != 2 * down.columns) {
+        std::fprintf(stderr, "moe_routed: gate_up [%d,%d,%d] and down [%d,%d,%d] do not match\n",
+                     gate_up.experts, gate_up.rows, gate_up.columns, down.experts, down.rows, down.columns);
+        std::abort();
+    }
+    Q3X_HIP_CHECK(q3x_hip_moe_routed(gate_up.weight, down.weight, gate_up.type, gate_up.experts,
+                                     gate_up.columns, down.columns, input, tokens, ids, weights, top_k,
+                                     output, add ? 1 : 0, workspace, workspace_bytes, stream));
+}
+
+}  // namespace qwen3x_hip

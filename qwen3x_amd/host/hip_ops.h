@@ -1,0 +1,60 @@
+// hip_ops.h -- C++ host interface of the HIP backend's quantized matmul, in
+// the shape of the reference CUDA backend's host helpers so an arch/hip
+// engine can call it exactly where engine.cu calls mv / mv_add / batch_mv /
+// moe.  Every function enqueues on `stream` and, like the reference (CUDA_OK
+// and Q3X_ASSERT, arch/cuda/engine.cu:48-56, internal.h:76-85), reports and
+// aborts on any error.  The work itself is done by the C ABI in q3x_hip.h.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+#include "q3x_hip.h"
+
+namespace qwen3x_hip {
+
+// q3x_model::MatrixType (model_config.h:16-20).
+enum MatrixType : uint32_t {
+    MATRIX_BF16 = Q3X_HIP_MATRIX_BF16,
+    MATRIX_Q8_0 = Q3X_HIP_MATRIX_Q8_0,
+    MATRIX_Q4_0 = Q3X_HIP_MATRIX_Q4_0,
+};
+
+// engine.cu:68-73
+struct Linear {
+    const void* weight = nullptr;
+    int rows = 0;
+    int columns = 0;
+    MatrixType type = MATRIX_BF16;
+};
+
+// engine.cu:89-95: experts contiguous matrices W[experts, rows, columns].
+struct ExpertLinear {
+    const void* weight = nullptr;
+    int experts = 0;
+    int rows = 0;
+    int columns = 0;
+    MatrixType type = MATRIX_BF16;
+};
+
+// output[rows] = W input (engine.cu:1531).
+void mv(const Linear& linear, const float* input, float* output, hipStream_t stream);
+// output[rows] += W input (engine.cu:1547).
+void mv_add(const Linear& linear, const float* input, float* output, hipStream_t stream);
+// output[count, rows] (+)= input[count, columns] W^T (engine.cu:1568, without
+// the cuBLAS handle and BF16 staging buffer of the BF16 path).
+void batch_mv(const Linear& linear, const float* input, float* output, int count, bool add,
+              hipStream_t stream);
+// output[columns] = dequantised row `token` (engine.cu:1499 embed).
+void embed(const Linear& table, int token, float* output, hipStream_t stream);
+// ids / weights [tokens, top_k] from logits [tokens, experts] (engine.cu:1153).
+void router_top_k(const float* logits, int tokens, int experts, int top_k, int* ids, float* weights,
+                  hipStream_t stream);
+// Routed experts of `tokens` tokens (engine.cu:1709-1726 routed part):
+// output (+)= sum_slot weights * down_e(silu(gate_e x) * up_e x).
+size_t moe_workspace_bytes(int tokens, int experts, int top_k, int H, int I);
+void moe_routed(const ExpertLinear& gate_up, const ExpertLinear& down, const float* input, int tokens,
+                const int* ids, const float* weights, int top_k, float* output, bool add, void* workspace,
+                size_t workspace_bytes, hipStream_t stream);
+
+}  // namespace qwen3x_hip

@@ -1,0 +1,296 @@
+// host_test.cpp -- the reference's GPU/CPU quantized-path unit tests, restated
+// against the HIP backend through the C++ host interface (hip_ops.h).
+//
+// Cases and tolerances follow tests/q4_cuda_test.cu (q4_mv_test :31-60,
+// router_test :109-131, expert_moe_test :62-107), tests/q8_cpu_test.cpp
+// (fixed 2x64 Q8_0 vector and embed, :271-318) and tests/q4_cpu_test.cpp
+// (q4_math_test :138-178).  Exit 0 = pass, 77 = no GPU (the reference CI's
+// skip code, .github/workflows/ci.yml:53-55), anything else = failure.
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include <hip/hip_runtime.h>
+
+#include "hip_ops.h"
+
+namespace {
+
+#define HIP_OK(call)                                                                    \
+    do {                                                                                \
+        const hipError_t e = (call);                                                    \
+        if (e != hipSuccess) {                                                          \
+            std::fprintf(stderr, "%s:%d: %s: %s\n", __FILE__, __LINE__, #call,         \
+                         hipGetErrorString(e));                                         \
+            std::exit(1);                                                               \
+        }                                                                               \
+    } while (0)
+
+#define CHECK(cond)                                                                     \
+    do {                                                                                \
+        if (!(cond)) {                                                                  \
+            std::fprintf(stderr, "%s:%d: check failed: %s\n", __FILE__, __LINE__, #cond); \
+            std::exit(1);                                                               \
+        }                                                                               \
+    } while (0)
+
+struct Q8Block { uint16_t scale; int8_t values[32]; };
+struct Q4Block { uint16_t scale; uint8_t values[16]; };
+static_assert(sizeof(Q8Block) == 34, "Q8_0 block layout");
+static_assert(sizeof(Q4Block) == 18, "Q4_0 block layout");
+
+template <typename T>
+T* device_copy(const T* source, size_t count) {
+    T* result = nullptr;
+    HIP_OK(hipMalloc(&result, count * sizeof(T)));
+    HIP_OK(hipMemcpy(result, source, count * sizeof(T), hipMemcpyHostToDevice));
+    return result;
+}
+
+template <typename T>
+std::vector<T> host_copy(const T* source, size_t count) {
+    std::vector<T> out(count);
+    HIP_OK(hipMemcpy(out.data(), source, count * sizeof(T), hipMemcpyDeviceToHost));
+    return out;
+}
+
+float* device_floats(size_t count) {
+    float* p = nullptr;
+    HIP_OK(hipMalloc(&p, count * sizeof(float)));
+    HIP_OK(hipMemset(p, 0, count * sizeof(float)));
+    return p;
+}
+
+float silu(float x) {  // engine.cpp:187-191
+    const float s = x >= 0.0f ? 1.0f / (1.0f + std::exp(-x)) : std::exp(x) / (1.0f + std::exp(x));
+    return x * s;
+}
+
+// tests/q4_cuda_test.cu:31-60
+void q4_mv_test() {
+    Q4Block host[2]{};
+    host[0].scale = 0x3c00;
+    host[1].scale = 0x3800;
+    for (int i = 0; i < 16; ++i) {
+        host[0].values[i] = static_cast<uint8_t>(i | ((15 - i) << 4));
+        host[1].values[i] = static_cast<uint8_t>((15 - i) | (i << 4));
+    }
+    float input[32];
+    for (int i = 0; i < 32; ++i) input[i] = (i % 9 - 4) * 0.25f;
+    float expected[2]{};
+    for (int row = 0; row < 2; ++row) {
+        const float scale = row == 0 ? 1.0f : 0.5f;
+        for (int i = 0; i < 16; ++i) {
+            expected[row] += scale * ((host[row].values[i] & 15) - 8) * input[i];
+            expected[row] += scale * ((host[row].values[i] >> 4) - 8) * input[i + 16];
+        }
+    }
+    auto* weight = device_copy(host, 2);
+    auto* device_input = device_copy(input, 32);
+    float* device_output = device_floats(2);
+    qwen3x_hip::mv({weight, 2, 32, qwen3x_hip::MATRIX_Q4_0}, device_input, device_output, nullptr);
+    const auto output = host_copy(device_output, 2);
+    CHECK(std::abs(output[0] - expected[0]) < 1e-5f);
+    CHECK(std::abs(output[1] - expected[1]) < 1e-5f);
+    // mv_add accumulates on top.
+    qwen3x_hip::mv_add({weight, 2, 32, qwen3x_hip::MATRIX_Q4_0}, device_input, device_output, nullptr);
+    const auto twice = host_copy(device_output, 2);
+    CHECK(std::abs(twice[0] - 2 * expected[0]) < 2e-5f);
+    CHECK(std::abs(twice[1] - 2 * expected[1]) < 2e-5f);
+    HIP_OK(hipFree(weight)); HIP_OK(hipFree(device_input)); HIP_OK(hipFree(device_output));
+}
+
+// tests/q8_cpu_test.cpp:271-318 (main): fixed 2x64 Q8_0, then embed row 1.
+void q8_fixed_test() {
+    Q8Block blocks[4]{};
+    const uint16_t scales[4] = {0x3c00, 0x3800, 0x4000, 0x3400};
+    for (int block = 0; block < 4; ++block) {
+        blocks[block].scale = scales[block];
+        for (int index = 0; index < 32; ++index)
+            blocks[block].values[index] = static_cast<int8_t>((index % 9) - 4 + block);
+    }
+    float input[64];
+    for (int index = 0; index < 64; ++index) input[index] = (index % 7 - 3) * 0.125f;
+    const float decoded_scales[4] = {1.0f, 0.5f, 2.0f, 0.25f};
+    float expected[2]{};
+    for (int row = 0; row < 2; ++row)
+        for (int block = 0; block < 2; ++block) {
+            float inner = 0.0f;
+            for (int index = 0; index < 32; ++index)
+                inner += blocks[row * 2 + block].values[index] * input[block * 32 + index];
+            expected[row] += decoded_scales[row * 2 + block] * inner;
+        }
+    auto* weight = device_copy(blocks, 4);
+    auto* device_input = device_copy(input, 64);
+    float* device_output = device_floats(2);
+    const qwen3x_hip::Linear matrix{weight, 2, 64, qwen3x_hip::MATRIX_Q8_0};
+    qwen3x_hip::mv(matrix, device_input, device_output, nullptr);
+    const auto output = host_copy(device_output, 2);
+    CHECK(std::abs(output[0] - expected[0]) < 1e-6f);
+    CHECK(std::abs(output[1] - expected[1]) < 1e-6f);
+
+    float* device_embedding = device_floats(64);
+    qwen3x_hip::embed(matrix, 1, device_embedding, nullptr);
+    const auto embedding = host_copy(device_embedding, 64);
+    for (int block = 0; block < 2; ++block)
+        for (int index = 0; index < 32; ++index)
+            CHECK(embedding[block * 32 + index] == decoded_scales[2 + block] * blocks[2 + block].values[index]);
+
+    // batch_mv: three identical tokens give the matvec result per token.
+    float batch_input[3 * 64];
+    for (int t = 0; t < 3; ++t) std::memcpy(batch_input + 64 * t, input, sizeof(input));
+    auto* device_batch = device_copy(batch_input, 3 * 64);
+    float* device_batch_out = device_floats(3 * 2);
+    qwen3x_hip::batch_mv(matrix, device_batch, device_batch_out, 3, false, nullptr);
+    const auto batch = host_copy(device_batch_out, 6);
+    for (int t = 0; t < 3; ++t)
+        for (int row = 0; row < 2; ++row) CHECK(std::abs(batch[2 * t + row] - expected[row]) < 1e-6f);
+    HIP_OK(hipFree(weight)); HIP_OK(hipFree(device_input)); HIP_OK(hipFree(device_output));
+    HIP_OK(hipFree(device_embedding)); HIP_OK(hipFree(device_batch)); HIP_OK(hipFree(device_batch_out));
+}
+
+// tests/q4_cpu_test.cpp:138-178
+void q4_math_test() {
+    Q4Block blocks[4]{};
+    const uint16_t scales[4] = {0x3c00, 0x3800, 0x4000, 0x3400};
+    for (int block = 0; block < 4; ++block) {
+        blocks[block].scale = scales[block];
+        for (int index = 0; index < 16; ++index) {
+            const int low = (index + block) % 16;
+            const int high = (15 - index + block) % 16;
+            blocks[block].values[index] = static_cast<uint8_t>(low | (high << 4));
+        }
+    }
+    float input[64];
+    for (int index = 0; index < 64; ++index) input[index] = (index % 7 - 3) * 0.125f;
+    const float decoded_scales[4] = {1.0f, 0.5f, 2.0f, 0.25f};
+    float expected[2]{};
+    for (int row = 0; row < 2; ++row)
+        for (int block = 0; block < 2; ++block)
+            for (int index = 0; index < 16; ++index) {
+                const uint8_t packed = blocks[row * 2 + block].values[index];
+                expected[row] += decoded_scales[row * 2 + block] * ((packed & 15) - 8) * input[block * 32 + index];
+                expected[row] += decoded_scales[row * 2 + block] * ((packed >> 4) - 8) * input[block * 32 + index + 16];
+            }
+    auto* weight = device_copy(blocks, 4);
+    auto* device_input = device_copy(input, 64);
+    float* device_output = device_floats(2);
+    const qwen3x_hip::Linear matrix{weight, 2, 64, qwen3x_hip::MATRIX_Q4_0};
+    qwen3x_hip::mv(matrix, device_input, device_output, nullptr);
+    const auto output = host_copy(device_output, 2);
+    CHECK(std::abs(output[0] - expected[0]) < 1e-6f);
+    CHECK(std::abs(output[1] - expected[1]) < 1e-6f);
+    float* device_embedding = device_floats(64);
+    qwen3x_hip::embed(matrix, 1, device_embedding, nullptr);
+    const auto embedding = host_copy(device_embedding, 64);
+    for (int index = 0; index < 16; ++index) {
+        const uint8_t low = blocks[2].values[index] & 15;
+        const uint8_t high = blocks[2].values[index] >> 4;
+        CHECK(embedding[index] == 2.0f * (low - 8));
+        CHECK(embedding[index + 16] == 2.0f * (high - 8));
+    }
+    HIP_OK(hipFree(weight)); HIP_OK(hipFree(device_input)); HIP_OK(hipFree(device_output));
+    HIP_OK(hipFree(device_embedding));
+}
+
+// tests/q4_cuda_test.cu:109-131 (and q4_cpu_test.cpp:180-202 for the six-logit case)
+void router_test() {
+    float logits[256];
+    for (int expert = 0; expert < 256; ++expert) logits[expert] = expert * 0.03125f;
+    auto* device_logits = device_copy(logits, 256);
+    int* ids = nullptr;
+    float* weights = device_floats(8);
+    HIP_OK(hipMalloc(&ids, 8 * sizeof(int)));
+    qwen3x_hip::router_top_k(device_logits, 1, 256, 8, ids, weights, nullptr);
+    const auto host_ids = host_copy(ids, 8);
+    const auto host_weights = host_copy(weights, 8);
+    float sum = 0.0f;
+    for (int slot = 0; slot < 8; ++slot) {
+        CHECK(host_ids[slot] == 255 - slot);
+        sum += host_weights[slot];
+    }
+    CHECK(std::abs(sum - 1.0f) < 1e-6f);
+
+    const float six[6] = {-2.0f, 3.0f, 1.0f, 4.0f, -1.0f, 2.0f};
+    auto* device_six = device_copy(six, 6);
+    qwen3x_hip::router_top_k(device_six, 1, 6, 3, ids, weights, nullptr);
+    const auto six_ids = host_copy(ids, 3);
+    const auto six_weights = host_copy(weights, 3);
+    CHECK(six_ids[0] == 3 && six_ids[1] == 1 && six_ids[2] == 5);
+    CHECK(std::abs(six_weights[0] + six_weights[1] + six_weights[2] - 1.0f) < 1e-6f);
+    HIP_OK(hipFree(device_logits)); HIP_OK(hipFree(device_six)); HIP_OK(hipFree(ids)); HIP_OK(hipFree(weights));
+}
+
+// tests/q4_cuda_test.cu:62-107: constant 0x99 nibbles (value 1) give closed
+// forms.  Run once as decode (1 token) and once grouped (3 equal tokens).
+void expert_moe_test() {
+    constexpr int EXPERTS = 4, TOP_K = 2, H = 32, I = 32;
+    const uint16_t scales[EXPERTS] = {0x3400, 0x3800, 0x3c00, 0x4000};
+    std::vector<Q4Block> host_gate(EXPERTS * 2 * I), host_down(EXPERTS * H);
+    for (int expert = 0; expert < EXPERTS; ++expert) {
+        for (int row = 0; row < 2 * I; ++row) {
+            host_gate[expert * 2 * I + row].scale = scales[expert];
+            std::memset(host_gate[expert * 2 * I + row].values, 0x99, 16);
+        }
+        for (int row = 0; row < H; ++row) {
+            host_down[expert * H + row].scale = scales[expert];
+            std::memset(host_down[expert * H + row].values, 0x99, 16);
+        }
+    }
+    auto* gate = device_copy(host_gate.data(), host_gate.size());
+    auto* down = device_copy(host_down.data(), host_down.size());
+    const float input_sum = 16.5f;
+    const float gate2 = input_sum, gate1 = input_sum * 0.5f;
+    const float hidden2 = silu(gate2) * gate2, hidden1 = silu(gate1) * gate1;
+    const float routing[TOP_K] = {0.75f, 0.25f};
+    const float expected = routing[0] * I * hidden2 + routing[1] * 0.5f * I * hidden1;
+    const qwen3x_hip::ExpertLinear gu{gate, EXPERTS, 2 * I, H, qwen3x_hip::MATRIX_Q4_0};
+    const qwen3x_hip::ExpertLinear dn{down, EXPERTS, H, I, qwen3x_hip::MATRIX_Q4_0};
+    for (int tokens : {1, 3}) {
+        std::vector<float> input(tokens * H);
+        std::vector<int> ids(tokens * TOP_K);
+        std::vector<float> weights(tokens * TOP_K);
+        for (int t = 0; t < tokens; ++t) {
+            for (int i = 0; i < H; ++i) input[t * H + i] = 0.03125f * (i + 1);
+            ids[t * TOP_K] = 2; ids[t * TOP_K + 1] = 1;
+            weights[t * TOP_K] = routing[0]; weights[t * TOP_K + 1] = routing[1];
+        }
+        auto* device_input = device_copy(input.data(), input.size());
+        auto* device_ids = device_copy(ids.data(), ids.size());
+        auto* device_weights = device_copy(weights.data(), weights.size());
+        float* output = device_floats(tokens * H);
+        const size_t ws_bytes = qwen3x_hip::moe_workspace_bytes(tokens, EXPERTS, TOP_K, H, I);
+        void* ws = nullptr;
+        HIP_OK(hipMalloc(&ws, ws_bytes));
+        qwen3x_hip::moe_routed(gu, dn, device_input, tokens, device_ids, device_weights, TOP_K, output, false,
+                               ws, ws_bytes, nullptr);
+        const auto actual = host_copy(output, tokens * H);
+        for (float v : actual) {
+            CHECK(std::isfinite(v));
+            CHECK(std::abs(v - expected) < 1e-2f);
+        }
+        HIP_OK(hipFree(device_input)); HIP_OK(hipFree(device_ids)); HIP_OK(hipFree(device_weights));
+        HIP_OK(hipFree(output)); HIP_OK(hipFree(ws));
+    }
+    HIP_OK(hipFree(gate)); HIP_OK(hipFree(down));
+}
+
+}  // namespace
+
+int main() {
+    int devices = 0;
+    if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0) {
+        std::puts("q3x-hip-host-test: skipped (no GPU)");
+        return 77;
+    }
+    q4_mv_test();
+    q8_fixed_test();
+    q4_math_test();
+    router_test();
+    expert_moe_test();
+    HIP_OK(hipDeviceSynchronize());
+    std::puts("q3x-hip-host-test: ok");
+    return 0;
+}

@@ -1,0 +1,334 @@
+"""GPU parity tests: the HIP library (through its C ABI) against the CPU oracle on
+the same seeded inputs.
+
+Bar (north star): dequantised weights bit-exact; outputs within
+max|delta| <= 1e-5 * ||w_row||_2 * ||x||_2 per element (norms in double),
+because only the FP32 summation order may differ.  Index work (router ids,
+grouping) is exact."""
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+import qwen3x_amd as q3x
+from tests.helpers import Q4_0, Q8_0, bits, dequant_numpy, random_blocks, row_bound
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def _torch():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need cuda:0"
+    return torch
+
+
+def dev(a):
+    torch = _torch()
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def host(t):
+    _torch().cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def check_bound(got, want, wd, x, label):
+    bound = row_bound(wd, x, TOL)
+    diff = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    bad = diff > bound
+    assert np.all(np.isfinite(got)), label
+    assert not bad.any(), f"{label}: {bad.sum()} outside bound; worst {diff[bad].max()} vs {bound[bad].min()}"
+
+
+# ----------------------------------------------------------- host binary ----
+
+def test_reference_unit_cases_through_cpp_host_interface(repo_root):
+    exe = os.path.join(repo_root, "qwen3x_amd", "q3x_hip_host_test")
+    say(f"running {exe}")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "q3x-hip-host-test: ok" in r.stdout
+
+
+# --------------------------------------------------------------- dequant ----
+
+SPECIAL = np.array([0x3555, 0x2E66, 0x0400, 0x0001, 0x8001, 0x03FF, 0x7BFF, 0xFBFF, 0x0000, 0x8000], np.uint16)
+
+
+@pytest.mark.parametrize("type_", [Q8_0, Q4_0])
+@pytest.mark.parametrize("rows,cols,special", [(2, 64, False), (37, 96, True), (256, 4096, False),
+                                               (64, 5120, True)])
+def test_dequant_bit_exact(type_, rows, cols, special):
+    torch = _torch()
+    rng = np.random.default_rng(rows + cols + type_)
+    w = random_blocks(rng, type_, rows, cols, SPECIAL if special else None)
+    want = oracle.dequant(w, type_, rows, cols)
+    out = torch.empty((rows, cols), dtype=torch.float32, device="cuda:0")
+    say(f"dequant type={type_} {rows}x{cols}")
+    q3x.dequant(q3x.Linear(dev(w), rows, cols, type_), 0, rows, out)
+    got = host(out)
+    assert np.array_equal(bits(got), bits(want))
+    # a window of the last rows
+    n = min(3, rows)
+    part = torch.empty((n, cols), dtype=torch.float32, device="cuda:0")
+    q3x.dequant(q3x.Linear(dev(w), rows, cols, type_), rows - n, n, part)
+    assert np.array_equal(bits(host(part)), bits(want[rows - n:]))
+
+
+def test_dequant_all_fp16_scales_bit_exact():
+    # Every one of the 65536 scale patterns, finite ones bit for bit, NaN as NaN.
+    torch = _torch()
+    scales = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    vals = np.tile(np.arange(-16, 16, dtype=np.int64), (65536, 1))
+    from tests.helpers import q8_blocks
+    w = q8_blocks(scales, vals)
+    rows, cols = 2048, 1024
+    want = oracle.dequant(w, Q8_0, rows, cols)
+    out = torch.empty((rows, cols), dtype=torch.float32, device="cuda:0")
+    q3x.dequant(q3x.Linear(dev(w), rows, cols, Q8_0), 0, rows, out)
+    got = host(out)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(bits(got)[~nan], bits(want)[~nan])
+
+
+# -------------------------------------------------------------------- mv ----
+
+MV_SHAPES = [
+    (1, 32), (2, 64), (3, 96), (5, 160),           # generic path (rows not 256-col multiples)
+    (7, 256), (33, 512),                           # 16 lanes per row
+    (65, 1024),                                    # 32 lanes per row
+    (100, 2048), (1000, 4096), (5, 12288),         # 64 lanes per row, passes
+    (17, 5120), (3, 17408), (129, 2304),           # partial last pass
+]
+
+
+@pytest.mark.parametrize("type_", [Q8_0, Q4_0])
+@pytest.mark.parametrize("rows,cols", MV_SHAPES)
+def test_mv_parity(type_, rows, cols):
+    torch = _torch()
+    rng = np.random.default_rng(rows * 31 + cols + type_)
+    w = random_blocks(rng, type_, rows, cols)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    want = oracle.mv(w, type_, rows, cols, x)
+    wd = dequant_numpy(w, type_, rows, cols)
+    lin = q3x.Linear(dev(w), rows, cols, type_)
+    y = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda:0")
+    say(f"mv type={type_} {rows}x{cols}")
+    q3x.mv(lin, dev(x), y)
+    got = host(y)
+    check_bound(got, want, wd, x, f"mv {rows}x{cols}")
+    # accumulate: y += W x
+    q3x.mv_add(lin, dev(x), y)
+    check_bound(host(y), 2 * want, wd, 2 * x, f"mv_add {rows}x{cols}")
+    # deterministic: identical bits on a second run
+    y2 = torch.empty_like(y)
+    q3x.mv(lin, dev(x), y2)
+    assert np.array_equal(bits(host(y2)), bits(got))
+
+
+@pytest.mark.parametrize("type_", [Q8_0, Q4_0])
+def test_mv_unaligned_pointers_take_the_generic_path(type_):
+    torch = _torch()
+    rows, cols = 40, 4096
+    rng = np.random.default_rng(17)
+    w = random_blocks(rng, type_, rows, cols)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    want = oracle.mv(w, type_, rows, cols, x)
+    wd = dequant_numpy(w, type_, rows, cols)
+    wbuf = torch.zeros(w.size + 16, dtype=torch.uint8, device="cuda:0")
+    wbuf[2:2 + w.size] = dev(w)
+    xbuf = torch.zeros(cols + 1, dtype=torch.float32, device="cuda:0")
+    xbuf[1:] = dev(x)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda:0")
+    q3x.mv(q3x.Linear(wbuf[2:], rows, cols, type_), xbuf[1:], y)
+    check_bound(host(y), want, wd, x, "unaligned mv")
+
+
+@pytest.mark.parametrize("type_,rows,cols", [(Q8_0, 70000, 2048), (Q4_0, 70000, 2048), (Q8_0, 20000, 768),
+                                             (Q4_0, 300000, 256)])
+def test_mv_many_rows_multi_row_waves(type_, rows, cols):
+    # Row counts that select 2 and 4 row iterations per wavefront.
+    torch = _torch()
+    rng = np.random.default_rng(rows + cols)
+    w = random_blocks(rng, type_, rows, cols)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    want = oracle.mv(w, type_, rows, cols, x)
+    wd = dequant_numpy(w, type_, rows, cols)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda:0")
+    say(f"mv many rows type={type_} {rows}x{cols}")
+    q3x.mv(q3x.Linear(dev(w), rows, cols, type_), dev(x), y)
+    check_bound(host(y), want, wd, x, f"mv {rows}x{cols}")
+
+
+def test_mv_zero_rows_are_exactly_zero():
+    # ||w_row|| = 0 allows no error at all: zero scales and all-0x88 Q4 blocks.
+    torch = _torch()
+    rows, cols = 8, 4096
+    rng = np.random.default_rng(2)
+    x = dev(rng.normal(0, 1, cols).astype(np.float32))
+    from tests.helpers import q4_blocks, q8_blocks
+    nb = rows * cols // 32
+    for type_, w in ((Q8_0, q8_blocks(np.zeros(nb), rng.integers(-128, 128, (nb, 32)))),
+                     (Q4_0, q4_blocks(np.full(nb, 0x3C00), np.full((nb, 16), 0x88)))):
+        y = torch.full((rows,), 7.0, dtype=torch.float32, device="cuda:0")
+        q3x.mv(q3x.Linear(dev(w), rows, cols, type_), x, y)
+        assert np.all(host(y) == 0.0)
+
+
+# ------------------------------------------------------------------ GEMM ----
+
+GEMM_CASES = [(Q8_0, 64, 128, 1), (Q8_0, 130, 256, 5), (Q8_0, 300, 512, 129), (Q4_0, 256, 1024, 37),
+              (Q4_0, 129, 4096, 300), (Q8_0, 1000, 2048, 128), (Q4_0, 77, 96, 3), (Q8_0, 3, 64, 200),
+              # 128x128-tile path (>= 512 workgroups), partial tiles on both edges
+              (Q8_0, 4096, 512, 2048), (Q4_0, 4000, 256, 2100)]
+
+
+@pytest.mark.parametrize("type_,rows,cols,count", GEMM_CASES)
+def test_gemm_parity(type_, rows, cols, count):
+    torch = _torch()
+    rng = np.random.default_rng(rows + cols + count + type_)
+    w = random_blocks(rng, type_, rows, cols)
+    X = rng.normal(0, 1, (count, cols)).astype(np.float32)
+    want = oracle.gemm(w, type_, rows, cols, X)
+    wd = dequant_numpy(w, type_, rows, cols)
+    lin = q3x.Linear(dev(w), rows, cols, type_)
+    Y = torch.full((count, rows), float("nan"), dtype=torch.float32, device="cuda:0")
+    say(f"gemm type={type_} {rows}x{cols} count={count}")
+    q3x.batch_mv(lin, dev(X), Y, count)
+    got = host(Y)
+    check_bound(got, want, wd, X, f"gemm {rows}x{cols}x{count}")
+    q3x.batch_mv(lin, dev(X), Y, count, add=True)
+    check_bound(host(Y), 2 * want, wd, 2 * X, "gemm add")
+
+
+# ---------------------------------------------------------------- router ----
+
+@pytest.mark.parametrize("tokens,experts,top_k", [(1, 256, 8), (2048, 256, 8), (37, 6, 3), (100, 1024, 8),
+                                                  (5, 64, 1)])
+def test_router_parity(tokens, experts, top_k):
+    torch = _torch()
+    rng = np.random.default_rng(tokens + experts)
+    logits = rng.normal(0, 1, (tokens, experts)).astype(np.float32)
+    logits[::7, 3] = logits[::7, 5]  # exact ties
+    ids_o, w_o, probs_o = oracle.router_top_k(logits, top_k)
+    ids = torch.empty((tokens, top_k), dtype=torch.int32, device="cuda:0")
+    w = torch.empty((tokens, top_k), dtype=torch.float32, device="cuda:0")
+    q3x.router_top_k(dev(logits), tokens, experts, top_k, ids, w)
+    ids_g, w_g = host(ids), host(w)
+    for t in range(tokens):
+        if not np.array_equal(ids_g[t], ids_o[t]):
+            # Only a near-tie (probabilities within a few ulp) may reorder.
+            p = probs_o[t]
+            for a, b in zip(ids_g[t], ids_o[t]):
+                if a != b:
+                    assert abs(p[a] - p[b]) <= 4 * np.spacing(np.float32(max(p[a], p[b]))), (t, a, b)
+        else:
+            assert np.allclose(w_g[t], w_o[t], rtol=2e-6, atol=0), t
+    assert np.allclose(w_g.sum(1), 1.0, atol=1e-6)
+
+
+# ------------------------------------------------------------------- MoE ----
+
+def moe_bound(gu, dn, type_, E, H, I, X, ids, wts):
+    """Per-element bound for the routed sum: each slot's down product within
+    TOL * ||down_row|| * ||h||, plus the first-order effect of the gate/up
+    products' own TOL * ||row|| * ||x|| errors on h (double precision)."""
+    gdq = dequant_numpy(gu, type_, E * 2 * I, H).reshape(E, 2 * I, H)
+    ddq = dequant_numpy(dn, type_, E * H, I).reshape(E, H, I)
+    T, k = ids.shape
+    Xd = X.astype(np.float64)
+    xn = np.linalg.norm(Xd, axis=1)
+    coef = np.zeros((T, k))                      # TOL*||h|| + ||dh|| per (token, slot)
+    for e in np.unique(ids):
+        if e < 0 or e >= E:
+            continue
+        ts, ss = np.nonzero(ids == e)
+        G = gdq[e].astype(np.float64)
+        gu_v = Xd[ts] @ G.T
+        g, u = gu_v[:, :I], gu_v[:, I:]
+        sig = 1 / (1 + np.exp(-g))
+        h = g * sig * u
+        dg = TOL * np.linalg.norm(G[:I], axis=1)[None, :] * xn[ts, None]
+        du = TOL * np.linalg.norm(G[I:], axis=1)[None, :] * xn[ts, None]
+        dsilu = sig * (1 + g * (1 - sig))
+        dh = np.abs(dsilu * u) * dg + np.abs(g * sig) * du + 1e-6 * np.abs(h)
+        coef[ts, ss] = TOL * np.linalg.norm(h, axis=1) + np.linalg.norm(dh, axis=1)
+    rown = np.linalg.norm(ddq.astype(np.float64), axis=2)          # [E, H]
+    valid = (ids >= 0) & (ids < E)
+    safe = np.where(valid, ids, 0)
+    contrib = (np.abs(wts) * coef * valid)[:, :, None] * rown[safe]  # [T, k, H]
+    return contrib.sum(axis=1)
+
+
+@pytest.mark.parametrize("type_,E,H,I,top_k,tokens", [
+    (Q4_0, 4, 32, 32, 2, 1), (Q4_0, 4, 32, 32, 2, 3), (Q4_0, 16, 256, 64, 4, 1), (Q4_0, 16, 256, 64, 4, 50),
+    (Q8_0, 8, 512, 256, 2, 1), (Q8_0, 8, 512, 256, 2, 70), (Q4_0, 64, 2048, 512, 8, 1),
+    (Q4_0, 64, 2048, 512, 8, 40)])
+def test_moe_routed_parity(type_, E, H, I, top_k, tokens):
+    torch = _torch()
+    rng = np.random.default_rng(E + H + I + tokens)
+    gu = random_blocks(rng, type_, E * 2 * I, H)
+    dn = random_blocks(rng, type_, E * H, I)
+    X = rng.normal(0, 1, (tokens, H)).astype(np.float32)
+    ids = np.stack([rng.choice(E, top_k, replace=False) for _ in range(tokens)]).astype(np.int32)
+    wts = rng.random((tokens, top_k)).astype(np.float32)
+    wts /= wts.sum(1, keepdims=True)
+    want = oracle.moe_routed(gu, dn, type_, E, H, I, X, ids, wts)
+    Y = torch.full((tokens, H), float("nan"), dtype=torch.float32, device="cuda:0")
+    say(f"moe type={type_} E={E} H={H} I={I} k={top_k} tokens={tokens}")
+    q3x.moe_routed(q3x.ExpertLinear(dev(gu), E, 2 * I, H, type_), q3x.ExpertLinear(dev(dn), E, H, I, type_),
+                   dev(X), tokens, dev(ids), dev(wts), top_k, Y)
+    got = host(Y)
+    bound = moe_bound(gu, dn, type_, E, H, I, X, ids, wts)
+    diff = np.abs(got.astype(np.float64) - want)
+    assert np.all(np.isfinite(got))
+    assert np.all(diff <= bound), f"{(diff > bound).sum()} outside; worst {diff.max()}"
+    # accumulate
+    q3x.moe_routed(q3x.ExpertLinear(dev(gu), E, 2 * I, H, type_), q3x.ExpertLinear(dev(dn), E, H, I, type_),
+                   dev(X), tokens, dev(ids), dev(wts), top_k, Y, accumulate=True)
+    assert np.all(np.abs(host(Y).astype(np.float64) - 2 * want) <= 2 * bound)
+
+
+def test_moe_invalid_ids_contribute_nothing():
+    torch = _torch()
+    E, H, I, k = 4, 256, 64, 3
+    rng = np.random.default_rng(99)
+    gu = random_blocks(rng, Q4_0, E * 2 * I, H)
+    dn = random_blocks(rng, Q4_0, E * H, I)
+    for tokens in (1, 6):
+        X = rng.normal(0, 1, (tokens, H)).astype(np.float32)
+        ids = np.tile(np.array([2, -1, 7], np.int32), (tokens, 1))
+        wts = np.tile(np.array([0.5, 0.3, 0.2], np.float32), (tokens, 1))
+        want = oracle.moe_routed(gu, dn, Q4_0, E, H, I, X, ids[:, :1], wts[:, :1])
+        Y = torch.empty((tokens, H), dtype=torch.float32, device="cuda:0")
+        q3x.moe_routed(q3x.ExpertLinear(dev(gu), E, 2 * I, H, Q4_0), q3x.ExpertLinear(dev(dn), E, H, I, Q4_0),
+                       dev(X), tokens, dev(ids), dev(wts), k, Y)
+        bound = moe_bound(gu, dn, Q4_0, E, H, I, X, ids[:, :1], wts[:, :1])
+        assert np.all(np.abs(host(Y) - want) <= bound)
+
+
+# -------------------------------------------------------------- quantize ----
+
+@pytest.mark.parametrize("type_", [Q8_0, Q4_0])
+def test_quantize_bit_exact(type_):
+    torch = _torch()
+    rng = np.random.default_rng(type_)
+    vals = rng.normal(0, 0.02, (512, 4096)).astype(np.float32)
+    vals[0, :32] = 0
+    vals[1, :32] = [127.0, -127.0, 126.5, -126.5, 0.5, -0.5] + [0.0] * 26
+    vals[2, :32] = np.linspace(-8, 7.5, 32)
+    vals[3, :32] = 1e-30
+    vals[4, :32] *= 1e4
+    want = oracle.quantize(type_, vals)
+    out = torch.empty(want.size, dtype=torch.uint8, device="cuda:0")
+    q3x.quantize(type_, dev(vals), 512, 4096, out)
+    assert np.array_equal(host(out), want)

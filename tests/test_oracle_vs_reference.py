@@ -1,0 +1,104 @@
+"""The oracle against the reference's own CPU code (oracle/_ref, compiled from
+the reference sources where they lie), bit for bit.  Skipped where the
+reference tree was not available to build it; tests/golden/ carries vectors
+from the same build for those hosts."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.helpers import Q4_0, Q8_0, bits, random_blocks
+
+ref = oracle.ref()
+pytestmark = pytest.mark.skipif(ref is None, reason="oracle/_ref not built (no reference tree)")
+
+
+def _p(a):
+    return a.ctypes.data
+
+
+def ref_mv(w, type_, rows, cols, x):
+    y = np.empty(rows, np.float32)
+    assert ref.q3xr_try_mv(_p(w), type_, rows, cols, _p(x), _p(y)) == 1
+    return y
+
+
+def ref_embed(w, type_, cols, row):
+    out = np.empty(cols, np.float32)
+    assert ref.q3xr_try_embed(_p(w), type_, cols, row, _p(out)) == 1
+    return out
+
+
+SPECIAL_SCALES = np.array([0x3555, 0x2E66, 0x0400, 0x0001, 0x8001, 0x03FF, 0x7BFF, 0xFBFF, 0x0000, 0x8000,
+                           0x3C00, 0xB800], np.uint16)
+
+
+@pytest.mark.parametrize("type_", [Q8_0, Q4_0])
+@pytest.mark.parametrize("rows,cols", [(1, 32), (3, 64), (17, 96), (64, 256), (33, 4096), (5, 12288)])
+@pytest.mark.parametrize("special", [False, True])
+def test_mv_and_embed_bit_exact(type_, rows, cols, special):
+    rng = np.random.default_rng(rows * 7919 + cols + type_ + 1000 * special)
+    w = random_blocks(rng, type_, rows, cols, SPECIAL_SCALES if special else None)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    assert np.array_equal(bits(oracle.mv_serial(w, type_, rows, cols, x)), bits(ref_mv(w, type_, rows, cols, x)))
+    for row in {0, rows // 2, rows - 1}:
+        assert np.array_equal(bits(oracle.embed(w, type_, cols, row)), bits(ref_embed(w, type_, cols, row)))
+
+
+def test_quantized_bytes_agree():
+    for t in (0, Q8_0, Q4_0, 7):
+        for rows, cols in [(3, 64), (0, 32), (1, -32), (1, 33), (1, 16), (4096, 4096), (151936, 4096),
+                           (2147483647, 2147483616)]:
+            a = ctypes.c_size_t(123)
+            ok = ref.q3xr_quantized_bytes(t, rows, cols, ctypes.byref(a))
+            mine = oracle.quantized_bytes(t, rows, cols)
+            assert (mine is not None) == bool(ok)
+            if ok:
+                assert mine == a.value
+
+
+@pytest.mark.parametrize("experts,top_k", [(6, 3), (256, 8), (64, 1), (256, 2)])
+def test_router_bit_exact(experts, top_k):
+    rng = np.random.default_rng(experts * 31 + top_k)
+    for t in range(50):
+        logits = rng.normal(0, 1 + 3 * (t % 3), experts).astype(np.float32)
+        if t % 5 == 0:
+            logits[rng.integers(0, experts, 4)] = logits.max()  # exact ties
+        ids_r = np.zeros(top_k, np.int32)
+        probs_r = np.zeros(experts, np.float32)
+        ref.q3xr_router_top_k(_p(logits), experts, top_k, _p(ids_r), _p(probs_r))
+        ids, weights, _ = oracle.router_top_k(logits, top_k)
+        assert np.array_equal(ids[0], ids_r)
+        assert np.array_equal(bits(weights[0]), bits(probs_r[ids_r]))
+
+
+def test_silu_sigmoid_bit_exact():
+    rng = np.random.default_rng(9)
+    values = np.concatenate([rng.normal(0, 6, 2000), [0.0, -0.0, 88.0, -88.0, 1e-30, -1e-30, 20.0]])
+    for v in values.astype(np.float32):
+        assert np.float32(ref.q3xr_sigmoid(float(v))).view(np.uint32) == np.float32(oracle.sigmoid(float(v))).view(np.uint32)
+        assert np.float32(ref.q3xr_silu(float(v))).view(np.uint32) == np.float32(oracle.silu(float(v))).view(np.uint32)
+
+
+@pytest.mark.parametrize("experts,H,I,top_k", [(8, 64, 32, 2), (16, 256, 64, 8), (256, 2048, 512, 8)])
+def test_moe_routed_bit_exact_against_reference_moe(experts, H, I, top_k):
+    # The reference moe() (engine.cpp:406-430) with a BF16 router and an
+    # all-zero shared expert, against this oracle's router + routed loop fed
+    # the reference's router logits.
+    rng = np.random.default_rng(experts + H + I)
+    router = (rng.normal(0, 0.5, (experts, H)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    gate_up = random_blocks(rng, Q4_0, experts * 2 * I, H)
+    down = random_blocks(rng, Q4_0, experts * H, I)
+    for t in range(3 if experts < 256 else 1):
+        x = rng.normal(0, 1, H).astype(np.float32)
+        logits = np.zeros(experts, np.float32)
+        ids_r = np.zeros(top_k, np.int32)
+        out_r = np.zeros(H, np.float32)
+        ref.q3xr_moe_q4(_p(router), _p(gate_up), _p(down), experts, H, I, top_k, _p(x), _p(logits), _p(ids_r),
+                        _p(out_r))
+        ids, weights, _ = oracle.router_top_k(logits, top_k)
+        assert np.array_equal(ids[0], ids_r)
+        y = oracle.moe_routed(gate_up, down, Q4_0, experts, H, I, x, ids, weights, threads=1)
+        # shared expert adds sigmoid(0) * 0: -0.0 becomes +0.0, nothing else changes
+        assert np.array_equal(bits(y[0] + np.float32(0.0)), bits(out_r))
