@@ -1,0 +1,101 @@
+"""CPU tests of the C ABI: the library loads, exports every entry point
+include/q3x_hip.h declares, and rejects invalid arguments before touching the
+device (so these calls need no GPU)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import oracle
+import qwen3x_amd as q3x
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "q3x_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w[\w\s\*]*?\b(q3x_hip_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    assert names == sorted(q3x.SIGNATURES), names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = q3x.lib()
+    out = subprocess.run(["nm", "-D", "--defined-only", q3x.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (q3x_hip_\w+)", out))
+    for name in declared_functions():
+        assert name in exported, name
+        assert getattr(lib, name) is not None
+
+
+def test_strerror():
+    assert q3x.strerror(q3x.OK) == "ok"
+    assert "invalid" in q3x.strerror(q3x.EINVAL)
+    assert q3x.strerror(q3x.ENOTSUP)
+    assert q3x.strerror(12345) == "unknown error"
+
+
+def test_quantized_bytes_match_the_oracle_rules():
+    cases = [(0, 3, 17), (1, 3, 64), (2, 3, 64), (1, 0, 32), (2, 1, -32), (1, 1, 33), (2, 1, 16), (999, 1, 32),
+             (1, 151936, 4096), (2, 17408, 5120), (1, 2147483647, 2147483616)]
+    for t, r, c in cases:
+        assert q3x.quantized_bytes(t, r, c) == oracle.quantized_bytes(t, r, c), (t, r, c)
+    out = ctypes.c_size_t(123)
+    assert q3x.lib().q3x_hip_quantized_bytes(1, 3, 64, None) == q3x.EINVAL
+    assert q3x.lib().q3x_hip_quantized_bytes(1, 1, 33, ctypes.byref(out)) == q3x.EINVAL
+    assert out.value == 123  # untouched on rejection
+
+
+def test_invalid_arguments_are_rejected_without_device_work():
+    lib = q3x.lib()
+    P = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    N = None
+    assert lib.q3x_hip_mv(N, 1, 4, 64, P, P, 0, N) == q3x.EINVAL
+    assert lib.q3x_hip_mv(P, 1, 4, 64, N, P, 0, N) == q3x.EINVAL
+    assert lib.q3x_hip_mv(P, 1, 4, 64, P, N, 0, N) == q3x.EINVAL
+    assert lib.q3x_hip_mv(P, 1, 0, 64, P, P, 0, N) == q3x.EINVAL
+    assert lib.q3x_hip_mv(P, 1, 4, 48, P, P, 0, N) == q3x.EINVAL
+    assert lib.q3x_hip_mv(P, 7, 4, 64, P, P, 0, N) == q3x.EINVAL
+    assert lib.q3x_hip_mv(P, 0, 4, 64, P, P, 0, N) == q3x.ENOTSUP   # BF16: caller's own path
+    assert lib.q3x_hip_gemm(P, 1, 4, 64, P, 0, P, 0, N) == q3x.EINVAL
+    assert lib.q3x_hip_gemm(P, 2, 4, 40, P, 3, P, 0, N) == q3x.EINVAL
+    assert lib.q3x_hip_gemm(P, 0, 4, 64, P, 3, P, 0, N) == q3x.ENOTSUP
+    assert lib.q3x_hip_dequant(P, 1, 64, -1, 1, P, N) == q3x.EINVAL
+    assert lib.q3x_hip_dequant(P, 2, 64, 0, 0, P, N) == q3x.EINVAL
+    assert lib.q3x_hip_router_topk(P, 1, 256, 9, P, P, N) == q3x.EINVAL       # top_k > 8
+    assert lib.q3x_hip_router_topk(P, 1, 4, 5, P, P, N) == q3x.EINVAL         # top_k > experts
+    assert lib.q3x_hip_router_topk(P, 1, 2048, 8, P, P, N) == q3x.EINVAL      # experts > 1024
+    assert lib.q3x_hip_router_topk(P, 0, 256, 8, P, P, N) == q3x.EINVAL
+    ws = lib.q3x_hip_moe_workspace_bytes(2048, 256, 8, 2048, 512)
+    assert lib.q3x_hip_moe_routed(P, P, 2, 256, 2048, 512, P, 2048, P, P, 8, P, 0, P, ws - 1, N) == q3x.EINVAL
+    assert lib.q3x_hip_moe_routed(P, P, 2, 256, 2048, 500, P, 2048, P, P, 8, P, 0, P, ws, N) == q3x.EINVAL
+    assert lib.q3x_hip_moe_routed(P, P, 2, 4, 2048, 512, P, 1, P, P, 5, P, 0, P, ws, N) == q3x.EINVAL
+    assert lib.q3x_hip_moe_routed(P, P, 0, 4, 2048, 512, P, 1, P, P, 2, P, 0, P, ws, N) == q3x.ENOTSUP
+    assert lib.q3x_hip_quantize(1, N, 4, 64, P, N) == q3x.EINVAL
+    assert lib.q3x_hip_quantize(2, P, 4, 48, P, N) == q3x.EINVAL
+
+
+def test_moe_workspace_sizes():
+    decode = q3x.moe_workspace_bytes(1, 256, 8, 2048, 512)
+    assert decode >= 4 * 8 * (2 * 512 + 512 + 2048)
+    prefill = q3x.moe_workspace_bytes(2048, 256, 8, 2048, 512)
+    pairs = 2048 * 8
+    assert prefill >= 4 * pairs * (2 * 512 + 512 + 2048) + 4 * 2 * pairs
+    assert q3x.moe_workspace_bytes(0, 256, 8, 2048, 512) == 0
+
+
+def test_cpp_host_interface_binary_skips_without_gpu():
+    exe = os.path.join(ROOT, "qwen3x_amd", "q3x_hip_host_test")
+    assert os.path.exists(exe), "build it with make -C qwen3x_amd"
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("GPU present: the binary runs in the GPU suite")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 77, r.stdout + r.stderr

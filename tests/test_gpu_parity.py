@@ -332,3 +332,15 @@ def test_quantize_bit_exact(type_):
     out = torch.empty(want.size, dtype=torch.uint8, device="cuda:0")
     q3x.quantize(type_, dev(vals), 512, 4096, out)
     assert np.array_equal(host(out), want)
+
+
+@pytest.mark.parametrize("type_,key", [(Q8_0, "q8_0"), (Q4_0, "q4_0")])
+def test_quantize_matches_reference_packer_fixture(type_, key):
+    torch = _torch()
+    f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "quantizer.npz"),
+                allow_pickle=False)
+    vals = (f["bf16"].astype(np.uint32) << 16).view(np.float32)
+    say(f"quantize fixture type={type_} blocks={vals.size // 32}")
+    out = torch.empty(f[key].size, dtype=torch.uint8, device="cuda:0")
+    q3x.quantize(type_, dev(vals), vals.size // 32, 32, out)
+    assert np.array_equal(host(out), f[key])
