@@ -5,24 +5,27 @@
 // mv_add_q4_kernel (arch/cuda/engine.cu:546-612), which give one 256-thread
 // block to each row and decode the fp16 scale per element.  Here:
 //
-//  * a wavefront owns G*RPI rows (G row groups of LPR lanes, RPI row
-//    iterations); one lane owns one 32-weight block column of a pass, so its 32
-//    activations stay in registers for all of the wave's rows;
-//  * each pass stages the wave's row segments (LPR blocks per row) into the
-//    wave's own LDS slice with coalesced 16-byte global loads.  Q8_0 rows of
-//    8 blocks are 272 B = 17 x 16 B and Q4_0 rows 144 B = 9 x 16 B, so any
-//    row whose length is a multiple of 256 columns starts 16-byte aligned;
-//  * a lane reads its block back with aligned dword LDS reads and one
-//    v_alignbyte per dword (blocks are 34 / 18 bytes, so they start on 2- or
-//    4-byte boundaries), converts bytes with sign-extending SDWA converts and
-//    accumulates in FP32 with FMAs: inner = sum q*x per block, then
-//    acc += f16(d) * inner, the per-block factorisation of arch/cpu.cpp:64-73;
-//  * Q4_0 nibbles become signed bytes 16*(n-8) with two logic ops per four
-//    bytes (xor 0x88, mask / shift), so each weight costs one convert and one
-//    FMA; the factor 16 is removed exactly by scaling d by 1/16;
+//  * one lane owns one 32-weight block column of a pass of LPR blocks, so its
+//    32 activations stay in registers for all the rows the wave streams;
+//  * row segments arrive with coalesced 16-byte buffer loads and go through
+//    the wave's LDS slice, where each lane reads its own block back with
+//    aligned dword reads and one v_alignbyte per dword (blocks are 34 / 18
+//    bytes, so they start on 2- or 4-byte boundaries).  Q8_0 rows of 8 blocks
+//    are 272 B = 17 x 16 B and Q4_0 rows 144 B = 9 x 16 B, so any row whose
+//    length is a multiple of 256 columns starts 16-byte aligned;
+//  * Q8_0 bytes convert with sign-extending SDWA converts and accumulate in
+//    FP32 with FMAs: inner = sum q*x per block, then acc += f16(d) * inner,
+//    the per-block factorisation of arch/cpu.cpp:64-73;
+//  * Q4_0 nibbles become exact binary16 subnormals that v_fma_mix_f32 takes
+//    directly (block_dot_q4_mix), or signed bytes 16*(n-8) for the SDWA path
+//    (block_dot_q4);
 //  * the row's lane partial sums are combined with a butterfly inside the
 //    row group; lane 0 of the group writes (or adds to) y.
-// Reduction order is fixed per shape, so results are deterministic.
+// mv_pipe_kernel (x shared by all rows, held in LDS) prefetches the next
+// step's weights into registers while the current step computes;
+// mv_stream_kernel (x per row group, e.g. per expert slot) stages weights
+// with direct-to-LDS loads.  Reduction order is fixed per shape, so results
+// are deterministic.
 #pragma once
 
 #include "common.h"
@@ -86,22 +89,25 @@ __device__ __forceinline__ float block_dot_q4(const uint8_t* lds, uint32_t p, co
     return (f16_fast(scale) * 0.0625f) * (lo_sum + hi_sum);
 }
 
-// Streaming kernel.  QT: matrix type; LPR: lanes (= block columns) per row
-// group, 16/32/64; R: row iterations per batch.  A unit of work is a batch
-// of RW = G*R rows (G = 64/LPR row groups) times one K pass of LPR blocks;
-// lane li of row group g owns block column b0 + li of the pass, so its 32
-// activations serve all R rows.  The grid is persistent (sized to what is
-// resident at once, GW wavefronts) and each wave accumulates a batch's rows
-// over all passes before storing them.
-//
-// Rows and activations: with XL every row reads the same x, which the
-// workgroup copies once into LDS (padded 16 bytes per two blocks, so the 64
-// lanes' 16-byte reads of consecutive blocks hit distinct banks), and wave
-// gw takes the strided rows gw, gw + GW, gw + 2*GW, ...: every wave streams
-// the same number of rows (+-1) whatever the row count, and at any moment
-// the GPU reads one band of consecutive rows.  Without XL (inputs that change
-// between groups of rows, e.g. per expert slot) a batch is RW consecutive
-// rows and each unit reads its x slice from global memory.
+constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9)
+constexpr int kNonTemporal = 2;           // buffer "nt" cache policy
+
+// LDS offset of x block b in the padded layout: 16 spare bytes after every
+// two 128-byte blocks, so the 16-byte reads of 16 consecutive blocks start in
+// 16 distinct bank groups.
+__host__ __device__ constexpr uint32_t x_block_offset(int b) { return 128u * b + 16u * (b >> 1); }
+__host__ __device__ constexpr uint32_t x_lds_bytes(int bpr) { return x_block_offset(bpr) + 16u; }
+
+// Streaming kernel for rows whose input changes between row groups (the
+// down projections of routed experts, one input per slot), and for inputs
+// too long for LDS.  QT: matrix type; LPR: lanes (= block columns) per row
+// group, 16/32/64; R: row iterations per batch.  A unit of work is a tile of
+// RW = G*R consecutive rows (G = 64/LPR row groups) times one K pass of LPR
+// blocks; lane li of row group g owns block column b0 + li of the pass and
+// reads its 32 activations from global memory, so they serve all R rows.
+// The grid is persistent (sized to what is resident at once, GW wavefronts,
+// which take tiles round-robin); a wave accumulates a tile over all passes
+// before storing it.
 //
 // Weights: each row segment of a unit (LPR blocks = SEG bytes) is copied
 // global -> LDS by direct-to-LDS buffer loads (non-temporal: weights are used
@@ -113,16 +119,13 @@ __device__ __forceinline__ float block_dot_q4(const uint8_t* lds, uint32_t p, co
 // one.  The wave waits for its loads, then reads its blocks back with aligned
 // dword reads (block_dot_q8 / block_dot_q4).  Latency is hidden by the other
 // resident wavefronts.
-// Requires: every row start 16-byte aligned, bpr % 8 == 0, bpr <= LPR when
-// LPR < 64, x 16-byte aligned; rows of a batch read one input.
-constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9)
-constexpr int kNonTemporal = 2;           // buffer "nt" cache policy
-
+// Requires: every row start 16-byte aligned, bpr % 8 == 0, x 16-byte aligned;
+// the rows of a tile read one input.
 template <uint32_t QT, int LPR, int R>
 struct StagedShape {
     static constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
     static constexpr int G = kWave / LPR;
-    static constexpr int RW = G * R;                      // rows per batch
+    static constexpr int RW = G * R;                      // rows per tile
     static constexpr int SEG = LPR * BB;                  // bytes of a full row segment
     static constexpr int J16 = SEG / 1024;                // 1 KB loads (16 B per lane)
     static constexpr int J4 = (SEG - 1024 * J16 + 255) / 256;  // 256 B loads (4 B per lane)
@@ -130,12 +133,7 @@ struct StagedShape {
     static constexpr int WAVE_LDS = RW * SEGP;            // LDS bytes per wave
 };
 
-// LDS offset of x block b in the padded layout: 16 spare bytes after every
-// two 128-byte blocks, so blocks b..b+15 start in 16 distinct bank groups.
-__host__ __device__ constexpr uint32_t x_block_offset(int b) { return 128u * b + 16u * (b >> 1); }
-__host__ __device__ constexpr uint32_t x_lds_bytes(int bpr) { return x_block_offset(bpr) + 16u; }
-
-template <uint32_t QT, int LPR, int R, bool XL, class Rows>
+template <uint32_t QT, int LPR, int R, class Rows>
 __global__ __launch_bounds__(512) void mv_stream_kernel(Rows rows, int nrows, int bpr) {
     using S = StagedShape<QT, LPR, R>;
     constexpr int BB = S::BB, G = S::G, RW = S::RW, J16 = S::J16, J4 = S::J4, SEGP = S::SEGP;
@@ -150,29 +148,11 @@ __global__ __launch_bounds__(512) void mv_stream_kernel(Rows rows, int nrows, in
     const int GW = gridDim.x * wpb;
     const int g = lane / LPR;
     const int li = lane % LPR;
-    const uint32_t xbytes = XL ? x_lds_bytes(bpr) : 0u;
-    uint8_t* const xl = lds_dyn;
-    uint8_t* const wl = lds_dyn + ((xbytes + 15u) & ~15u) + wave * S::WAVE_LDS;
+    uint8_t* const wl = lds_dyn + wave * S::WAVE_LDS;
     const int npass = (bpr + LPR - 1) / LPR;
-    // Batches of this wave: strided rows (XL) or consecutive row tiles.
-    const int my_rows = XL ? (gw < nrows ? (nrows - gw + GW - 1) / GW : 0) : 0;
-    const int batches = XL ? (my_rows + RW - 1) / RW : 0;
     const int tiles = (nrows + RW - 1) / RW;
-    auto row_of = [&](int batch, int seg) {
-        return XL ? gw + (batch * RW + seg) * GW : batch * RW + seg;
-    };
 
-    if (XL) {
-        // x into LDS once: 16-byte chunk c of block b lands at
-        // x_block_offset(b) + 16 * (c % 8).
-        const f32x4* xs = reinterpret_cast<const f32x4*>(rows.input(0));
-        for (int c = threadIdx.x; c < bpr * 8; c += blockDim.x)
-            *reinterpret_cast<f32x4*>(xl + x_block_offset(c >> 3) + 16 * (c & 7)) = xs[c];
-        __syncthreads();
-    }
-
-    // XL: batch index 0..batches-1 of this wave; otherwise tile index.
-    for (int b = XL ? 0 : gw; XL ? b < batches : b < tiles; b += XL ? 1 : GW) {
+    for (int b = gw; b < tiles; b += GW) {
         float acc[R];
 #pragma unroll
         for (int it = 0; it < R; ++it) acc[it] = 0.0f;
@@ -181,7 +161,7 @@ __global__ __launch_bounds__(512) void mv_stream_kernel(Rows rows, int nrows, in
             const int nb = min(LPR, bpr - b0);
 #pragma unroll
             for (int seg = 0; seg < RW; ++seg) {
-                const int row = row_of(b, seg);
+                const int row = b * RW + seg;
                 const uint8_t* src = row < nrows ? rows.row(row) : nullptr;
                 const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
                     const_cast<uint8_t*>(src ? src + static_cast<size_t>(b0) * BB : rows.any()), 0,
@@ -200,23 +180,15 @@ __global__ __launch_bounds__(512) void mv_stream_kernel(Rows rows, int nrows, in
             }
             float xv[32];
             const int col = li < nb ? b0 + li : 0;  // lanes past the pass read block 0 (unused)
-            if (XL) {
-                const uint8_t* xs = xl + x_block_offset(col);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const f32x4 t = *reinterpret_cast<const f32x4*>(xs + 16 * i);
-                    xv[4 * i + 0] = t.x; xv[4 * i + 1] = t.y; xv[4 * i + 2] = t.z; xv[4 * i + 3] = t.w;
-                }
-            } else {
-                const f32x4* xs = reinterpret_cast<const f32x4*>(
-                    rows.input(min(row_of(b, g), nrows - 1)) + 32 * col);
+            {
+                const f32x4* xs = reinterpret_cast<const f32x4*>(rows.input(min(b * RW + g, nrows - 1)) + 32 * col);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const f32x4 t = xs[i];
                     xv[4 * i + 0] = t.x; xv[4 * i + 1] = t.y; xv[4 * i + 2] = t.z; xv[4 * i + 3] = t.w;
                 }
             }
-            // The direct-to-LDS loads (and any x loads) have landed.
+            // The direct-to-LDS loads (and the x loads) have landed.
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             wave_lds_sync();
             if (li < nb) {
@@ -233,9 +205,199 @@ __global__ __launch_bounds__(512) void mv_stream_kernel(Rows rows, int nrows, in
 #pragma unroll
         for (int it = 0; it < R; ++it) {
             const float total = group_sum<LPR>(acc[it]);
-            const int row = row_of(b, it * G + g);
+            const int row = b * RW + it * G + g;
             if (li == 0 && row < nrows) rows.store(row, rows.previous(row) + total);
         }
+    }
+}
+
+// Q4_0 block dot through binary16 subnormals: a nibble n in bits 0-3 of a
+// 16-bit half is the half n * 2^-24, in bits 4-7 it is 16n * 2^-24, and
+// v_fma_mix_f32 multiplies such a half by an FP32 activation exactly (f16 and
+// f32 denormals are enabled).  Two masks per half-pair replace the per-byte
+// converts.  With s(n) = lo + hi / 16 accumulated in a fixed order,
+// sum (n - 8) x = 2^24 * (s(n) - s(8)), where xref = s(8) is the same
+// accumulation with every nibble 8, computed once per block column; a block
+// of zero weights (all nibbles 8) therefore contributes exactly zero.
+// Returns f16(d) times that.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2_t as_half2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+
+__device__ __forceinline__ float block_dot_q4_mix(const uint8_t* lds, uint32_t p, const float* xv, float xref) {
+    const uint32_t scale = *reinterpret_cast<const uint16_t*>(lds + p);
+    const uint32_t start = p + 2;
+    const uint32_t base = start & ~3u;
+    const uint32_t shift = start & 3u;
+    uint32_t a[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) a[k] = *reinterpret_cast<const uint32_t*>(lds + base + 4 * k);
+    float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        // Bytes 4k..4k+3: low nibble of byte j is element j, high nibble 16 + j.
+        const uint32_t u = __builtin_amdgcn_alignbyte(a[k + 1], a[k], shift);
+        const uint32_t t = u >> 8;
+        const half2_t e0 = as_half2(u & 0x000F000Fu);  // elements 4k, 4k+2
+        const half2_t e1 = as_half2(u & 0x00F000F0u);  // elements 16+4k, 16+4k+2 (x16)
+        const half2_t e2 = as_half2(t & 0x000F000Fu);  // elements 4k+1, 4k+3
+        const half2_t e3 = as_half2(t & 0x00F000F0u);  // elements 16+4k+1, 16+4k+3 (x16)
+        lo = fmaf(static_cast<float>(e0.x), xv[4 * k + 0], lo);
+        hi = fmaf(static_cast<float>(e1.x), xv[16 + 4 * k + 0], hi);
+        lo = fmaf(static_cast<float>(e2.x), xv[4 * k + 1], lo);
+        hi = fmaf(static_cast<float>(e3.x), xv[16 + 4 * k + 1], hi);
+        lo = fmaf(static_cast<float>(e0.y), xv[4 * k + 2], lo);
+        hi = fmaf(static_cast<float>(e1.y), xv[16 + 4 * k + 2], hi);
+        lo = fmaf(static_cast<float>(e2.y), xv[4 * k + 3], lo);
+        hi = fmaf(static_cast<float>(e3.y), xv[16 + 4 * k + 3], hi);
+    }
+    const float inner = (fmaf(hi, 0.0625f, lo) - xref) * 16777216.0f;
+    return f16_fast(scale) * inner;
+}
+
+// s(8) of block_dot_q4_mix for one block of 32 activations: the same FMA
+// chains (elements 0..15 and 16..31 in order) with every nibble 8.
+__device__ __forceinline__ float q4_mix_reference(const float* xb) {
+    const half2_t eight = as_half2(0x00800008u);  // 8 * 2^-24 (low nibble), 128 * 2^-24 (high nibble)
+    float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        lo = fmaf(static_cast<float>(eight.x), xb[i], lo);
+        hi = fmaf(static_cast<float>(eight.y), xb[16 + i], hi);
+    }
+    return fmaf(hi, 0.0625f, lo);
+}
+
+// Software-pipelined streaming kernel for inputs shared by every row (x held
+// in LDS, once per workgroup).  A wave works on G = 64 / LPR rows at a time,
+// LPR lanes per row, one lane per 32-weight block column of an LPR-block
+// pass; it owns the strided rows gw, gw + GW, ... in batches of G * R.  A
+// step is one (batch, pass): its G * R row segments arrive in registers by
+// 16-byte buffer loads issued one step ahead, so the loads of step s+1 are in
+// flight while step s computes.  The G segments of a row iteration are
+// written to the wave's LDS slice (reused iteration after iteration: LDS
+// executes a wave's operations in issue order) and read back block-wise.
+// Rows past the matrix, and the prefetch after the last step, use an empty
+// buffer range, which reads zeros without touching memory.
+// Requires: rows 16-byte aligned, bpr % 8 == 0, x 16-byte aligned.
+template <uint32_t QT, int LPR>
+struct PipeShape {
+    static constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
+    static constexpr int G = kWave / LPR;           // rows in flight per wave
+    static constexpr int SEG = LPR * BB;            // bytes of a full row segment
+    static constexpr int J = (SEG + 1023) / 1024;   // 16-byte loads per lane per segment
+    static constexpr int SEGP = 1024 * J;           // LDS bytes per segment
+    static constexpr int WAVE_LDS = G * SEGP;       // LDS bytes per wave
+};
+
+// LDS bytes of the shared part of a pipe launch: x (padded) and, for Q4_0,
+// the per-block references s(8) of block_dot_q4_mix.
+__host__ __device__ constexpr uint32_t pipe_x_bytes(uint32_t qt, int bpr) {
+    return ((x_lds_bytes(bpr) + 15u) & ~15u) +
+           (qt == Q3X_HIP_MATRIX_Q4_0 ? ((4u * bpr + 15u) & ~15u) : 0u);
+}
+
+template <uint32_t QT, int LPR, int R, class Rows>
+__global__ __launch_bounds__(1024) void mv_pipe_kernel(Rows rows, int nrows, int bpr) {
+    using S = PipeShape<QT, LPR>;
+    constexpr int BB = S::BB, G = S::G, J = S::J, RS = G * R;
+    constexpr bool Q4 = QT == Q3X_HIP_MATRIX_Q4_0;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int wpb = blockDim.x / kWave;
+    const int gw = blockIdx.x * wpb + wave;
+    const int GW = gridDim.x * wpb;
+    const int g = lane / LPR;
+    const int li = lane % LPR;
+    uint8_t* const xl = lds_dyn;
+    float* const sxl = reinterpret_cast<float*>(lds_dyn + ((x_lds_bytes(bpr) + 15u) & ~15u));
+    uint8_t* const wl = lds_dyn + pipe_x_bytes(QT, bpr) + wave * S::WAVE_LDS;
+    const int npass = (bpr + LPR - 1) / LPR;
+    const int my_rows = gw < nrows ? (nrows - gw + GW - 1) / GW : 0;
+    const int steps = (my_rows + RS - 1) / RS * npass;
+
+    u32x4 pre[RS][J];
+    // Loads of row i of step (batch b, pass p) into pre[i]; `live` false
+    // gives zeros.
+    auto issue_row = [&](int b, int p, int i, bool live) {
+        const int row = gw + (b * RS + i) * GW;
+        const int b0 = p * LPR;
+        const uint8_t* base = live && row < nrows ? rows.row(row) : nullptr;  // null: expert id out of range
+        const uint8_t* src = base ? base + static_cast<size_t>(b0) * BB : rows.any();
+        const int bytes = base ? min(LPR, bpr - b0) * BB : 0;
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src), 0, bytes, kBufferFlags);
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            pre[i][j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * lane + 1024 * j, 0, kNonTemporal);
+    };
+#pragma unroll
+    for (int i = 0; i < RS; ++i) issue_row(0, 0, i, steps > 0);
+
+    // x into LDS once per workgroup (overlaps the first weight loads), then
+    // the per-block references for Q4_0.
+    {
+        const f32x4* xs = reinterpret_cast<const f32x4*>(rows.input(0));
+        for (int c = threadIdx.x; c < bpr * 8; c += blockDim.x)
+            *reinterpret_cast<f32x4*>(xl + x_block_offset(c >> 3) + 16 * (c & 7)) = xs[c];
+        __syncthreads();
+        if (Q4) {
+            for (int b = threadIdx.x; b < bpr; b += blockDim.x)
+                sxl[b] = q4_mix_reference(reinterpret_cast<const float*>(xl + x_block_offset(b)));
+            __syncthreads();
+        }
+    }
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    int cb = 0, cp = 0;  // current batch and pass
+    for (int s = 0; s < steps; ++s) {
+        int nb = cb, np = cp + 1;
+        if (np == npass) { np = 0; ++nb; }
+        const bool more = s + 1 < steps;
+        const int b0 = cp * LPR;
+        const int nblk = min(LPR, bpr - b0);
+        const int col = li < nblk ? b0 + li : 0;
+        float xv[32];
+        {
+            const uint8_t* xs = xl + x_block_offset(col);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const f32x4 t = *reinterpret_cast<const f32x4*>(xs + 16 * i);
+                xv[4 * i + 0] = t.x; xv[4 * i + 1] = t.y; xv[4 * i + 2] = t.z; xv[4 * i + 3] = t.w;
+            }
+        }
+        const float xref = Q4 ? sxl[col] : 0.0f;
+#pragma unroll
+        for (int it = 0; it < R; ++it) {
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg) {
+#pragma unroll
+                for (int j = 0; j < J; ++j)
+                    *reinterpret_cast<u32x4*>(wl + gg * S::SEGP + 1024 * j + 16 * lane) = pre[it * G + gg][j];
+                issue_row(nb, np, it * G + gg, more);
+            }
+            wave_lds_sync();
+            if (li < nblk) {
+                const uint32_t p = g * S::SEGP + li * BB;
+                acc[it] += Q4 ? block_dot_q4_mix(wl, p, xv, xref) : block_dot_q8(wl, p, xv);
+            }
+            wave_lds_sync();
+        }
+        if (cp == npass - 1) {
+#pragma unroll
+            for (int it = 0; it < R; ++it) {
+                const float total = group_sum<LPR>(acc[it]);
+                const int row = gw + (cb * RS + it * G + g) * GW;
+                if (li == 0 && row < nrows) rows.store(row, rows.previous(row) + total);
+                acc[it] = 0.0f;
+            }
+        }
+        cb = nb;
+        cp = np;
     }
 }
 
@@ -279,26 +441,25 @@ __global__ __launch_bounds__(kMvWaves * kWave) void mv_generic_kernel(Rows rows,
 
 // ---- launch helpers shared with the MoE decode path ----
 
-// Persistent grid sized to what is resident at once on 256 CUs: workgroups
-// of 4 (or 8) wavefronts, as many per CU as LDS allows (at most 2 of 4 or 1
-// of 8 = 8 wavefronts per CU, the occupancy that streams best), never more
-// workgroups than row tiles need.
 constexpr int kCUs = 256;
 constexpr size_t kLdsPerCU = 160 * 1024;
 
-template <uint32_t QT, int LPR, int R, bool XL, class Rows>
+// Streaming launch: persistent grid sized to what is resident at once on 256
+// CUs -- workgroups of 4 (or 8) wavefronts, as many per CU as LDS allows (at
+// most 2 of 4 or 1 of 8 = 8 wavefronts per CU, the occupancy that streams
+// best) -- never more workgroups than row tiles need.
+template <uint32_t QT, int LPR, int R, class Rows>
 inline int launch_stream(const Rows& rows, int nrows, int bpr, int wpb, size_t lds, int wgs_per_cu,
                          hipStream_t stream) {
     using S = StagedShape<QT, LPR, R>;
-    auto kernel = mv_stream_kernel<QT, LPR, R, XL, Rows>;
+    auto kernel = mv_stream_kernel<QT, LPR, R, Rows>;
     // Allow the largest dynamic LDS this instantiation can use (once per
     // process: the first call of each instantiation, typically eager).
     static const bool lds_ready =
         hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(kLdsPerCU)) == hipSuccess;
     if (lds > 64 * 1024 && !lds_ready) return Q3X_HIP_ERUNTIME;
-    // XL: at most one wavefront per row; otherwise one per row tile.
-    const long long units = XL ? nrows : (nrows + S::RW - 1) / S::RW;
+    const long long units = (nrows + S::RW - 1) / S::RW;
     const long long need = (units + wpb - 1) / wpb;
     const int grid = static_cast<int>(std::min<long long>(need, static_cast<long long>(kCUs) * wgs_per_cu));
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWave * wpb), lds, stream, rows, nrows, bpr);
@@ -312,38 +473,24 @@ struct StreamPlan {
     bool ok = false;
 };
 
-inline StreamPlan plan_stream(size_t xb, int wave_lds) {
+inline StreamPlan plan_stream(int wave_lds) {
     StreamPlan p;
     // 8 resident wavefronts per CU: one workgroup of 8 (measured slightly
     // ahead), else two of 4.
-    if (xb + 8u * wave_lds <= kLdsPerCU) { p.wpb = 8; p.per_cu = 1; p.lds = xb + 8u * wave_lds; p.ok = true; }
-    else if ((xb + 4u * wave_lds) * 2 <= kLdsPerCU) { p.wpb = 4; p.per_cu = 2; p.lds = xb + 4u * wave_lds; p.ok = true; }
+    if (8u * wave_lds <= kLdsPerCU) { p.wpb = 8; p.per_cu = 1; p.lds = 8u * wave_lds; p.ok = true; }
+    else if (4u * wave_lds * 2 <= kLdsPerCU) { p.wpb = 4; p.per_cu = 2; p.lds = 4u * wave_lds; p.ok = true; }
     return p;
 }
 
-// Chooses R for LPR lanes per row.  XL (strided rows): batch sizes measured
-// best per shape class (below).  Otherwise (consecutive tiles), the cost of a candidate is the
-// rows one wavefront streams -- ceil(tiles / waves) * rows per tile, so
-// uneven tile counts are charged -- times the extra x traffic of small tiles.
-template <uint32_t QT, int LPR, bool XL, class Rows>
+// Chooses R for LPR lanes per row: the cost of a candidate is the rows one
+// wavefront streams -- ceil(tiles / waves) * rows per tile, so uneven tile
+// counts are charged -- times the extra x traffic of small tiles.
+template <uint32_t QT, int LPR, class Rows>
 inline int launch_staged(const Rows& rows, int nrows, int bpr, hipStream_t stream) {
-    const size_t xb = XL ? ((x_lds_bytes(bpr) + 15) & ~size_t{15}) : 0;
-    const StreamPlan p4 = plan_stream(xb, StagedShape<QT, LPR, 4>::WAVE_LDS);
-    const StreamPlan p2 = plan_stream(xb, StagedShape<QT, LPR, 2>::WAVE_LDS);
-    const StreamPlan p1 = plan_stream(xb, StagedShape<QT, LPR, 1>::WAVE_LDS);
+    const StreamPlan p4 = plan_stream(StagedShape<QT, LPR, 4>::WAVE_LDS);
+    const StreamPlan p2 = plan_stream(StagedShape<QT, LPR, 2>::WAVE_LDS);
+    const StreamPlan p1 = plan_stream(StagedShape<QT, LPR, 1>::WAVE_LDS);
     const bool q8 = QT == Q3X_HIP_MATRIX_Q8_0;
-    if (XL) {
-        // Q8_0: 4-row batches once every wavefront has many rows (lm_head),
-        // 2-row batches for matrices of a few rows per wavefront; Q4_0: 4.
-        const long long waves = static_cast<long long>(kCUs) * 8;
-        const int target = !q8 ? 4 : (nrows >= 16 * waves ? 4 : (nrows >= waves ? 2 : 1));
-        if (target >= 4 && p4.ok)
-            return launch_stream<QT, LPR, 4, XL>(rows, nrows, bpr, p4.wpb, p4.lds, p4.per_cu, stream);
-        if (target >= 2 && p2.ok)
-            return launch_stream<QT, LPR, 2, XL>(rows, nrows, bpr, p2.wpb, p2.lds, p2.per_cu, stream);
-        if (p1.ok) return launch_stream<QT, LPR, 1, XL>(rows, nrows, bpr, p1.wpb, p1.lds, p1.per_cu, stream);
-        return Q3X_HIP_ENOTSUP;  // x too long for LDS: caller uses the global-x variant
-    }
     auto cost = [&](const StreamPlan& p, int r, double x_factor) {
         if (!p.ok) return 1e300;
         const long long rw = static_cast<long long>(kWave / LPR) * r;
@@ -355,10 +502,50 @@ inline int launch_staged(const Rows& rows, int nrows, int bpr, hipStream_t strea
     const double c2 = cost(p2, 2, q8 ? 1.15 : 1.3);
     const double c1 = cost(p1, 1, q8 ? 1.5 : 2.0);
     if (c4 <= c2 && c4 <= c1 && p4.ok)
-        return launch_stream<QT, LPR, 4, XL>(rows, nrows, bpr, p4.wpb, p4.lds, p4.per_cu, stream);
+        return launch_stream<QT, LPR, 4>(rows, nrows, bpr, p4.wpb, p4.lds, p4.per_cu, stream);
     if (c2 <= c1 && p2.ok)
-        return launch_stream<QT, LPR, 2, XL>(rows, nrows, bpr, p2.wpb, p2.lds, p2.per_cu, stream);
-    return launch_stream<QT, LPR, 1, XL>(rows, nrows, bpr, p1.wpb, p1.lds, p1.per_cu, stream);
+        return launch_stream<QT, LPR, 2>(rows, nrows, bpr, p2.wpb, p2.lds, p2.per_cu, stream);
+    return launch_stream<QT, LPR, 1>(rows, nrows, bpr, p1.wpb, p1.lds, p1.per_cu, stream);
+}
+
+// Pipe launch: rows per step RS = G * R; a wave takes B batches, B the
+// fewest that the resident waves allow, and the grid then shrinks so that
+// every wave gets B full batches (balanced), spreading the waves over all
+// CUs (fewer per workgroup) when there are fewer than 256 workgroups' worth.
+template <uint32_t QT, int LPR, int R, class Rows>
+inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_t stream) {
+    using S = PipeShape<QT, LPR>;
+    auto kernel = mv_pipe_kernel<QT, LPR, R, Rows>;
+    static const bool lds_ready =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(kLdsPerCU)) == hipSuccess;
+    size_t lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb) * S::WAVE_LDS;
+    while (lds > kLdsPerCU && wpb > 4) {
+        wpb -= 4;
+        lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb) * S::WAVE_LDS;
+    }
+    if (lds > kLdsPerCU) return Q3X_HIP_ENOTSUP;  // x too long for LDS
+    if (lds > 64 * 1024 && !lds_ready) return Q3X_HIP_ERUNTIME;
+    const long long rs = static_cast<long long>(S::G) * R;
+    const long long gw_max = static_cast<long long>(kCUs) * wpb;
+    const long long batches = (nrows + gw_max * rs - 1) / (gw_max * rs);
+    const long long waves = (nrows + batches * rs - 1) / (batches * rs);
+    const int wpb_used = static_cast<int>(std::min<long long>(wpb, (waves + kCUs - 1) / kCUs));
+    const int grid = static_cast<int>((waves + wpb_used - 1) / wpb_used);
+    lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb_used) * S::WAVE_LDS;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWave * wpb_used), lds, stream, rows, nrows, bpr);
+    return launch_status();
+}
+
+// Shapes measured on MI355X: one row per step and 16 waves per CU while a
+// wave has about one row; two rows per step and 12 waves per CU beyond.
+template <uint32_t QT, class Rows>
+inline int launch_pipe_for(const Rows& rows, int nrows, int bpr, hipStream_t stream) {
+    if (bpr <= 16) return launch_pipe<QT, 16, 1>(rows, nrows, bpr, 16, stream);
+    if (bpr <= 32) return launch_pipe<QT, 32, 1>(rows, nrows, bpr, 16, stream);
+    const int small = QT == Q3X_HIP_MATRIX_Q8_0 ? 6144 : 4096;
+    if (nrows <= small) return launch_pipe<QT, 64, 1>(rows, nrows, bpr, 16, stream);
+    return launch_pipe<QT, 64, 2>(rows, nrows, bpr, 12, stream);
 }
 
 template <uint32_t QT, class Rows>
@@ -369,20 +556,14 @@ int launch_mv(const Rows& rows, int nrows, int bpr, bool staged, hipStream_t str
                            stream, rows, nrows, bpr);
         return launch_status();
     }
-    // x shared by all rows (and short enough for LDS): staged once per
-    // workgroup; otherwise per unit from global memory.
+    // x shared by all rows and short enough for LDS: the pipelined kernel;
+    // otherwise the streaming kernel reading x per unit from global memory.
     int status = Q3X_HIP_ENOTSUP;
-    if (bpr <= 16) {
-        if constexpr (Rows::kSharedInput) status = launch_staged<QT, 16, true>(rows, nrows, bpr, stream);
-        if (status == Q3X_HIP_ENOTSUP) status = launch_staged<QT, 16, false>(rows, nrows, bpr, stream);
-    } else if (bpr <= 32) {
-        if constexpr (Rows::kSharedInput) status = launch_staged<QT, 32, true>(rows, nrows, bpr, stream);
-        if (status == Q3X_HIP_ENOTSUP) status = launch_staged<QT, 32, false>(rows, nrows, bpr, stream);
-    } else {
-        if constexpr (Rows::kSharedInput) status = launch_staged<QT, 64, true>(rows, nrows, bpr, stream);
-        if (status == Q3X_HIP_ENOTSUP) status = launch_staged<QT, 64, false>(rows, nrows, bpr, stream);
-    }
-    return status;
+    if constexpr (Rows::kSharedInput) status = launch_pipe_for<QT>(rows, nrows, bpr, stream);
+    if (status != Q3X_HIP_ENOTSUP) return status;
+    if (bpr <= 16) return launch_staged<QT, 16>(rows, nrows, bpr, stream);
+    if (bpr <= 32) return launch_staged<QT, 32>(rows, nrows, bpr, stream);
+    return launch_staged<QT, 64>(rows, nrows, bpr, stream);
 }
 
 }  // namespace q3x
