@@ -3,12 +3,14 @@
 Headline (BASELINE.json metric, configs[1]): one decode step's Q8_0 matvec
 set of a dense 9B-class layer (q, k, v, o 4096->4096; gate, up 4096->12288;
 down 12288->4096) plus the lm_head matvec 4096->151936, batch 1, FP32
-activations.  value = algorithmic bytes (weights + x + y) / time, GB/s, with
-all inputs resident in HBM.  Distinct weight copies are rotated so the
+activations, launched in the reference's call pattern (q|k|v and gate|up
+each one projections launch, o and down accumulating into the residual).
+value = algorithmic bytes (weights + inputs + outputs) / step time, GB/s,
+with all inputs resident in HBM.  Distinct weight copies are rotated so the
 256 MB Infinity Cache cannot serve them.  The other configurations are
 reported under "configs" (matvec GB/s, GEMM TFLOP/s, MoE).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-configs] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-configs] [--no-cpu] [--roofline-only]
 """
 from __future__ import annotations
 
@@ -35,6 +37,8 @@ def parse():
     ap.add_argument("--no-configs", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the lm_head kernel (--steps launches) and a same-size copy, for counter runs")
     return ap.parse_args()
 
 
@@ -58,22 +62,70 @@ def capture(torch, fn):
     return g
 
 
-def check_replays(torch, graph, eager, outputs, times=3):
-    """Every replay must reproduce the eager result bit for bit (the kernels are
-    deterministic); eager work runs between the replays."""
-    eager()
+LAYER_LAUNCHES = ("attention projections q|k|v (one q3x_hip_mv_multi), o (mv_add), "
+                  "ffn projections gate|up (one q3x_hip_mv_multi), down (mv_add), then lm_head (mv)")
+
+
+class LayerStep:
+    """One decode step's matvecs in the reference's call pattern (engine.cu
+    attention :1682-1700 and ffn :1701-1707 over the projection helpers
+    :1607-1619, then the lm_head mv :1990): q/k/v share the normed input, o and
+    down add into the residual, gate/up share the FFN input."""
+
+    def __init__(self, torch, q3x, wl, mats):
+        self.q3x = q3x
+        self.by = {m.name: m for m in mats}
+        h = 4096
+        self.x_attn = wl.activations(1, 1, h, salt=1)[0].contiguous()
+        self.x_o = wl.activations(1, 1, h, salt=2)[0].contiguous()
+        self.x_ffn = wl.activations(1, 1, h, salt=3)[0].contiguous()
+        self.h = wl.activations(1, 1, 12288, salt=4)[0].contiguous()
+        self.x_final = wl.activations(1, 1, h, salt=5)[0].contiguous()
+        self.resid0 = wl.activations(1, 1, h, salt=6)[0].contiguous()
+        self.resid = self.resid0.clone()
+        self.out = {m.name: torch.empty(m.rows, dtype=torch.float32, device="cuda") for m in mats
+                    if m.name not in ("o", "down")}
+
+    def run_layer(self, s):
+        q3x, o = self.q3x, self.out
+        q3x.mv_multi([s["q"].linear, s["k"].linear, s["v"].linear], self.x_attn, [o["q"], o["k"], o["v"]])
+        q3x.mv_add(s["o"].linear, self.x_o, self.resid)
+        q3x.mv_multi([s["gate"].linear, s["up"].linear], self.x_ffn, [o["gate"], o["up"]])
+        q3x.mv_add(s["down"].linear, self.h, self.resid)
+
+    def run_lm(self, lm):
+        self.q3x.mv(lm.linear, self.x_final, self.out["lm_head"])
+
+    def reset(self):
+        self.resid.copy_(self.resid0)
+
+    def step_bytes(self):
+        """Algorithmic HBM bytes of one step: every weight byte once, each
+        launch's input once, each output written (and read once more where it
+        accumulates)."""
+        b = self.by
+        weights = sum(m.nbytes for m in b.values())
+        inputs = 4 * (4096 * 4 + 12288)                       # q|k|v, o, gate|up, lm_head inputs + down's h
+        outputs = 4 * (b["q"].rows + b["k"].rows + b["v"].rows + b["gate"].rows + b["up"].rows
+                       + b["lm_head"].rows) + 2 * 4 * (b["o"].rows + b["down"].rows)
+        return weights + inputs + outputs
+
+
+def lm_head_launch_ms(torch, step, lm_set, reps):
+    """Average duration of the lm_head kernel: `reps` back-to-back launches
+    (rotating weight copies) between two HIP events on the launch stream."""
+    for i in range(3):
+        step.run_lm(lm_set[i % len(lm_set)])
     torch.cuda.synchronize()
-    want = [o.clone() for o in outputs]
-    for _ in range(times):
-        for o in outputs:
-            o.fill_(float("nan"))
-        graph.replay()
-        torch.cuda.synchronize()
-        for o, w in zip(outputs, want):
-            if not torch.equal(o.view(torch.int32), w.view(torch.int32)):
-                raise RuntimeError("graph replay differs from the eager result")
-        eager()
-        torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        step.run_lm(lm_set[i % len(lm_set)])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
 
 
 def headline(torch, q3x, wl, steps, warmup):
@@ -83,46 +135,31 @@ def headline(torch, q3x, wl, steps, warmup):
     layer_bytes = sum(m.nbytes for m in layer)
     n_layer = copies_for(layer_bytes)
     n_lm = copies_for(lm.nbytes)
-    layer_sets = [layer] + [[wl.Matrix(m.name, m.type, m.rows, m.cols, m.weight.clone()) for m in layer]
-                            for _ in range(n_layer - 1)]
+    layer_sets = [{m.name: m for m in layer}] + [
+        {m.name: wl.Matrix(m.name, m.type, m.rows, m.cols, m.weight.clone()) for m in layer}
+        for _ in range(n_layer - 1)]
     lm_set = [lm] + [wl.Matrix(lm.name, lm.type, lm.rows, lm.cols, lm.weight.clone()) for _ in range(n_lm - 1)]
-    x = wl.activations(1, 1, 12288)[0].contiguous()
-    ys = {m.name: torch.empty(m.rows, dtype=torch.float32, device="cuda") for m in mats}
-    step_bytes = sum(mv_bytes(m) for m in mats)
+    step = LayerStep(torch, q3x, wl, mats)
 
-    def run_layer(r):
-        for m in layer_sets[r]:
-            q3x.mv(m.linear, x, ys[m.name])
-
-    def run_lm(r):
-        q3x.mv(lm_set[r].linear, x, ys["lm_head"])
-
-    # The layer set (seven launches) is replayed as a HIP graph; lm_head is
-    # launched directly between two events.  The host queues it while the GPU
-    # still runs the layer graph, so the events bracket the lm_head kernel
-    # itself (the dominant kernel of the step, timed for the roofline).
-    layer_graphs = [capture(torch, lambda r=r: run_layer(r)) for r in range(n_layer)]
-    check_replays(torch, layer_graphs[1], lambda: run_layer(1), [ys[m.name] for m in layer])
+    # A step is five launches on one stream (back-to-back kernels on a
+    # stream start without a gap on this runtime, while consecutive graph
+    # launches leave ~8 us between graphs).
+    def run_step(r):
+        step.run_layer(layer_sets[r])
+        step.run_lm(lm_set[r % n_lm])
 
     for i in range(warmup):
-        layer_graphs[i % n_layer].replay()
-        run_lm(i % n_lm)
-    events = []
+        run_step(i % n_layer)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        layer_graphs[i % n_layer].replay()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        run_lm(i % n_lm)
-        e1.record()
-        events.append((e0, e1))
+        run_step(i % n_layer)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms = elapsed * 1e3 / steps
-    lm_ms = statistics.fmean(a.elapsed_time(b) for a, b in events)
+    lm_ms = lm_head_launch_ms(torch, step, lm_set, 20)
     lm_alg = mv_bytes(lm)
+    step_bytes = step.step_bytes()
     return {
         "value": step_bytes / (ms * 1e-3) / 1e9,
         "ms_per_step": ms,
@@ -131,6 +168,36 @@ def headline(torch, q3x, wl, steps, warmup):
         "lm_head": {"bytes": lm_alg, "ms": lm_ms, "GBps": lm_alg / (lm_ms * 1e-3) / 1e9},
         "mats": mats,
     }
+
+
+def measured_traffic():
+    """HBM bytes per lm_head launch from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel), or None."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic_lm_head_q8_0.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def roofline_only(torch, q3x, wl, reps):
+    """Short program for counter runs: the lm_head kernel `reps` times on two
+    weight copies, then a plain device copy of the same size (the calibration
+    kernel for FETCH_SIZE / WRITE_SIZE)."""
+    mats = wl.dense_matrices(1)
+    lm = [m for m in mats if m.name == "lm_head"][0]
+    lm_set = [lm, wl.Matrix(lm.name, lm.type, lm.rows, lm.cols, lm.weight.clone())]
+    step = LayerStep(torch, q3x, wl, mats)
+    ms = lm_head_launch_ms(torch, step, lm_set, reps)
+    src = torch.empty(lm.nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"lm_head_ms": ms, "lm_head_bytes": mv_bytes(lm), "copy_bytes_each_way": src.numel() * 4,
+                      "GBps": mv_bytes(lm) / (ms * 1e-3) / 1e9}), flush=True)
 
 
 def time_graph(torch, fn, calls, replays, warmup=2):
@@ -186,10 +253,11 @@ def extra_configs(torch, q3x, wl):
     ys = {mm.name: torch.empty(mm.rows, dtype=torch.float32, device="cuda") for mm in mats}
 
     def run_mv(i):
-        for mm in sets[i % n]:
-            q3x.mv(mm.linear, x, ys[mm.name])
+        s = {mm.name: mm for mm in sets[i % n]}
+        q3x.mv_multi([s["gate"].linear, s["up"].linear], x, [ys["gate"], ys["up"]])
+        q3x.mv(s["down"].linear, x, ys["down"])
     ms = time_graph(torch, run_mv, 2 * n, 10)
-    alg = sum(mv_bytes(mm) for mm in mats)
+    alg = sum(mv_bytes(mm) for mm in mats) - 4 * 5120  # gate|up read x once
     out["cfg3_q4_mv_27b_ffn"] = {"GBps": alg / (ms * 1e-3) / 1e9, "us": ms * 1e3, "copies": n}
     del sets
     X = wl.activations(3, 512, 5120)
@@ -220,7 +288,7 @@ def extra_configs(torch, q3x, wl):
         def run_moe(i):
             q3x.router_top_k(logits, T, moe.experts, k, ids, wts)
             q3x.moe_routed(moe.gate_up_linear, moe.down_linear, X, T, ids, wts, k, Y, workspace=wsb)
-        ms = time_graph(torch, run_moe, 1, 50 if T == 1 else 5)
+        ms = time_graph(torch, run_moe, 20 if T == 1 else 1, 10 if T == 1 else 5)
         if T == 1:
             per_expert = (moe.gate_up.numel() + moe.down.numel()) // moe.experts
             alg = k * per_expert
@@ -275,8 +343,12 @@ def main():
     from qwen3x_amd import workloads as wl
 
     torch.cuda.set_device(0)
+    if args.roofline_only:
+        roofline_only(torch, q3x, wl, args.steps)
+        return
     head = headline(torch, q3x, wl, args.steps, args.warmup)
     lm = head["lm_head"]
+    traffic = measured_traffic()
     result = {
         "metric": "Q8/Q4 matvec HBM GB/s (% of peak) at N=1; prefill GEMM FP32 TFLOP/s",
         "value": round(head["value"], 2),
@@ -292,12 +364,13 @@ def main():
         "data": "synthetic (seeded N(0,0.02) weights quantised to Q8_0; N(0,1) activations)",
         "config": {"workload": "config 1: Q8_0 decode matvec set of one 9B-class layer "
                                "(q/k/v/o 4096->4096, gate/up 4096->12288, down 12288->4096) + lm_head "
-                               "4096->151936, batch 1", "step_bytes": head["step_bytes"],
+                               "4096->151936, batch 1", "launches": LAYER_LAUNCHES, "step_bytes": head["step_bytes"],
                    "weight_copies_rotated": head["copies"], "frac_of_hbm_peak": round(head["value"] / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(lm["GBps"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lm["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "mv_stream_kernel<Q8_0, 64 lanes/row, 4-row batches, x in LDS> on lm_head 151936x4096",
-                     "algorithmic_bytes_per_launch": lm["bytes"], "avg_launch_ms": round(lm["ms"], 5)},
+                     "frac": round(lm["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "mv_pipe_kernel<Q8_0, 64 lanes/row, 2 rows/step, 12 waves/CU> on lm_head 151936x4096",
+                     "algorithmic_bytes_per_launch": lm["bytes"], "avg_launch_ms": round(lm["ms"], 5),
+                     "traffic_source": "profiles/pmc_traffic_lm_head_q8_0.txt" if traffic else None},
     }
     if not args.no_configs:
         result["configs"] = extra_configs(torch, q3x, wl)

@@ -71,6 +71,25 @@ int q3x_hip_quantized_bytes(uint32_t type, int rows, int cols, size_t* bytes);
 int q3x_hip_mv(const void* w, uint32_t type, int rows, int cols,
                const float* x, float* y, int accumulate, hipStream_t stream);
 
+/* One matrix of a q3x_hip_mv_multi call: out[rows] (+)= W[rows, cols] x. */
+typedef struct q3x_hip_mv_item {
+    const void* weight;  /* device, row-major [rows, cols/32] blocks */
+    int rows;
+    float* out;          /* device, out[rows] */
+    int accumulate;      /* nonzero: out += W x */
+} q3x_hip_mv_item;
+
+#define Q3X_HIP_MV_MULTI_MAX 8
+
+/* Several matrices of one type and width applied to the same input x, in one
+ * launch: items[i].out (+)= items[i].W x for i < count (1..8).  Replaces the
+ * CUDA backend's projection helpers attention_projections (q, k, v),
+ * ffn_projections (gate, up) and delta_projections (qkv, z, a, b)
+ * (arch/cuda/engine.cu:1599-1661), which issue one mv() per matrix for Q8_0.
+ * Results equal q3x_hip_mv on each item bit for bit. */
+int q3x_hip_mv_multi(const q3x_hip_mv_item* items, int count, uint32_t type, int cols,
+                     const float* x, hipStream_t stream);
+
 /* Y[count, rows] (+)= X[count, cols] W[rows, cols]^T, row-major X and Y.
  * Replaces batch_mv() (arch/cuda/engine.cu:1568; batch_mv_q8_kernel :761),
  * and adds the Q4_0 case the CUDA backend lacks (engine.cu:1580).  `count`

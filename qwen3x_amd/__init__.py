@@ -38,6 +38,7 @@ SIGNATURES = {
     "q3x_hip_strerror": (ctypes.c_char_p, [_I]),
     "q3x_hip_quantized_bytes": (_I, [_U, _I, _I, ctypes.POINTER(_S)]),
     "q3x_hip_mv": (_I, [_P, _U, _I, _I, _P, _P, _I, _P]),
+    "q3x_hip_mv_multi": (_I, [_P, _I, _U, _I, _P, _P]),
     "q3x_hip_gemm": (_I, [_P, _U, _I, _I, _P, _I, _P, _I, _P]),
     "q3x_hip_dequant": (_I, [_P, _U, _I, _I, _I, _P, _P]),
     "q3x_hip_router_topk": (_I, [_P, _I, _I, _I, _P, _P, _P]),
@@ -45,6 +46,15 @@ SIGNATURES = {
     "q3x_hip_moe_routed": (_I, [_P, _P, _U, _I, _I, _I, _P, _I, _P, _P, _I, _P, _I, _P, _S, _P]),
     "q3x_hip_quantize": (_I, [_U, _P, _I, _I, _P, _P]),
 }
+
+
+MV_MULTI_MAX = 8
+
+
+class MvItem(ctypes.Structure):
+    """struct q3x_hip_mv_item of include/q3x_hip.h."""
+    _fields_ = [("weight", ctypes.c_void_p), ("rows", ctypes.c_int), ("out", ctypes.c_void_p),
+                ("accumulate", ctypes.c_int)]
 
 
 class Q3xHipError(RuntimeError):
@@ -147,6 +157,26 @@ def mv(linear: Linear, x, y, accumulate: bool = False, stream=None):
 
 def mv_add(linear: Linear, x, y, stream=None):
     return mv(linear, x, y, True, stream)
+
+
+def mv_multi(linears, x, outs, accumulate=None, stream=None):
+    """outs[i] (+)= linears[i] x for matrices of one type and width, one launch
+    (the projection helpers attention_projections / ffn_projections /
+    delta_projections, engine.cu:1599-1661)."""
+    n = len(linears)
+    if n != len(outs) or not 1 <= n <= MV_MULTI_MAX:
+        raise ValueError(f"mv_multi takes 1..{MV_MULTI_MAX} matrices with one output each")
+    accumulate = accumulate or [False] * n
+    first = linears[0]
+    for m in linears:
+        if m.type != first.type or m.columns != first.columns:
+            raise ValueError("mv_multi: every matrix must share the type and the width")
+    _need_device(x, *outs, *(m.weight for m in linears))
+    items = (MvItem * n)(*[MvItem(_ptr(m.weight), m.rows, _ptr(o), int(a))
+                           for m, o, a in zip(linears, outs, accumulate)])
+    _check("q3x_hip_mv_multi", lib().q3x_hip_mv_multi(ctypes.cast(items, ctypes.c_void_p), n, first.type,
+                                                      first.columns, _ptr(x), _stream(stream)))
+    return outs
 
 
 def batch_mv(linear: Linear, X, Y, count: int, add: bool = False, stream=None):

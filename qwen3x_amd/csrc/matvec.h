@@ -298,7 +298,7 @@ __host__ __device__ constexpr uint32_t pipe_x_bytes(uint32_t qt, int bpr) {
 }
 
 template <uint32_t QT, int LPR, int R, class Rows>
-__global__ __launch_bounds__(1024) void mv_pipe_kernel(Rows rows, int nrows, int bpr) {
+__global__ __launch_bounds__(1024) void mv_pipe_kernel(Rows all_rows, int nrows, int bpr) {
     using S = PipeShape<QT, LPR>;
     constexpr int BB = S::BB, G = S::G, J = S::J, RS = G * R;
     constexpr bool Q4 = QT == Q3X_HIP_MATRIX_Q4_0;
@@ -307,8 +307,10 @@ __global__ __launch_bounds__(1024) void mv_pipe_kernel(Rows rows, int nrows, int
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int wpb = blockDim.x / kWave;
-    const int gw = blockIdx.x * wpb + wave;
-    const int GW = gridDim.x * wpb;
+    int gw = blockIdx.x * wpb + wave;
+    int GW = gridDim.x * wpb;
+    // The wave's matrix (multi-matrix launches); gw, GW, nrows become its own.
+    const auto rows = all_rows.for_wave(gw, GW, nrows);
     const int g = lane / LPR;
     const int li = lane % LPR;
     uint8_t* const xl = lds_dyn;
@@ -529,11 +531,14 @@ inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_
     const long long rs = static_cast<long long>(S::G) * R;
     const long long gw_max = static_cast<long long>(kCUs) * wpb;
     const long long batches = (nrows + gw_max * rs - 1) / (gw_max * rs);
-    const long long waves = (nrows + batches * rs - 1) / (batches * rs);
+    const long long waves =
+        std::max<long long>((nrows + batches * rs - 1) / (batches * rs), rows.matrices());
     const int wpb_used = static_cast<int>(std::min<long long>(wpb, (waves + kCUs - 1) / kCUs));
     const int grid = static_cast<int>((waves + wpb_used - 1) / wpb_used);
     lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb_used) * S::WAVE_LDS;
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWave * wpb_used), lds, stream, rows, nrows, bpr);
+    Rows planned = rows;
+    planned.plan_waves(grid * wpb_used);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWave * wpb_used), lds, stream, planned, nrows, bpr);
     return launch_status();
 }
 

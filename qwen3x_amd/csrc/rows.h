@@ -30,6 +30,107 @@ struct DenseRows {
     // Value the result is added to.
     __device__ float previous(int r) const { return ACCUMULATE ? y[r] : 0.0f; }
     __device__ void store(int r, float v) const { y[r] = v; }
+    __host__ int matrices() const { return 1; }
+    __host__ void plan_waves(int) {}
+    __device__ const DenseRows& for_wave(int&, int&, int&) const { return *this; }
+};
+
+// One dense matrix chosen at run time (a wave's share of a multi-matrix
+// launch): y[r] = W[r] x, or y[r] += W[r] x when `accumulate`.
+struct OneMatrix {
+    static constexpr bool kSharedInput = true;
+    const uint8_t* w;
+    size_t row_bytes;
+    const float* x;
+    float* y;
+    bool accumulate;
+    __device__ const uint8_t* row(int r) const { return w + static_cast<size_t>(r) * row_bytes; }
+    __device__ const uint8_t* any() const { return w; }
+    __device__ const float* input(int) const { return x; }
+    __device__ float previous(int r) const { return accumulate ? y[r] : 0.0f; }
+    __device__ void store(int r, float v) const { y[r] = v; }
+};
+
+// Up to Q3X_HIP_MV_MULTI_MAX matrices of one type and width that read the
+// same x.  Matrix i holds virtual rows [end[i-1], end[i]) and owns the waves
+// [wave_end[i-1], wave_end[i]) of the launch (in proportion to its rows, set
+// by plan_waves once the launch's wave count is known), so a wave looks its
+// matrix up once, at the start, and then streams it like a dense matrix.
+struct MultiRows {
+    static constexpr bool kSharedInput = true;
+    static constexpr int kMax = Q3X_HIP_MV_MULTI_MAX;
+    const uint8_t* w[kMax];
+    float* y[kMax];
+    int end[kMax];
+    int wave_end[kMax];
+    int count;
+    uint32_t accumulate_mask;
+    size_t row_bytes;
+    const float* x;
+
+    __host__ __device__ int rows_of(int i) const { return end[i] - (i ? end[i - 1] : 0); }
+    __host__ int matrices() const { return count; }
+
+    // Waves per matrix for a launch of GW waves (GW >= count): one each, then
+    // the rest in proportion to the rows, the remainder to the matrices with
+    // the most rows per wave.
+    __host__ void plan_waves(int GW) {
+        const long long total = end[count - 1];
+        int waves[kMax];
+        int used = 0;
+        for (int i = 0; i < count; ++i) {
+            waves[i] = 1 + static_cast<int>((static_cast<long long>(GW - count) * rows_of(i)) / total);
+            used += waves[i];
+        }
+        while (used < GW) {
+            int best = 0;
+            for (int i = 1; i < count; ++i)
+                if (static_cast<long long>(rows_of(i)) * waves[best] > static_cast<long long>(rows_of(best)) * waves[i])
+                    best = i;
+            ++waves[best];
+            ++used;
+        }
+        int acc = 0;
+        for (int i = 0; i < kMax; ++i) {
+            acc += i < count ? waves[i] : 0;
+            wave_end[i] = acc;
+        }
+    }
+
+    // The matrix of wave gw; gw, GW and nrows become that matrix's own wave
+    // index, wave count and row count.  Unrolled over the fixed maximum with
+    // compile-time indices, so the table stays in scalar registers.
+    __device__ OneMatrix for_wave(int& gw, int& GW, int& nrows) const {
+        int k = 0;
+#pragma unroll
+        for (int i = 1; i < kMax; ++i)
+            if (i < count && gw >= wave_end[i - 1]) k = i;
+        const uint8_t* wk = nullptr;
+        float* yk = nullptr;
+        int first_wave = 0, first_row = 0, last_wave = 0, last_row = 0;
+#pragma unroll
+        for (int i = 0; i < kMax; ++i) {
+            // Opaque scalar copies: keeps the compiler from turning this
+            // select chain into an indexed access of a private copy of the
+            // table (scratch memory and divergent pointers).
+            const uint8_t* wi = w[i];
+            float* yi = y[i];
+            int fw = i ? wave_end[i - 1] : 0, fr = i ? end[i - 1] : 0, lw = wave_end[i], lr = end[i];
+            asm volatile("" : "+s"(wi), "+s"(yi), "+s"(fw), "+s"(fr), "+s"(lw), "+s"(lr));
+            if (i == k) {
+                wk = wi;
+                yk = yi;
+                first_wave = fw;
+                first_row = fr;
+                last_wave = lw;
+                last_row = lr;
+            }
+        }
+        gw -= first_wave;
+        GW = last_wave - first_wave;
+        nrows = last_row - first_row;
+        return OneMatrix{wk, row_bytes, x, yk, ((accumulate_mask >> k) & 1u) != 0};
+    }
 };
 
 // The experts one token selected, viewed as one tall matrix: virtual row
@@ -63,6 +164,9 @@ struct ExpertRows {
     __device__ const float* input(int r) const { return SHARED ? x : x + slot(r) * x_slot_stride; }
     __device__ float previous(int) const { return 0.0f; }
     __device__ void store(int r, float v) const { y[r] = v; }
+    __host__ int matrices() const { return 1; }
+    __host__ void plan_waves(int) {}
+    __device__ const ExpertRows& for_wave(int&, int&, int&) const { return *this; }
 };
 
 }  // namespace q3x

@@ -14,6 +14,8 @@ void check(int status, const char* what, const char* file, int line) {
 }
 
 #define Q3X_HIP_CHECK(call) check((call), #call, __FILE__, __LINE__)
+// Fatal invariant, like Q3X_ASSERT (internal.h:76-85).
+#define Q3X_HIP_ASSERT(cond) check((cond) ? Q3X_HIP_OK : Q3X_HIP_EINVAL, #cond, __FILE__, __LINE__)
 
 }  // namespace
 
@@ -25,6 +27,17 @@ void mv(const Linear& linear, const float* input, float* output, hipStream_t str
 void mv_add(const Linear& linear, const float* input, float* output, hipStream_t stream) {
     Q3X_HIP_CHECK(q3x_hip_mv(linear.weight, linear.type, linear.rows, linear.columns, input, output, 1,
                              stream));
+}
+
+void projections(const Linear* linears, float* const* outputs, int count, const float* input,
+                 hipStream_t stream) {
+    Q3X_HIP_ASSERT(count >= 1 && count <= Q3X_HIP_MV_MULTI_MAX);
+    q3x_hip_mv_item items[Q3X_HIP_MV_MULTI_MAX];
+    for (int i = 0; i < count; ++i) {
+        Q3X_HIP_ASSERT(linears[i].type == linears[0].type && linears[i].columns == linears[0].columns);
+        items[i] = q3x_hip_mv_item{linears[i].weight, linears[i].rows, outputs[i], 0};
+    }
+    Q3X_HIP_CHECK(q3x_hip_mv_multi(items, count, linears[0].type, linears[0].columns, input, stream));
 }
 
 void batch_mv(const Linear& linear, const float* input, float* output, int count, bool add,

@@ -41,6 +41,12 @@ struct ExpertLinear {
 void mv(const Linear& linear, const float* input, float* output, hipStream_t stream);
 // output[rows] += W input (engine.cu:1547).
 void mv_add(const Linear& linear, const float* input, float* output, hipStream_t stream);
+// outputs[i] = linears[i] input for count (1..8) matrices of one type and
+// width in one launch: the projection helpers attention_projections (q, k,
+// v), ffn_projections (gate, up) and delta_projections (qkv, z, a, b)
+// (engine.cu:1599-1661).
+void projections(const Linear* linears, float* const* outputs, int count, const float* input,
+                 hipStream_t stream);
 // output[count, rows] (+)= input[count, columns] W^T (engine.cu:1568, without
 // the cuBLAS handle and BF16 staging buffer of the BF16 path).
 void batch_mv(const Linear& linear, const float* input, float* output, int count, bool add,

@@ -3,7 +3,8 @@
 //
 // Cases and tolerances follow tests/q4_cuda_test.cu (q4_mv_test :31-60,
 // router_test :109-131, expert_moe_test :62-107), tests/q8_cpu_test.cpp
-// (fixed 2x64 Q8_0 vector and embed, :271-318) and tests/q4_cpu_test.cpp
+// (fixed 2x64 Q8_0 vector and embed, :271-318; plus the projection helper of
+// engine.cu:1607-1619 on the same matrix) and tests/q4_cpu_test.cpp
 // (q4_math_test :138-178).  Exit 0 = pass, 77 = no GPU (the reference CI's
 // skip code, .github/workflows/ci.yml:53-55), anything else = failure.
 #include <cmath>
@@ -137,6 +138,19 @@ void q8_fixed_test() {
     for (int block = 0; block < 2; ++block)
         for (int index = 0; index < 32; ++index)
             CHECK(embedding[block * 32 + index] == decoded_scales[2 + block] * blocks[2 + block].values[index]);
+
+    // projections: the same matrix twice plus its first row alone, one launch,
+    // equal to mv bit for bit.
+    {
+        float* outs[3] = {device_floats(2), device_floats(2), device_floats(1)};
+        const qwen3x_hip::Linear linears[3] = {matrix, matrix, {weight, 1, 64, qwen3x_hip::MATRIX_Q8_0}};
+        qwen3x_hip::projections(linears, outs, 3, device_input, nullptr);
+        for (int i = 0; i < 3; ++i) {
+            const auto got = host_copy(outs[i], i < 2 ? 2 : 1);
+            for (size_t r = 0; r < got.size(); ++r) CHECK(std::memcmp(&got[r], &output[r], sizeof(float)) == 0);
+            HIP_OK(hipFree(outs[i]));
+        }
+    }
 
     // batch_mv: three identical tokens give the matvec result per token.
     float batch_input[3 * 64];

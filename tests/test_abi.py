@@ -78,6 +78,20 @@ def test_invalid_arguments_are_rejected_without_device_work():
     assert lib.q3x_hip_moe_routed(P, P, 2, 256, 2048, 500, P, 2048, P, P, 8, P, 0, P, ws, N) == q3x.EINVAL
     assert lib.q3x_hip_moe_routed(P, P, 2, 4, 2048, 512, P, 1, P, P, 5, P, 0, P, ws, N) == q3x.EINVAL
     assert lib.q3x_hip_moe_routed(P, P, 0, 4, 2048, 512, P, 1, P, P, 2, P, 0, P, ws, N) == q3x.ENOTSUP
+    item = q3x.MvItem(0x1000, 4, 0x1000, 0)
+    items = (q3x.MvItem * 9)(*([item] * 9))
+    ip = ctypes.cast(items, ctypes.c_void_p)
+    assert lib.q3x_hip_mv_multi(ip, 0, 1, 64, P, N) == q3x.EINVAL
+    assert lib.q3x_hip_mv_multi(ip, 9, 1, 64, P, N) == q3x.EINVAL          # more than 8 matrices
+    assert lib.q3x_hip_mv_multi(N, 1, 1, 64, P, N) == q3x.EINVAL
+    assert lib.q3x_hip_mv_multi(ip, 2, 1, 48, P, N) == q3x.EINVAL
+    assert lib.q3x_hip_mv_multi(ip, 2, 1, 64, N, N) == q3x.EINVAL
+    assert lib.q3x_hip_mv_multi(ip, 2, 0, 64, P, N) == q3x.ENOTSUP
+    bad = (q3x.MvItem * 2)(item, q3x.MvItem(0x1000, 0, 0x1000, 0))
+    assert lib.q3x_hip_mv_multi(ctypes.cast(bad, ctypes.c_void_p), 2, 2, 64, P, N) == q3x.EINVAL
+    bad = (q3x.MvItem * 2)(item, q3x.MvItem(None, 4, 0x1000, 0))
+    assert lib.q3x_hip_mv_multi(ctypes.cast(bad, ctypes.c_void_p), 2, 2, 64, P, N) == q3x.EINVAL
+    assert ctypes.sizeof(q3x.MvItem) == 32  # struct q3x_hip_mv_item on LP64
     assert lib.q3x_hip_quantize(1, N, 4, 64, P, N) == q3x.EINVAL
     assert lib.q3x_hip_quantize(2, P, 4, 48, P, N) == q3x.EINVAL
 

@@ -184,6 +184,53 @@ def test_mv_zero_rows_are_exactly_zero():
         assert np.all(host(y) == 0.0)
 
 
+# -------------------------------------------------------------- mv_multi ----
+
+@pytest.mark.parametrize("type_,cols,rows_list,acc", [
+    (Q8_0, 4096, [4096, 1024, 1024], [False, False, True]),    # q, k, v (v accumulates)
+    (Q4_0, 5120, [3000, 3000], [False, False]),                # gate, up
+    (Q8_0, 2048, [1, 7, 100, 2049, 33, 5, 64, 900], [True, False] * 4),  # 8 matrices
+    (Q4_0, 512, [70, 3], [False, True]),                       # 16 lanes per row
+    (Q8_0, 96, [5, 3], [False, True]),                         # rows not 16-byte multiples: generic path
+])
+def test_mv_multi_equals_separate_mv(type_, cols, rows_list, acc):
+    torch = _torch()
+    rng = np.random.default_rng(cols + len(rows_list) + type_)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    xd = dev(x)
+    mats, outs, seps = [], [], []
+    for i, rows in enumerate(rows_list):
+        w = random_blocks(rng, type_, rows, cols)
+        start = rng.normal(0, 1, rows).astype(np.float32)
+        mats.append((w, q3x.Linear(dev(w), rows, cols, type_)))
+        outs.append(dev(start))
+        seps.append(dev(start))
+    say(f"mv_multi type={type_} cols={cols} rows={rows_list}")
+    q3x.mv_multi([m for _, m in mats], xd, outs, acc)
+    for (w, m), y, a in zip(mats, seps, acc):
+        q3x.mv(m, xd, y, a)
+    for (w, m), got, sep, a, in zip(mats, outs, seps, acc):
+        g = host(got)
+        assert np.array_equal(bits(g), bits(host(sep))), f"rows={m.rows}: mv_multi differs from mv"
+        want = oracle.mv(w, type_, m.rows, cols, x)
+        wd = dequant_numpy(w, type_, m.rows, cols)
+        if not a:
+            check_bound(g, want, wd, x, f"mv_multi {m.rows}x{cols}")
+
+
+def test_mv_multi_rejects_mixed_or_bad_items():
+    torch = _torch()
+    w = torch.zeros(34 * 4, dtype=torch.uint8, device="cuda:0")
+    x = torch.zeros(128, dtype=torch.float32, device="cuda:0")
+    y = torch.zeros(4, dtype=torch.float32, device="cuda:0")
+    with pytest.raises(ValueError):
+        q3x.mv_multi([q3x.Linear(w, 1, 128, Q8_0), q3x.Linear(w, 1, 64, Q8_0)], x, [y, y])
+    with pytest.raises(ValueError):
+        q3x.mv_multi([q3x.Linear(w, 1, 128, Q8_0)] * 9, x, [y] * 9)
+    with pytest.raises(q3x.Q3xHipError):
+        q3x.mv_multi([q3x.Linear(w, 0, 128, Q8_0)], x, [y])
+
+
 # ------------------------------------------------------------------ GEMM ----
 
 GEMM_CASES = [(Q8_0, 64, 128, 1), (Q8_0, 130, 256, 5), (Q8_0, 300, 512, 129), (Q4_0, 256, 1024, 37),
