@@ -368,7 +368,7 @@ def main():
                    "weight_copies_rotated": head["copies"], "frac_of_hbm_peak": round(head["value"] / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(lm["GBps"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(lm["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "mv_pipe_kernel<Q8_0, 64 lanes/row, 2 rows/step, 12 waves/CU> on lm_head 151936x4096",
+                     "kernel": "mv_pipe_kernel<Q8_0, 64 lanes/row, 1 row/step, 2x16 waves/CU> on lm_head 151936x4096",
                      "algorithmic_bytes_per_launch": lm["bytes"], "avg_launch_ms": round(lm["ms"], 5),
                      "traffic_source": "profiles/pmc_traffic_lm_head_q8_0.txt" if traffic else None},
     }

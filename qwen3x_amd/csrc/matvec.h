@@ -515,7 +515,7 @@ inline int launch_staged(const Rows& rows, int nrows, int bpr, hipStream_t strea
 // every wave gets B full batches (balanced), spreading the waves over all
 // CUs (fewer per workgroup) when there are fewer than 256 workgroups' worth.
 template <uint32_t QT, int LPR, int R, class Rows>
-inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_t stream) {
+inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_t stream, int per_cu = 1) {
     using S = PipeShape<QT, LPR>;
     auto kernel = mv_pipe_kernel<QT, LPR, R, Rows>;
     static const bool lds_ready =
@@ -528,12 +528,13 @@ inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_
     }
     if (lds > kLdsPerCU) return Q3X_HIP_ENOTSUP;  // x too long for LDS
     if (lds > 64 * 1024 && !lds_ready) return Q3X_HIP_ERUNTIME;
+    if (lds * per_cu > kLdsPerCU) per_cu = 1;
     const long long rs = static_cast<long long>(S::G) * R;
-    const long long gw_max = static_cast<long long>(kCUs) * wpb;
+    const long long gw_max = static_cast<long long>(kCUs) * per_cu * wpb;
     const long long batches = (nrows + gw_max * rs - 1) / (gw_max * rs);
     const long long waves =
         std::max<long long>((nrows + batches * rs - 1) / (batches * rs), rows.matrices());
-    const int wpb_used = static_cast<int>(std::min<long long>(wpb, (waves + kCUs - 1) / kCUs));
+    const int wpb_used = static_cast<int>(std::min<long long>(wpb, (waves + kCUs * per_cu - 1) / (kCUs * per_cu)));
     const int grid = static_cast<int>((waves + wpb_used - 1) / wpb_used);
     lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb_used) * S::WAVE_LDS;
     Rows planned = rows;
@@ -542,15 +543,18 @@ inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_
     return launch_status();
 }
 
-// Shapes measured on MI355X: one row per step and 16 waves per CU while a
-// wave has about one row; two rows per step and 12 waves per CU beyond.
+// Shapes measured on MI355X (rows per step x waves per workgroup x
+// workgroups per CU): Q8_0 streams best with one row per step; Q4_0, whose
+// rows are half as long, with two; large matrices gain from a second
+// 16-wave workgroup per CU (more, shorter waves: the grid drains evenly).
 template <uint32_t QT, class Rows>
 inline int launch_pipe_for(const Rows& rows, int nrows, int bpr, hipStream_t stream) {
     if (bpr <= 16) return launch_pipe<QT, 16, 1>(rows, nrows, bpr, 16, stream);
     if (bpr <= 32) return launch_pipe<QT, 32, 1>(rows, nrows, bpr, 16, stream);
-    const int small = QT == Q3X_HIP_MATRIX_Q8_0 ? 6144 : 4096;
-    if (nrows <= small) return launch_pipe<QT, 64, 1>(rows, nrows, bpr, 16, stream);
-    return launch_pipe<QT, 64, 2>(rows, nrows, bpr, 12, stream);
+    if (QT == Q3X_HIP_MATRIX_Q8_0)
+        return launch_pipe<QT, 64, 1>(rows, nrows, bpr, 16, stream, nrows >= 8192 ? 2 : 1);
+    if (nrows <= 4096) return launch_pipe<QT, 64, 1>(rows, nrows, bpr, 16, stream);
+    return launch_pipe<QT, 64, 2>(rows, nrows, bpr, 16, stream, 2);
 }
 
 template <uint32_t QT, class Rows>
