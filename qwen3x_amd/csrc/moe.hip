@@ -8,9 +8,11 @@
 //
 // Here the router runs one wavefront per token.  The routed matmul has two
 // shapes:
-//   decode (tokens == 1): the selected experts are one tall virtual matrix
-//     for the staged matvec (matvec.h), then SwiGLU, the down matvec, and a
-//     combine in slot order;
+//   decode (tokens == 1): the selected experts' gate_up rows are one tall
+//     virtual matrix for the pipelined matvec (matvec.h; its waves split
+//     evenly over the slots), then one kernel applies SwiGLU to the slots'
+//     gate_up outputs in LDS, runs every slot's down row for each output row
+//     and combines the slots in order (moe_down_combine_kernel);
 //   prefill (tokens > 1): the (token, slot) pairs are grouped by expert with
 //     a stable counting sort (deterministic positions), each expert's group is
 //     cut into 32-token tiles, and one grouped FP32-MFMA GEMM launch (gemm.h)
@@ -129,7 +131,7 @@ inline MoeLayout moe_layout(int tokens, int experts, int top_k, int H, int I) {
     const size_t P = static_cast<size_t>(tokens) * top_k;
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t at = off; off = align_up(off + bytes, 256); return at; };
-    if (tokens > 1) {
+    {  // grouping arrays (also for one token: the fallback of unaligned decode shapes)
         L.max_tiles = static_cast<int>(P / kGrpBM + std::min<size_t>(experts, P) + 1);
         L.ntiles = take(sizeof(int));
         L.nvalid = take(sizeof(int));
@@ -319,31 +321,172 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     else Y[idx] = acc;
 }
 
+// Decode (one token): the down projection of every selected expert, with
+// SwiGLU applied to its input on the way into LDS (engine.cpp:415-416) and
+// the slot-order combine (engine.cpp:411, 418-419: out = 0, then
+// out += w * d per slot), in one kernel.  Wave gw computes the output rows
+// i = gw, gw + GW, ...: for each, the rows (slot s, i) of the top_k experts,
+// G = 64 / LPR slots at a time (one row group of LPR lanes per slot, one lane
+// per 32-weight block of a pass), then lane 0 adds the slots' results in
+// slot order from zero.  Slots whose id is out of range are skipped.
+template <uint32_t QT, int LPR>
+__global__ __launch_bounds__(512) void moe_down_combine_kernel(
+    const uint8_t* __restrict__ down, size_t expert_bytes, size_t row_bytes, int experts,
+    const int* __restrict__ ids, const float* __restrict__ weights, int top_k, const float* __restrict__ gu,
+    int I, int H, float* __restrict__ Y, int accumulate) {
+    using S = PipeShape<QT, LPR>;
+    constexpr int BB = S::BB, G = S::G, J = S::J;
+    constexpr int IT = (kRouterMaxTopK + G - 1) / G;  // slot groups at most
+    constexpr bool Q4 = QT == Q3X_HIP_MATRIX_Q4_0;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
+
+    const int bpr = I / kBlock;
+    const uint32_t xs_bytes = pipe_x_bytes(QT, bpr);  // one slot's activations (+ Q4 references)
+    const uint32_t ref_off = (x_lds_bytes(bpr) + 15u) & ~15u;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int wpb = blockDim.x / kWave;
+    const int gw = blockIdx.x * wpb + wave;
+    const int GW = gridDim.x * wpb;
+    const int g = lane / LPR;
+    const int li = lane % LPR;
+    uint8_t* const wl = lds_dyn + top_k * xs_bytes + wave * S::WAVE_LDS;
+
+    // h = silu(gate) * up for every slot, into the padded x layout.
+    for (int c = threadIdx.x; c < top_k * I; c += blockDim.x) {
+        const int slot = c / I, j = c - slot * I;
+        const float* row = gu + static_cast<size_t>(slot) * 2 * I;
+        *reinterpret_cast<float*>(lds_dyn + slot * xs_bytes + x_block_offset(j >> 5) + 4 * (j & 31)) =
+            silu_ref(row[j]) * row[I + j];
+    }
+    __syncthreads();
+    if (Q4) {
+        for (int c = threadIdx.x; c < top_k * bpr; c += blockDim.x) {
+            const int slot = c / bpr, b = c - slot * bpr;
+            uint8_t* xs = lds_dyn + slot * xs_bytes;
+            reinterpret_cast<float*>(xs + ref_off)[b] =
+                q4_mix_reference(reinterpret_cast<const float*>(xs + x_block_offset(b)));
+        }
+        __syncthreads();
+    }
+
+    const int npass = (bpr + LPR - 1) / LPR;
+    const int groups = (top_k + G - 1) / G;
+    for (int i = gw; i < H; i += GW) {
+        float acc[IT];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) acc[it] = 0.0f;
+        for (int pass = 0; pass < npass; ++pass) {
+            const int b0 = pass * LPR;
+            const int nblk = min(LPR, bpr - b0);
+            const int col = li < nblk ? b0 + li : 0;
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                if (it >= groups) break;
+                u32x4 pre[G][J];
+#pragma unroll
+                for (int gg = 0; gg < G; ++gg) {
+                    const int slot = it * G + gg;
+                    const int e = slot < top_k ? __builtin_amdgcn_readfirstlane(ids[slot]) : -1;
+                    const bool ok = e >= 0 && e < experts;
+                    const uint8_t* src = ok ? down + static_cast<size_t>(e) * expert_bytes +
+                                                  static_cast<size_t>(i) * row_bytes + static_cast<size_t>(b0) * BB
+                                            : down;
+                    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+                        const_cast<uint8_t*>(src), 0, ok ? nblk * BB : 0, kBufferFlags);
+#pragma unroll
+                    for (int j = 0; j < J; ++j)
+                        pre[gg][j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * lane + 1024 * j, 0, kNonTemporal);
+                }
+                // x of this lane's slot, block col.
+                const int my_slot = it * G + g;
+                const uint8_t* xs = lds_dyn + (my_slot < top_k ? my_slot : 0) * xs_bytes;
+                float xv[32];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const f32x4 t = *reinterpret_cast<const f32x4*>(xs + x_block_offset(col) + 16 * q);
+                    xv[4 * q + 0] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
+                }
+                const float xref = Q4 ? reinterpret_cast<const float*>(xs + ref_off)[col] : 0.0f;
+#pragma unroll
+                for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+                    for (int j = 0; j < J; ++j)
+                        *reinterpret_cast<u32x4*>(wl + gg * S::SEGP + 1024 * j + 16 * lane) = pre[gg][j];
+                wave_lds_sync();
+                if (li < nblk && my_slot < top_k) {
+                    const uint32_t p = g * S::SEGP + li * BB;
+                    acc[it] += Q4 ? block_dot_q4_mix(wl, p, xv, xref) : block_dot_q8(wl, p, xv);
+                }
+                wave_lds_sync();
+            }
+        }
+        // Slot results to lane 0, then the ordered combine.
+        float out = 0.0f;
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            if (it >= groups) break;
+            const float total = group_sum<LPR>(acc[it]);
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg) {
+                const int slot = it * G + gg;
+                const float d = __shfl(total, gg * LPR);
+                if (slot < top_k) {
+                    const int e = ids[slot];
+                    if (e >= 0 && e < experts) out = fmaf(weights[slot], d, out);
+                }
+            }
+        }
+        if (lane == 0) Y[i] = accumulate ? Y[i] + out : out;
+    }
+}
+
+template <uint32_t QT, int LPR>
+int launch_moe_down(const uint8_t* down, int experts, int H, int I, const int* ids, const float* weights,
+                    int top_k, const float* gu, float* Y, int accumulate, hipStream_t stream) {
+    using S = PipeShape<QT, LPR>;
+    constexpr int kWaves = 8;
+    const size_t row_bytes = static_cast<size_t>(I / kBlock) * (QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes);
+    const size_t lds = static_cast<size_t>(top_k) * pipe_x_bytes(QT, I / kBlock) + kWaves * S::WAVE_LDS;
+    if (lds > kLdsPerCU) return Q3X_HIP_ENOTSUP;
+    auto kernel = moe_down_combine_kernel<QT, LPR>;
+    static const bool lds_ready =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(kLdsPerCU)) == hipSuccess;
+    if (lds > 64 * 1024 && !lds_ready) return Q3X_HIP_ERUNTIME;
+    const int grid = std::min((H + kWaves - 1) / kWaves, kCUs * 2);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWaves * kWave), lds, stream, down, row_bytes * H, row_bytes,
+                       experts, ids, weights, top_k, gu, I, H, Y, accumulate);
+    return launch_status();
+}
+
 template <uint32_t QT>
 int moe_decode(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
                const int* ids, const float* weights, int top_k, float* Y, int accumulate,
                uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
     constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
     float* gu = reinterpret_cast<float*>(ws + L.gu);
-    float* h = reinterpret_cast<float*>(ws + L.h);
-    float* d = reinterpret_cast<float*>(ws + L.d);
     const size_t gu_row = static_cast<size_t>(H / kBlock) * BB;
     const size_t down_row = static_cast<size_t>(I / kBlock) * BB;
-    ExpertRows<true> gate{gate_up, gu_row * 2 * I, gu_row, 2 * I, experts, ids, X, 0, gu};
-    const bool gate_staged = aligned(gate_up, 16) && aligned(X, 16) && gu_row % 16 == 0;
-    int status = launch_mv<QT>(gate, top_k * 2 * I, H / kBlock, gate_staged, stream);
-    if (status != Q3X_HIP_OK) return status;
-    const int sw = top_k * I;
-    hipLaunchKernelGGL(swiglu_kernel, dim3((sw + 255) / 256), dim3(256), 0, stream, gu, h, I, top_k,
-                       nullptr);
-    if ((status = launch_status()) != Q3X_HIP_OK) return status;
-    ExpertRows<false> dn{down, down_row * H, down_row, H, experts, ids, h, static_cast<size_t>(I), d};
-    const bool down_staged = aligned(down, 16) && down_row % 16 == 0;
-    status = launch_mv<QT>(dn, top_k * H, I / kBlock, down_staged, stream);
-    if (status != Q3X_HIP_OK) return status;
-    hipLaunchKernelGGL(combine_kernel, dim3((H + 255) / 256), dim3(256), 0, stream, d, nullptr, ids,
-                       experts, weights, 1, top_k, H, Y, accumulate);
-    return launch_status();
+    const bool staged = aligned(gate_up, 16) && aligned(X, 16) && gu_row % 16 == 0 && aligned(down, 16) &&
+                        down_row % 16 == 0;
+    if (staged) {
+        ExpertRows gate{gate_up, gu_row * 2 * I, gu_row, 2 * I, experts, ids, top_k, X, gu, {}};
+        int status = launch_pipe_for<QT>(gate, top_k * 2 * I, H / kBlock, stream);
+        if (status == Q3X_HIP_OK) {
+            const int bpr = I / kBlock;
+            status = bpr <= 16   ? launch_moe_down<QT, 16>(down, experts, H, I, ids, weights, top_k, gu, Y,
+                                                           accumulate, stream)
+                     : bpr <= 32 ? launch_moe_down<QT, 32>(down, experts, H, I, ids, weights, top_k, gu, Y,
+                                                           accumulate, stream)
+                                 : launch_moe_down<QT, 64>(down, experts, H, I, ids, weights, top_k, gu, Y,
+                                                           accumulate, stream);
+        }
+        if (status != Q3X_HIP_ENOTSUP) return status;
+    }
+    // Unaligned or very wide shapes: the caller takes the grouped path, which
+    // handles one token too.
+    return Q3X_HIP_ENOTSUP;
 }
 
 template <uint32_t QT>
@@ -449,11 +592,12 @@ extern "C" int q3x_hip_moe_routed(const void* gate_up, const void* down, uint32_
     const uint8_t* dn = static_cast<const uint8_t*>(down);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     if (tokens == 1) {
-        return type == Q3X_HIP_MATRIX_Q8_0
-                   ? moe_decode<Q3X_HIP_MATRIX_Q8_0>(gu, dn, experts, H, I, X, ids, weights, top_k, Y,
-                                                     accumulate, ws, L, stream)
-                   : moe_decode<Q3X_HIP_MATRIX_Q4_0>(gu, dn, experts, H, I, X, ids, weights, top_k, Y,
-                                                     accumulate, ws, L, stream);
+        const int status = type == Q3X_HIP_MATRIX_Q8_0
+                               ? moe_decode<Q3X_HIP_MATRIX_Q8_0>(gu, dn, experts, H, I, X, ids, weights, top_k, Y,
+                                                                 accumulate, ws, L, stream)
+                               : moe_decode<Q3X_HIP_MATRIX_Q4_0>(gu, dn, experts, H, I, X, ids, weights, top_k, Y,
+                                                                 accumulate, ws, L, stream);
+        if (status != Q3X_HIP_ENOTSUP) return status;
     }
     return type == Q3X_HIP_MATRIX_Q8_0
                ? moe_grouped<Q3X_HIP_MATRIX_Q8_0>(gu, dn, experts, H, I, X, tokens, ids, weights, top_k, Y,

@@ -39,13 +39,14 @@ struct DenseRows {
 // launch): y[r] = W[r] x, or y[r] += W[r] x when `accumulate`.
 struct OneMatrix {
     static constexpr bool kSharedInput = true;
-    const uint8_t* w;
+    const uint8_t* w;  // null: every row reads as zeros (an expert id out of range)
     size_t row_bytes;
     const float* x;
     float* y;
     bool accumulate;
-    __device__ const uint8_t* row(int r) const { return w + static_cast<size_t>(r) * row_bytes; }
-    __device__ const uint8_t* any() const { return w; }
+    const uint8_t* any_w;  // a valid address for empty buffer ranges
+    __device__ const uint8_t* row(int r) const { return w ? w + static_cast<size_t>(r) * row_bytes : nullptr; }
+    __device__ const uint8_t* any() const { return any_w; }
     __device__ const float* input(int) const { return x; }
     __device__ float previous(int r) const { return accumulate ? y[r] : 0.0f; }
     __device__ void store(int r, float v) const { y[r] = v; }
@@ -129,44 +130,55 @@ struct MultiRows {
         gw -= first_wave;
         GW = last_wave - first_wave;
         nrows = last_row - first_row;
-        return OneMatrix{wk, row_bytes, x, yk, ((accumulate_mask >> k) & 1u) != 0};
+        return OneMatrix{wk, row_bytes, x, yk, ((accumulate_mask >> k) & 1u) != 0, wk};
     }
 };
 
-// The experts one token selected, viewed as one tall matrix: virtual row
-// r = slot * rows_per_expert + j is row j of expert ids[slot] in the pool
-// [experts, rows_per_expert, cols].  An id outside [0, experts) yields a
-// null row, which the kernels read as zeros (the reference CUDA kernels skip
-// such slots, engine.cu:1198, 1235).  SHARED: every slot reads x (gate_up);
-// otherwise slot s reads x + s * x_slot_stride (down).  The result of
-// virtual row r goes to y[r].
-template <bool SHARED>
+// The experts one token selected, viewed as one tall matrix for the gate_up
+// matvec of a decode step: virtual row r = slot * rows_per_expert + j is row
+// j of expert ids[slot] in the pool [experts, rows_per_expert, cols], and
+// every slot reads x.  The launch's waves are split evenly over the slots
+// (plan_waves), so a wave reads its slot's expert id once, at the start.  An
+// id outside [0, experts) reads as zeros (the reference CUDA kernels skip such
+// slots, engine.cu:1198, 1235).  The result of virtual row r goes to y[r].
 struct ExpertRows {
-    static constexpr bool kSharedInput = SHARED;
+    static constexpr bool kSharedInput = true;
+    static constexpr int kMaxSlots = 8;
     const uint8_t* pool;
     size_t expert_bytes;
     size_t row_bytes;
     int rows_per_expert;
     int experts;
     const int* ids;
+    int slots;
     const float* x;
-    size_t x_slot_stride;
     float* y;
-    __device__ int slot(int r) const { return r / rows_per_expert; }
-    __device__ const uint8_t* row(int r) const {
-        const int s = slot(r);
-        const int e = ids[s];
-        if (e < 0 || e >= experts) return nullptr;
-        return pool + static_cast<size_t>(e) * expert_bytes +
-               static_cast<size_t>(r - s * rows_per_expert) * row_bytes;
+    int wave_end[kMaxSlots];
+
+    __host__ int matrices() const { return slots; }
+    __host__ void plan_waves(int GW) {
+        for (int s = 0; s < kMaxSlots; ++s)
+            wave_end[s] = static_cast<int>((static_cast<long long>(GW) * (s < slots ? s + 1 : slots)) / slots);
     }
-    __device__ const uint8_t* any() const { return pool; }
-    __device__ const float* input(int r) const { return SHARED ? x : x + slot(r) * x_slot_stride; }
-    __device__ float previous(int) const { return 0.0f; }
-    __device__ void store(int r, float v) const { y[r] = v; }
-    __host__ int matrices() const { return 1; }
-    __host__ void plan_waves(int) {}
-    __device__ const ExpertRows& for_wave(int&, int&, int&) const { return *this; }
+    __device__ OneMatrix for_wave(int& gw, int& GW, int& nrows) const {
+        int s = 0;
+#pragma unroll
+        for (int i = 1; i < kMaxSlots; ++i)
+            if (i < slots && gw >= wave_end[i - 1]) s = i;
+        int first = 0, last = wave_end[0];
+#pragma unroll
+        for (int i = 1; i < kMaxSlots; ++i) {
+            int fw = wave_end[i - 1], lw = wave_end[i];
+            asm volatile("" : "+s"(fw), "+s"(lw));  // keep the table in scalar registers
+            if (i == s) { first = fw; last = lw; }
+        }
+        gw -= first;
+        GW = last - first;
+        nrows = rows_per_expert;
+        const int e = __builtin_amdgcn_readfirstlane(ids[s]);
+        const uint8_t* w = e >= 0 && e < experts ? pool + static_cast<size_t>(e) * expert_bytes : nullptr;
+        return OneMatrix{w, row_bytes, x, y + static_cast<size_t>(s) * rows_per_expert, false, pool};
+    }
 };
 
 }  // namespace q3x
