@@ -22,6 +22,7 @@
 namespace q3x {
 
 constexpr int kGemmPad = 4;            // floats of padding per LDS tile row
+constexpr int kXcds = 8;               // MI355X: 8 XCDs of 32 CUs
 constexpr int kGemmLd = 32 + kGemmPad; // LDS row pitch (floats)
 
 struct GemmTile {
@@ -35,6 +36,10 @@ struct GemmTile {
 // [part*N, part*N + N), N = 32/PARTS.  Q4_0: nibble bytes
 // [NB*part, NB*part + NB), NB = 16/PARTS, i.e. elements NB*part + j (low
 // nibbles) and 16 + NB*part + j (high nibbles).  `blk` is 2-byte aligned.
+// A part's N values go to the N consecutive LDS columns [part*N, part*N + N)
+// (16-byte stores without bank conflicts); for Q4_0 that permutes the k order
+// inside a block, and the activation tile is stored with the same
+// permutation (a_chunk), so the products pair up unchanged.
 template <uint32_t QT, int PARTS>
 struct BlockPart {
     static constexpr int N = 32 / PARTS;                    // elements
@@ -65,10 +70,13 @@ struct BlockPart {
         }
     }
     // Column within the block of output element e.
-    __device__ static __forceinline__ int column(int part, int e) {
-        if (QT == Q3X_HIP_MATRIX_Q8_0) return part * N + e;
-        constexpr int NB = N / 2;
-        return e < NB ? part * NB + e : 16 + part * NB + (e - NB);
+    __device__ static __forceinline__ int column(int part, int e) { return part * N + e; }
+    // LDS chunk (4 columns) of the activations' 16-byte chunk c (elements
+    // 4c..4c+3).  Q4_0 with two parts: elements 0-7 | 16-23 | 8-15 | 24-31
+    // go to columns 0-7 | 8-15 | 16-23 | 24-31, i.e. chunks 2,3 <-> 4,5.
+    __device__ static __forceinline__ int a_chunk(int c) {
+        if (QT == Q3X_HIP_MATRIX_Q8_0 || PARTS == 1) return c;
+        return (c & 1) | ((c & 2) << 1) | ((c & 4) >> 1);
     }
 };
 
@@ -94,9 +102,22 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
     __shared__ __attribute__((aligned(16))) float As[2][BM * kGemmLd];
     __shared__ __attribute__((aligned(16))) float Bs[2][BN * kGemmLd];
 
+    // Tile coordinates: a 2-D grid (x = weight-row tiles, y = A-row tiles), or
+    // a 1-D grid over gx * gy tiles (Policy::kLinearGrid) remapped so that
+    // each XCD (workgroups are dealt to the 8 XCDs round-robin) takes a
+    // contiguous run of tiles: workgroups that share an A tile (same y,
+    // consecutive x) then share one XCD's L2.
+    int bx = blockIdx.x, by = blockIdx.y;
+    if constexpr (Policy::kLinearGrid) {
+        const int total = gridDim.x, L = blockIdx.x;
+        const int q = total / kXcds, r = total % kXcds, xcd = L % kXcds, k = L / kXcds;
+        const int t = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + k;
+        bx = t % pol.tiles_x;
+        by = t / pol.tiles_x;
+    }
     GemmTile tile;
-    if (!pol.tile(blockIdx.y, BM, tile)) return;
-    const int n0 = blockIdx.x * BN;
+    if (!pol.tile(by, BM, tile)) return;
+    const int n0 = bx * BN;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
@@ -142,7 +163,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
         for (int i = 0; i < A_PER_T; ++i) {
             const int idx = tid + i * NT;
             if (idx < A_VEC)
-                *reinterpret_cast<f32x4*>(&As[buf][(idx >> 3) * kGemmLd + 4 * (idx & 7)]) = a_reg[i];
+                *reinterpret_cast<f32x4*>(&As[buf][(idx >> 3) * kGemmLd + 4 * Part::a_chunk(idx & 7)]) = a_reg[i];
         }
 #pragma unroll
         for (int p = 0; p < B_PASSES; ++p) {

@@ -11,6 +11,8 @@ namespace q3x {
 
 // Token rows X[count, cols] against one weight matrix.
 struct DenseGemm {
+    static constexpr bool kLinearGrid = true;
+    int tiles_x;  // weight-row tiles of the launch
     const float* X;
     int cols;
     int count;
@@ -38,36 +40,29 @@ struct DenseGemm {
     }
 };
 
-// Large tiles: 2x2 waves of 2x2 32x32 tiles = 128 tokens x 128 weight rows.
-// Small tiles (2x2 waves of one 32x32 tile = 64 x 64) when large tiles would
-// give fewer than two workgroups per CU (256 CUs).
-constexpr int kMaxGridY = 65535;
-constexpr int kFillWorkgroups = 512;
-
-template <uint32_t QT, int TM, int TN>
+// Tile shapes (WM x WN waves, each TM x TN tiles of 32x32), measured on
+// MI355X over the prefill shapes: 128 x 128 tiles on 8 waves while the grid
+// has >= 4 such tiles per CU (e.g. N = 4096); below that 64 tokens x 128
+// weight rows on 8 waves for Q8_0 and 64 x 64 on 4 waves for Q4_0, whose
+// heavier dequantisation favours more, smaller workgroups.
+template <uint32_t QT, int WM, int WN, int TM, int TN>
 int launch_dense_gemm_tiles(const DenseGemm& base, hipStream_t stream) {
-    constexpr int BM = 2 * TM * 32, BN = 2 * TN * 32;
-    // Chunk the token dimension so grid.y stays within the launch limit.
-    const int chunk = kMaxGridY * BM;
-    for (int start = 0; start < base.count; start += chunk) {
-        DenseGemm part = base;
-        part.X = base.X + static_cast<size_t>(start) * base.cols;
-        part.Y = base.Y + static_cast<size_t>(start) * base.rows;
-        part.count = min(chunk, base.count - start);
-        const dim3 grid((base.rows + BN - 1) / BN, (part.count + BM - 1) / BM);
-        hipLaunchKernelGGL((gemm_mfma_kernel<QT, 2, 2, TM, TN, DenseGemm>), grid, dim3(4 * kWave), 0, stream,
-                           part, base.rows, base.cols);
-        const int status = launch_status();
-        if (status != Q3X_HIP_OK) return status;
-    }
-    return Q3X_HIP_OK;
+    constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
+    DenseGemm g = base;
+    g.tiles_x = (base.rows + BN - 1) / BN;
+    const long long tiles = static_cast<long long>(g.tiles_x) * ((base.count + BM - 1) / BM);
+    if (tiles > 0x7fffffffLL) return Q3X_HIP_EINVAL;
+    hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, WN, TM, TN, DenseGemm>), dim3(static_cast<unsigned>(tiles)),
+                       dim3(WM * WN * kWave), 0, stream, g, base.rows, base.cols);
+    return launch_status();
 }
 
 template <uint32_t QT>
 int launch_dense_gemm(const DenseGemm& g, hipStream_t stream) {
     const long long large = static_cast<long long>((g.rows + 127) / 128) * ((g.count + 127) / 128);
-    if (large >= kFillWorkgroups) return launch_dense_gemm_tiles<QT, 2, 2>(g, stream);
-    return launch_dense_gemm_tiles<QT, 1, 1>(g, stream);
+    if (large >= 4LL * kCUs) return launch_dense_gemm_tiles<QT, 2, 4, 2, 1>(g, stream);
+    if (QT == Q3X_HIP_MATRIX_Q8_0) return launch_dense_gemm_tiles<QT, 2, 4, 1, 1>(g, stream);
+    return launch_dense_gemm_tiles<QT, 2, 2, 1, 1>(g, stream);
 }
 
 }  // namespace q3x
@@ -92,7 +87,7 @@ extern "C" int q3x_hip_gemm(const void* w, uint32_t type, int rows, int cols, co
         }
         return Q3X_HIP_OK;
     }
-    DenseGemm g{X, cols, count, static_cast<const uint8_t*>(w), row_bytes, Y, rows, accumulate != 0};
+    DenseGemm g{0, X, cols, count, static_cast<const uint8_t*>(w), row_bytes, Y, rows, accumulate != 0};
     return type == Q3X_HIP_MATRIX_Q8_0 ? launch_dense_gemm<Q3X_HIP_MATRIX_Q8_0>(g, stream)
                                        : launch_dense_gemm<Q3X_HIP_MATRIX_Q4_0>(g, stream);
 }

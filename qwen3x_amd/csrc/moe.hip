@@ -28,9 +28,10 @@ constexpr int kRouterMaxExperts = 1024;
 constexpr int kRouterMaxTopK = 8;          // q3x_model::MAX_TOP_K (model_config.h:14)
 constexpr int kGroupThreads = 1024;
 constexpr int kChunk = 1024;               // pairs per grouping chunk
-// Grouped GEMM: 1 x 4 waves of one 32x32 tile -> 32 pairs x 128 weight rows
-// (experts average 64 pairs at 2048 tokens, so short tiles waste little).
-constexpr int kGrpWM = 1, kGrpWN = 4, kGrpTM = 1, kGrpTN = 1;
+// Grouped GEMM: 2 x 4 waves of one 32x32 tile -> 64 pairs x 128 weight rows
+// (measured ahead of 32-pair tiles, which waste fewer rows of an expert's
+// last tile but stream the weights twice as often per pair).
+constexpr int kGrpWM = 2, kGrpWN = 4, kGrpTM = 1, kGrpTN = 1;
 constexpr int kGrpBM = kGrpWM * kGrpTM * 32;
 constexpr int kGrpBN = kGrpWN * kGrpTN * 32;
 
@@ -246,6 +247,8 @@ __global__ __launch_bounds__(kChunk) void moe_scatter_kernel(const int* __restri
 // gathered (a_index[position] = source row) or taken in position order; the
 // weights are expert tile_expert[ty] of the pool; out[position, n].
 struct GroupedGemm {
+    static constexpr bool kLinearGrid = false;
+    int tiles_x;  // unused (2-D grid)
     const float* A;
     int a_cols;
     const int* a_index;
@@ -522,7 +525,7 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
     const size_t gu_row = static_cast<size_t>(H / kBlock) * BB;
     const size_t down_row = static_cast<size_t>(I / kBlock) * BB;
     const int tiles_bound = L.max_tiles;
-    GroupedGemm g1{X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
+    GroupedGemm g1{0, X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
                    ntiles, gu, 2 * I};
     hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm>),
                        dim3((2 * I + kGrpBN - 1) / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0,
@@ -533,7 +536,7 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
     hipLaunchKernelGGL(swiglu_kernel, dim3(sw_blocks), dim3(256), 0, stream, gu, h, I, 0,
                        static_cast<const int*>(nvalid));
     if ((status = launch_status()) != Q3X_HIP_OK) return status;
-    GroupedGemm g2{h, I, nullptr, down, down_row * H, down_row, tile_expert, tile_start, tile_count,
+    GroupedGemm g2{0, h, I, nullptr, down, down_row * H, down_row, tile_expert, tile_start, tile_count,
                    ntiles, d, H};
     hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm>),
                        dim3((H + kGrpBN - 1) / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0,
