@@ -229,11 +229,23 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const int n = n0 + (wn * TN + j) * 32 + li;
-            if (n >= rows) continue;
+            if constexpr (Policy::kPairedColumns) {
+                // Columns li and li + 16 of a 32-column tile form a pair
+                // (e.g. gate and up of one output feature): lane li < 16
+                // receives its partner's value and stores the pair.
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = (wm * TM + i) * 32 + 8 * (r >> 2) + 4 * kh + (r & 3);
-                if (m < tile.mcount) pol.store(tile, m, n, acc[i][j][r]);
+                for (int r = 0; r < 16; ++r) {
+                    const float partner = __shfl_xor(acc[i][j][r], 16);
+                    const int m = (wm * TM + i) * 32 + 8 * (r >> 2) + 4 * kh + (r & 3);
+                    if (!(li & 16) && n < rows && m < tile.mcount) pol.store_pair(tile, m, n, acc[i][j][r], partner);
+                }
+            } else {
+                if (n >= rows) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = (wm * TM + i) * 32 + 8 * (r >> 2) + 4 * kh + (r & 3);
+                    if (m < tile.mcount) pol.store(tile, m, n, acc[i][j][r]);
+                }
             }
         }
 }

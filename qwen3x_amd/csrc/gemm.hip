@@ -12,6 +12,7 @@ namespace q3x {
 // Token rows X[count, cols] against one weight matrix.
 struct DenseGemm {
     static constexpr bool kLinearGrid = true;
+    static constexpr bool kPairedColumns = false;
     int tiles_x;  // weight-row tiles of the launch
     const float* X;
     int cols;
@@ -38,6 +39,7 @@ struct DenseGemm {
         if (accumulate) *p += v;
         else *p = v;
     }
+    __device__ void store_pair(const GemmTile&, int, int, float, float) const {}
 };
 
 // Tile shapes (WM x WN waves, each TM x TN tiles of 32x32), measured on

@@ -553,6 +553,14 @@ inline int launch_pipe_for(const Rows& rows, int nrows, int bpr, hipStream_t str
     if (bpr <= 32) return launch_pipe<QT, 32, 1>(rows, nrows, bpr, 16, stream);
     if (QT == Q3X_HIP_MATRIX_Q8_0)
         return launch_pipe<QT, 64, 1>(rows, nrows, bpr, 16, stream, nrows >= 8192 ? 2 : 1);
+    // Short Q4_0 rows that 64-block passes would leave partly idle (e.g. 160
+    // blocks = 2.5 passes) take 32 lanes per row (two rows per pass).  The
+    // lanes per row depend on the row length only, so the per-row reduction
+    // order (and the result) is the same whatever the launch's row count.
+    if (bpr <= 256 && bpr % 64 != 0 && bpr % 32 == 0) {
+        if (nrows <= 4096) return launch_pipe<QT, 32, 1>(rows, nrows, bpr, 16, stream);
+        return launch_pipe<QT, 32, 2>(rows, nrows, bpr, 16, stream, 2);
+    }
     if (nrows <= 4096) return launch_pipe<QT, 64, 1>(rows, nrows, bpr, 16, stream);
     return launch_pipe<QT, 64, 2>(rows, nrows, bpr, 16, stream, 2);
 }

@@ -248,6 +248,7 @@ __global__ __launch_bounds__(kChunk) void moe_scatter_kernel(const int* __restri
 // weights are expert tile_expert[ty] of the pool; out[position, n].
 struct GroupedGemm {
     static constexpr bool kLinearGrid = false;
+    static constexpr bool kPairedColumns = false;
     int tiles_x;  // unused (2-D grid)
     const float* A;
     int a_cols;
@@ -278,6 +279,27 @@ struct GroupedGemm {
     }
     __device__ void store(const GemmTile& t, int m, int n, float v) const {
         out[static_cast<size_t>(t.m0 + m) * out_cols + n] = v;
+    }
+    __device__ void store_pair(const GemmTile&, int, int, float, float) const {}
+};
+
+// The gate_up grouped GEMM with SwiGLU in its epilogue.  Tile column block
+// bx covers outputs j in [64 bx, 64 bx + 64): its 32-row subtile s holds the
+// gate rows j = 64 bx + 16 s + q (q < 16) followed by the matching up rows
+// I + j, so the kernel pairs column q with q + 16 and this policy stores
+// h[pos, j] = silu(gate) * up (engine.cpp:415-416) instead of gate_up.
+struct GroupedGateUp : GroupedGemm {
+    static constexpr bool kPairedColumns = true;
+    int I;
+    float* h;
+    __device__ static int out_col(int n) { return 64 * (n >> 7) + 16 * ((n >> 5) & 3) + (n & 15); }
+    __device__ const uint8_t* b_row(const GemmTile& t, int n) const {
+        const int j = out_col(n);
+        const int row = (n & 16) ? I + j : j;
+        return pool + static_cast<size_t>(t.group) * expert_bytes + static_cast<size_t>(row) * row_bytes;
+    }
+    __device__ void store_pair(const GemmTile& t, int m, int n, float gate, float up) const {
+        h[static_cast<size_t>(t.m0 + m) * I + out_col(n)] = silu_ref(gate) * up;
     }
 };
 
@@ -332,6 +354,36 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // G = 64 / LPR slots at a time (one row group of LPR lanes per slot, one lane
 // per 32-weight block of a pass), then lane 0 adds the slots' results in
 // slot order from zero.  Slots whose id is out of range are skipped.
+// combine_kernel over four consecutive outputs per thread (16-byte loads and
+// stores; H % 4 == 0, d and Y 16-byte aligned), same arithmetic per element.
+__global__ __launch_bounds__(256) void combine4_kernel(const float* __restrict__ d,
+                                                       const int* __restrict__ pos_of_pair,
+                                                       const float* __restrict__ weights, int tokens, int top_k,
+                                                       int H, float* __restrict__ Y, int accumulate) {
+    const size_t idx = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    const int H4 = H / 4;
+    if (idx >= static_cast<size_t>(tokens) * H4) return;
+    const int t = static_cast<int>(idx / H4), i4 = static_cast<int>(idx % H4);
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int slot = 0; slot < top_k; ++slot) {
+        const int pair = t * top_k + slot;
+        const int pos = pos_of_pair[pair];
+        if (pos < 0) continue;
+        const float w = weights[pair];
+        const f32x4 v = reinterpret_cast<const f32x4*>(d + static_cast<size_t>(pos) * H)[i4];
+        acc.x = fmaf(w, v.x, acc.x);
+        acc.y = fmaf(w, v.y, acc.y);
+        acc.z = fmaf(w, v.z, acc.z);
+        acc.w = fmaf(w, v.w, acc.w);
+    }
+    f32x4* out = reinterpret_cast<f32x4*>(Y + static_cast<size_t>(t) * H) + i4;
+    if (accumulate) {
+        const f32x4 y = *out;
+        acc.x += y.x; acc.y += y.y; acc.z += y.z; acc.w += y.w;
+    }
+    *out = acc;
+}
+
 template <uint32_t QT, int LPR>
 __global__ __launch_bounds__(512) void moe_down_combine_kernel(
     const uint8_t* __restrict__ down, size_t expert_bytes, size_t row_bytes, int experts,
@@ -525,17 +577,30 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
     const size_t gu_row = static_cast<size_t>(H / kBlock) * BB;
     const size_t down_row = static_cast<size_t>(I / kBlock) * BB;
     const int tiles_bound = L.max_tiles;
-    GroupedGemm g1{0, X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
-                   ntiles, gu, 2 * I};
-    hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm>),
-                       dim3((2 * I + kGrpBN - 1) / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0,
-                       stream, g1, 2 * I, H);
-    if ((status = launch_status()) != Q3X_HIP_OK) return status;
-    const size_t sw = static_cast<size_t>(P) * I;
-    const int sw_blocks = static_cast<int>(std::min<size_t>((sw + 255) / 256, 65536));
-    hipLaunchKernelGGL(swiglu_kernel, dim3(sw_blocks), dim3(256), 0, stream, gu, h, I, 0,
-                       static_cast<const int*>(nvalid));
-    if ((status = launch_status()) != Q3X_HIP_OK) return status;
+    if (I % 64 == 0) {
+        // SwiGLU in the gate_up epilogue: h directly.
+        GroupedGateUp g1{};
+        static_cast<GroupedGemm&>(g1) = GroupedGemm{0, X, H, src_token, gate_up, gu_row * 2 * I, gu_row,
+                                                    tile_expert, tile_start, tile_count, ntiles, nullptr, 0};
+        g1.I = I;
+        g1.h = h;
+        hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGateUp>),
+                           dim3(2 * I / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0, stream, g1, 2 * I,
+                           H);
+        if ((status = launch_status()) != Q3X_HIP_OK) return status;
+    } else {
+        GroupedGemm g1{0, X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
+                       ntiles, gu, 2 * I};
+        hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm>),
+                           dim3((2 * I + kGrpBN - 1) / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0,
+                           stream, g1, 2 * I, H);
+        if ((status = launch_status()) != Q3X_HIP_OK) return status;
+        const size_t sw = static_cast<size_t>(P) * I;
+        const int sw_blocks = static_cast<int>(std::min<size_t>((sw + 255) / 256, 65536));
+        hipLaunchKernelGGL(swiglu_kernel, dim3(sw_blocks), dim3(256), 0, stream, gu, h, I, 0,
+                           static_cast<const int*>(nvalid));
+        if ((status = launch_status()) != Q3X_HIP_OK) return status;
+    }
     GroupedGemm g2{0, h, I, nullptr, down, down_row * H, down_row, tile_expert, tile_start, tile_count,
                    ntiles, d, H};
     hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm>),
@@ -543,6 +608,11 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
                        stream, g2, H, I);
     if ((status = launch_status()) != Q3X_HIP_OK) return status;
     const size_t outs = static_cast<size_t>(tokens) * H;
+    if (H % 4 == 0 && aligned(Y, 16)) {
+        hipLaunchKernelGGL(combine4_kernel, dim3(static_cast<unsigned>((outs / 4 + 255) / 256)), dim3(256), 0,
+                           stream, d, pos_of_pair, weights, tokens, top_k, H, Y, accumulate);
+        return launch_status();
+    }
     hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0,
                        stream, d, pos_of_pair, ids, experts, weights, tokens, top_k, H, Y, accumulate);
     return launch_status();
