@@ -39,6 +39,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the lm_head kernel (--steps launches) and a same-size copy, for counter runs")
+    ap.add_argument("--only", default="",
+                    help="comma list of configs (cfg0,cfg2,cfg3,cfg4) to run alone, for counter runs")
     return ap.parse_args()
 
 
@@ -128,6 +130,50 @@ def lm_head_launch_ms(torch, step, lm_set, reps):
     return e0.elapsed_time(e1) / reps
 
 
+def events_ms(torch, fn, reps, warmup=3):
+    """Mean ms per call of fn(i) over `reps` back-to-back calls between two
+    HIP events on the current stream."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def launch_breakdown(torch, q3x, step, layer_sets):
+    """Each launch of the layer on its own (back-to-back launches of one kind,
+    rotating the weight copies): microseconds and algorithmic GB/s."""
+    n = len(layer_sets)
+    o = step.out
+
+    def mb(*names, inputs=4096, acc=False):
+        b = sum(layer_sets[0][k].nbytes + 4 * layer_sets[0][k].rows * (2 if acc else 1) for k in names)
+        return b + 4 * inputs
+
+    kinds = {
+        "q|k|v": (lambda i: q3x.mv_multi([layer_sets[i % n][k].linear for k in ("q", "k", "v")], step.x_attn,
+                                         [o["q"], o["k"], o["v"]]), mb("q", "k", "v")),
+        "o (+=)": (lambda i: q3x.mv_add(layer_sets[i % n]["o"].linear, step.x_o, step.resid), mb("o", acc=True)),
+        "gate|up": (lambda i: q3x.mv_multi([layer_sets[i % n][k].linear for k in ("gate", "up")], step.x_ffn,
+                                           [o["gate"], o["up"]]), mb("gate", "up")),
+        "down (+=)": (lambda i: q3x.mv_add(layer_sets[i % n]["down"].linear, step.h, step.resid),
+                      mb("down", inputs=12288, acc=True)),
+    }
+    out = {}
+    for name, (fn, nbytes) in kinds.items():
+        ms = events_ms(torch, fn, 4 * n)
+        out[name] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    step.reset()
+    return out
+
+
 def headline(torch, q3x, wl, steps, warmup):
     mats = wl.dense_matrices(1)
     layer = [m for m in mats if m.name != "lm_head"]
@@ -160,7 +206,10 @@ def headline(torch, q3x, wl, steps, warmup):
     lm_ms = lm_head_launch_ms(torch, step, lm_set, 20)
     lm_alg = mv_bytes(lm)
     step_bytes = step.step_bytes()
+    per_launch = launch_breakdown(torch, q3x, step, layer_sets)
+    per_launch["lm_head"] = {"us": round(lm_ms * 1e3, 2), "GBps": round(lm_alg / (lm_ms * 1e-3) / 1e9, 1)}
     return {
+        "per_launch": per_launch,
         "value": step_bytes / (ms * 1e-3) / 1e9,
         "ms_per_step": ms,
         "step_bytes": step_bytes,
@@ -216,90 +265,98 @@ def time_graph(torch, fn, calls, replays, warmup=2):
     return start.elapsed_time(end) / (replays * calls)
 
 
-def extra_configs(torch, q3x, wl):
+def extra_configs(torch, q3x, wl, only=None):
     out = {}
-    # config 0: one Q8_0 4096x4096 matvec, copies rotated
-    m = wl.dense_matrices(0)[0]
-    n = copies_for(m.nbytes)
-    ws = [m.weight] + [m.weight.clone() for _ in range(n - 1)]
-    x = wl.activations(0, 1, 4096)[0].contiguous()
-    y = torch.empty(4096, dtype=torch.float32, device="cuda")
-    ms = time_graph(torch, lambda i: q3x.mv(q3x.Linear(ws[i % n], 4096, 4096, m.type), x, y), 4 * n, 20)
-    out["cfg0_q8_mv_4096"] = {"GBps": mv_bytes(m) / (ms * 1e-3) / 1e9, "us": ms * 1e3, "copies": n}
-    del ws
-    # config 2: Q8_0 prefill GEMM, N in {512, 4096}
-    mats = wl.dense_matrices(2)
-    for count in (512, 4096):
-        X = wl.activations(2, count, 4096)
-        H = wl.activations(2, count, 12288, salt=1)
-        Ys = {mm.name: torch.empty((count, mm.rows), dtype=torch.float32, device="cuda") for mm in mats}
+    want = (lambda c: only is None or c in only)
+    if want("cfg0"):
+        # config 0: one Q8_0 4096x4096 matvec, copies rotated
+        m = wl.dense_matrices(0)[0]
+        n = copies_for(m.nbytes)
+        ws = [m.weight] + [m.weight.clone() for _ in range(n - 1)]
+        x = wl.activations(0, 1, 4096)[0].contiguous()
+        y = torch.empty(4096, dtype=torch.float32, device="cuda")
+        ms = time_graph(torch, lambda i: q3x.mv(q3x.Linear(ws[i % n], 4096, 4096, m.type), x, y), 4 * n, 20)
+        out["cfg0_q8_mv_4096"] = {"GBps": mv_bytes(m) / (ms * 1e-3) / 1e9, "us": ms * 1e3, "copies": n}
+        del ws
+    if want("cfg2"):
+        # config 2: Q8_0 prefill GEMM, N in {512, 4096}
+        mats = wl.dense_matrices(2)
+        for count in (512, 4096):
+            X = wl.activations(2, count, 4096)
+            H = wl.activations(2, count, 12288, salt=1)
+            Ys = {mm.name: torch.empty((count, mm.rows), dtype=torch.float32, device="cuda") for mm in mats}
 
-        def run(i):
+            def run(i):
+                for mm in mats:
+                    q3x.batch_mv(mm.linear, H if mm.name == "down" else X, Ys[mm.name], count)
+            ms = time_graph(torch, run, 1, 4 if count == 4096 else 10)
+            flops = sum(2.0 * count * mm.rows * mm.cols for mm in mats)
+            out[f"cfg2_q8_gemm_N{count}"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
+                                             "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+            del X, H, Ys
+        del mats
+    if want("cfg3"):
+        # config 3: Q4_0 27B FFN at N = 1 (matvec) and N = 512 (GEMM)
+        mats = wl.dense_matrices(3)
+        total = sum(mm.nbytes for mm in mats)
+        n = copies_for(total)
+        sets = [mats] + [[wl.Matrix(mm.name, mm.type, mm.rows, mm.cols, mm.weight.clone()) for mm in mats]
+                         for _ in range(n - 1)]
+        x = wl.activations(3, 1, 17408)[0].contiguous()
+        ys = {mm.name: torch.empty(mm.rows, dtype=torch.float32, device="cuda") for mm in mats}
+
+        def run_mv(i):
+            s = {mm.name: mm for mm in sets[i % n]}
+            q3x.mv_multi([s["gate"].linear, s["up"].linear], x, [ys["gate"], ys["up"]])
+            q3x.mv(s["down"].linear, x, ys["down"])
+        ms = time_graph(torch, run_mv, 2 * n, 10)
+        alg = sum(mv_bytes(mm) for mm in mats) - 4 * 5120  # gate|up read x once
+        out["cfg3_q4_mv_27b_ffn"] = {"GBps": alg / (ms * 1e-3) / 1e9, "us": ms * 1e3, "copies": n}
+        del sets
+        X = wl.activations(3, 512, 5120)
+        H = wl.activations(3, 512, 17408, salt=1)
+        Ys = {mm.name: torch.empty((512, mm.rows), dtype=torch.float32, device="cuda") for mm in mats}
+
+        def run_gemm(i):
             for mm in mats:
-                q3x.batch_mv(mm.linear, H if mm.name == "down" else X, Ys[mm.name], count)
-        ms = time_graph(torch, run, 1, 4 if count == 4096 else 10)
-        flops = sum(2.0 * count * mm.rows * mm.cols for mm in mats)
-        out[f"cfg2_q8_gemm_N{count}"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
-                                         "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
-        del X, H, Ys
-    del mats
-    # config 3: Q4_0 27B FFN at N = 1 (matvec) and N = 512 (GEMM)
-    mats = wl.dense_matrices(3)
-    total = sum(mm.nbytes for mm in mats)
-    n = copies_for(total)
-    sets = [mats] + [[wl.Matrix(mm.name, mm.type, mm.rows, mm.cols, mm.weight.clone()) for mm in mats]
-                     for _ in range(n - 1)]
-    x = wl.activations(3, 1, 17408)[0].contiguous()
-    ys = {mm.name: torch.empty(mm.rows, dtype=torch.float32, device="cuda") for mm in mats}
+                q3x.batch_mv(mm.linear, H if mm.name == "down" else X, Ys[mm.name], 512)
+        ms = time_graph(torch, run_gemm, 1, 10)
+        flops = sum(2.0 * 512 * mm.rows * mm.cols for mm in mats)
+        out["cfg3_q4_gemm_N512"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
+                                    "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+        del mats, X, H, Ys
+    if want("cfg4"):
+        # config 4: Q4_0 routed MoE (router + experts), decode and 2048-token prefill
+        moe = wl.moe_weights(4)
+        cfg = wl.CONFIGS[4]
+        k = cfg["top_k"]
+        for T in (1, 2048):
+            logits = wl.router_logits(4, T, moe.experts)
+            X = wl.activations(4, T, moe.H)
+            ids = torch.empty((T, k), dtype=torch.int32, device="cuda")
+            wts = torch.empty((T, k), dtype=torch.float32, device="cuda")
+            Y = torch.empty((T, moe.H), dtype=torch.float32, device="cuda")
+            wsb = torch.empty(q3x.moe_workspace_bytes(T, moe.experts, k, moe.H, moe.I), dtype=torch.uint8,
+                              device="cuda")
 
-    def run_mv(i):
-        s = {mm.name: mm for mm in sets[i % n]}
-        q3x.mv_multi([s["gate"].linear, s["up"].linear], x, [ys["gate"], ys["up"]])
-        q3x.mv(s["down"].linear, x, ys["down"])
-    ms = time_graph(torch, run_mv, 2 * n, 10)
-    alg = sum(mv_bytes(mm) for mm in mats) - 4 * 5120  # gate|up read x once
-    out["cfg3_q4_mv_27b_ffn"] = {"GBps": alg / (ms * 1e-3) / 1e9, "us": ms * 1e3, "copies": n}
-    del sets
-    X = wl.activations(3, 512, 5120)
-    H = wl.activations(3, 512, 17408, salt=1)
-    Ys = {mm.name: torch.empty((512, mm.rows), dtype=torch.float32, device="cuda") for mm in mats}
-
-    def run_gemm(i):
-        for mm in mats:
-            q3x.batch_mv(mm.linear, H if mm.name == "down" else X, Ys[mm.name], 512)
-    ms = time_graph(torch, run_gemm, 1, 10)
-    flops = sum(2.0 * 512 * mm.rows * mm.cols for mm in mats)
-    out["cfg3_q4_gemm_N512"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
-                                "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
-    del mats, X, H, Ys
-    # config 4: Q4_0 routed MoE (router + experts), decode and 2048-token prefill
-    moe = wl.moe_weights(4)
-    cfg = wl.CONFIGS[4]
-    k = cfg["top_k"]
-    for T in (1, 2048):
-        logits = wl.router_logits(4, T, moe.experts)
-        X = wl.activations(4, T, moe.H)
-        ids = torch.empty((T, k), dtype=torch.int32, device="cuda")
-        wts = torch.empty((T, k), dtype=torch.float32, device="cuda")
-        Y = torch.empty((T, moe.H), dtype=torch.float32, device="cuda")
-        wsb = torch.empty(q3x.moe_workspace_bytes(T, moe.experts, k, moe.H, moe.I), dtype=torch.uint8,
-                          device="cuda")
-
-        def run_moe(i):
-            q3x.router_top_k(logits, T, moe.experts, k, ids, wts)
-            q3x.moe_routed(moe.gate_up_linear, moe.down_linear, X, T, ids, wts, k, Y, workspace=wsb)
-        ms = time_graph(torch, run_moe, 20 if T == 1 else 1, 10 if T == 1 else 5)
-        if T == 1:
-            per_expert = (moe.gate_up.numel() + moe.down.numel()) // moe.experts
-            alg = k * per_expert
-            out["cfg4_q4_moe_decode"] = {"GBps": alg / (ms * 1e-3) / 1e9, "us": ms * 1e3,
-                                         "note": "router + 8 experts per call; the same token's 14 MB of "
-                                                 "expert weights repeat, so the Infinity Cache serves them"}
-        else:
-            flops = 2.0 * T * k * (2 * moe.I * moe.H + moe.H * moe.I)
-            out["cfg4_q4_moe_prefill_T2048"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
-                                                "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
-        del logits, X, ids, wts, Y, wsb
+            def run_moe(i):
+                q3x.router_top_k(logits, T, moe.experts, k, ids, wts)
+                q3x.moe_routed(moe.gate_up_linear, moe.down_linear, X, T, ids, wts, k, Y, workspace=wsb)
+            ms = time_graph(torch, run_moe, 20 if T == 1 else 1, 10 if T == 1 else 5)
+            router_ms = time_graph(torch, lambda i: q3x.router_top_k(logits, T, moe.experts, k, ids, wts), 20, 5)
+            if T == 1:
+                per_expert = (moe.gate_up.numel() + moe.down.numel()) // moe.experts
+                alg = k * per_expert
+                out["cfg4_q4_moe_decode"] = {"GBps": alg / (ms * 1e-3) / 1e9, "us": ms * 1e3,
+                                             "router_us": router_ms * 1e3,
+                                             "note": "router + 8 experts per call; the same token's 14 MB of "
+                                                     "expert weights repeat, so the Infinity Cache serves them"}
+            else:
+                flops = 2.0 * T * k * (2 * moe.I * moe.H + moe.H * moe.I)
+                out["cfg4_q4_moe_prefill_T2048"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
+                                                    "router_ms": router_ms,
+                                                    "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+            del logits, X, ids, wts, Y, wsb
     return out
 
 
@@ -346,6 +403,9 @@ def main():
     if args.roofline_only:
         roofline_only(torch, q3x, wl, args.steps)
         return
+    if args.only:
+        print(json.dumps(extra_configs(torch, q3x, wl, set(args.only.split(",")))), flush=True)
+        return
     head = headline(torch, q3x, wl, args.steps, args.warmup)
     lm = head["lm_head"]
     traffic = measured_traffic()
@@ -365,7 +425,8 @@ def main():
         "config": {"workload": "config 1: Q8_0 decode matvec set of one 9B-class layer "
                                "(q/k/v/o 4096->4096, gate/up 4096->12288, down 12288->4096) + lm_head "
                                "4096->151936, batch 1", "launches": LAYER_LAUNCHES, "step_bytes": head["step_bytes"],
-                   "weight_copies_rotated": head["copies"], "frac_of_hbm_peak": round(head["value"] / HBM_PEAK_GBS, 4)},
+                   "weight_copies_rotated": head["copies"], "frac_of_hbm_peak": round(head["value"] / HBM_PEAK_GBS, 4),
+                   "per_launch": head["per_launch"]},
         "roofline": {"bound": "hbm", "achieved": round(lm["GBps"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(lm["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "mv_pipe_kernel<Q8_0, 64 lanes/row, 1 row/step, 2x16 waves/CU> on lm_head 151936x4096",

@@ -190,34 +190,40 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     const int nblk = cols / kBlock;
+    // A wave whose A rows all lie past the tile's valid rows (the last tile
+    // of an expert's group) has nothing to compute: it only helps stage the
+    // tiles, leaving the SIMD's matrix core to the other waves.
+    const bool active = !Policy::kPartialTiles || wm * TM * 32 < tile.mcount;
     load_stage(0);
     store_stage(0);
     __syncthreads();
     for (int kb = 0; kb < nblk; ++kb) {
         const int buf = kb & 1;
         if (kb + 1 < nblk) load_stage(kb + 1);
-        f32x4 af[TM][4], bf[TN][4];
+        if (active) {
+            f32x4 af[TM][4], bf[TN][4];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const float* src = &As[buf][((wm * TM + i) * 32 + li) * kGemmLd + 16 * kh];
+            for (int i = 0; i < TM; ++i) {
+                const float* src = &As[buf][((wm * TM + i) * 32 + li) * kGemmLd + 16 * kh];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) af[i][q] = *reinterpret_cast<const f32x4*>(src + 4 * q);
+                for (int q = 0; q < 4; ++q) af[i][q] = *reinterpret_cast<const f32x4*>(src + 4 * q);
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const float* src = &Bs[buf][((wn * TN + j) * 32 + li) * kGemmLd + 16 * kh];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) bf[j][q] = *reinterpret_cast<const f32x4*>(src + 4 * q);
+            }
+#pragma unroll
+            for (int s = 0; s < 16; ++s)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s >> 2][s & 3],
+                                                                         bf[j][s >> 2][s & 3],
+                                                                         acc[i][j], 0, 0, 0);
         }
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const float* src = &Bs[buf][((wn * TN + j) * 32 + li) * kGemmLd + 16 * kh];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) bf[j][q] = *reinterpret_cast<const f32x4*>(src + 4 * q);
-        }
-#pragma unroll
-        for (int s = 0; s < 16; ++s)
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s >> 2][s & 3],
-                                                                     bf[j][s >> 2][s & 3],
-                                                                     acc[i][j], 0, 0, 0);
         if (kb + 1 < nblk) store_stage(buf ^ 1);
         __syncthreads();
     }

@@ -13,6 +13,7 @@ namespace q3x {
 struct DenseGemm {
     static constexpr bool kLinearGrid = true;
     static constexpr bool kPairedColumns = false;
+    static constexpr bool kPartialTiles = false;  // only the last token tile is short
     int tiles_x;  // weight-row tiles of the launch
     const float* X;
     int cols;

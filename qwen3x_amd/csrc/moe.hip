@@ -249,6 +249,7 @@ __global__ __launch_bounds__(kChunk) void moe_scatter_kernel(const int* __restri
 struct GroupedGemm {
     static constexpr bool kLinearGrid = false;
     static constexpr bool kPairedColumns = false;
+    static constexpr bool kPartialTiles = true;  // every expert's last tile is short
     int tiles_x;  // unused (2-D grid)
     const float* A;
     int a_cols;

@@ -345,21 +345,24 @@ def test_moe_routed_parity(type_, E, H, I, top_k, tokens):
     assert np.all(np.abs(host(Y).astype(np.float64) - 2 * want) <= 2 * bound)
 
 
-def test_moe_invalid_ids_contribute_nothing():
+@pytest.mark.parametrize("type_,H,I", [(Q4_0, 256, 64),    # unaligned down rows: grouped path at 1 token
+                                       (Q8_0, 256, 256)])  # aligned: fused decode kernel at 1 token
+def test_moe_invalid_ids_contribute_nothing(type_, H, I):
     torch = _torch()
-    E, H, I, k = 4, 256, 64, 3
-    rng = np.random.default_rng(99)
-    gu = random_blocks(rng, Q4_0, E * 2 * I, H)
-    dn = random_blocks(rng, Q4_0, E * H, I)
+    E, k = 4, 3
+    rng = np.random.default_rng(99 + I)
+    gu = random_blocks(rng, type_, E * 2 * I, H)
+    dn = random_blocks(rng, type_, E * H, I)
     for tokens in (1, 6):
         X = rng.normal(0, 1, (tokens, H)).astype(np.float32)
         ids = np.tile(np.array([2, -1, 7], np.int32), (tokens, 1))
         wts = np.tile(np.array([0.5, 0.3, 0.2], np.float32), (tokens, 1))
-        want = oracle.moe_routed(gu, dn, Q4_0, E, H, I, X, ids[:, :1], wts[:, :1])
+        want = oracle.moe_routed(gu, dn, type_, E, H, I, X, ids[:, :1], wts[:, :1])
         Y = torch.empty((tokens, H), dtype=torch.float32, device="cuda:0")
-        q3x.moe_routed(q3x.ExpertLinear(dev(gu), E, 2 * I, H, Q4_0), q3x.ExpertLinear(dev(dn), E, H, I, Q4_0),
+        say(f"moe invalid ids type={type_} H={H} I={I} tokens={tokens}")
+        q3x.moe_routed(q3x.ExpertLinear(dev(gu), E, 2 * I, H, type_), q3x.ExpertLinear(dev(dn), E, H, I, type_),
                        dev(X), tokens, dev(ids), dev(wts), k, Y)
-        bound = moe_bound(gu, dn, Q4_0, E, H, I, X, ids[:, :1], wts[:, :1])
+        bound = moe_bound(gu, dn, type_, E, H, I, X, ids[:, :1], wts[:, :1])
         assert np.all(np.abs(host(Y) - want) <= bound)
 
 
