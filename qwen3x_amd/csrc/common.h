@@ -100,6 +100,53 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Lane exchange inside rows of 16 lanes through DPP (no LDS round trip).
+// Controls (gfx9): quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E,
+// row_half_mirror (lane i <- 7-i of its 8) = 0x141, row_mirror (i <- 15-i) =
+// 0x140.  Every source lane lies inside the row, so no lane reads a bound.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(v)));
+}
+__device__ __forceinline__ uint32_t read_lane_u32(uint32_t v, int lane) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
+}
+__device__ __forceinline__ float read_lane_f32(float v, int lane) {
+    return __uint_as_float(read_lane_u32(__float_as_uint(v), lane));
+}
+
+// Wave-wide maximum of an unsigned value, returned to every lane (uniform):
+// xor-1, xor-2 and the two mirrors leave each row's maximum in all its lanes,
+// then the four rows are compared.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0xB1>(v));
+    v = max(v, dpp_u32<0x4E>(v));
+    v = max(v, dpp_u32<0x141>(v));
+    v = max(v, dpp_u32<0x140>(v));
+    return max(max(read_lane_u32(v, 0), read_lane_u32(v, 16)), max(read_lane_u32(v, 32), read_lane_u32(v, 48)));
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    return fmaxf(fmaxf(read_lane_f32(v, 0), read_lane_f32(v, 16)), fmaxf(read_lane_f32(v, 32), read_lane_f32(v, 48)));
+}
+// Wave-wide sum in a fixed tree order (pairs, quads, eights, rows, then
+// (row0 + row1) + (row2 + row3)); every lane of a row sees the same bits at
+// each level, because each level adds the same two values.
+__device__ __forceinline__ float wave_sum_f32(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    return (read_lane_f32(v, 0) + read_lane_f32(v, 16)) + (read_lane_f32(v, 32) + read_lane_f32(v, 48));
+}
+
 // Orders LDS traffic of one wavefront: every lane's earlier LDS writes are
 // visible to every lane's later LDS reads (LDS executes a wave's operations
 // in issue order; this keeps the compiler from moving them across).

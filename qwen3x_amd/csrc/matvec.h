@@ -390,12 +390,22 @@ __global__ __launch_bounds__(1024) void mv_pipe_kernel(Rows all_rows, int nrows,
             wave_lds_sync();
         }
         if (cp == npass - 1) {
+            if constexpr (decltype(rows)::kSwiGLUPairs) {
+                // Iteration 0 is a gate row, iteration 1 its up row.
+                static_assert(R == 2 && G == 1, "SwiGLU pairs need two row iterations of one row group");
+                const float gate = group_sum<LPR>(acc[0]);
+                const float up = group_sum<LPR>(acc[1]);
+                const int row = gw + cb * RS * GW;
+                if (li == 0 && row < nrows) rows.store_pair(row, gate, up);
+                acc[0] = acc[1] = 0.0f;
+            } else {
 #pragma unroll
-            for (int it = 0; it < R; ++it) {
-                const float total = group_sum<LPR>(acc[it]);
-                const int row = gw + (cb * RS + it * G + g) * GW;
-                if (li == 0 && row < nrows) rows.store(row, rows.previous(row) + total);
-                acc[it] = 0.0f;
+                for (int it = 0; it < R; ++it) {
+                    const float total = group_sum<LPR>(acc[it]);
+                    const int row = gw + (cb * RS + it * G + g) * GW;
+                    if (li == 0 && row < nrows) rows.store(row, rows.previous(row) + total);
+                    acc[it] = 0.0f;
+                }
             }
         }
         cb = nb;

@@ -6,13 +6,13 @@
 // expert_down_weighted_q4_kernel run per token, so the reference has no
 // grouped expert GEMM and its prefill is token by token).
 //
-// Here the router runs one wavefront per token.  The routed matmul has two
-// shapes:
-//   decode (tokens == 1): the selected experts' gate_up rows are one tall
-//     virtual matrix for the pipelined matvec (matvec.h; its waves split
-//     evenly over the slots), then one kernel applies SwiGLU to the slots'
-//     gate_up outputs in LDS, runs every slot's down row for each output row
-//     and combines the slots in order (moe_down_combine_kernel);
+// Here the router runs one wavefront per token, exchanging values by DPP.
+// The routed matmul has two shapes:
+//   decode (tokens == 1): the selected experts' gate and up rows go through
+//     the pipelined matvec (matvec.h; its waves split evenly over the slots,
+//     each step a gate row and its up row), which stores h = silu(g) * u;
+//     then one kernel runs every slot's down row for each output row and
+//     combines the slots in order (moe_down_combine_kernel);
 //   prefill (tokens > 1): the (token, slot) pairs are grouped by expert with
 //     a stable counting sort (deterministic positions), each expert's group is
 //     cut into 32-token tiles, and one grouped FP32-MFMA GEMM launch (gemm.h)
@@ -37,44 +37,43 @@ constexpr int kGrpBN = kGrpWN * kGrpTN * 32;
 
 // ---------------------------------------------------------------- router ----
 
-// One wavefront per token.  Softmax with the maximum subtracted, then top_k
-// passes of a wave-wide argmax (larger probability wins; equal values go to
-// the lower expert index, as the reference's strict '>' scan does), then
-// weights = p / (sum of the selected p, added in slot order).
+// One wavefront per token; lane l holds experts [PER*l, PER*l + PER), so lane
+// order is expert order.  Softmax with the maximum subtracted, then top_k
+// argmax passes, each over keys (0 for an expert already chosen or past the
+// end, else the probability's bits + 1: probabilities are >= 0, so their bits
+// order like the values).  A lane keeps its best key (lowest index among
+// equal ones); the wave's largest key is found with DPP and readlanes, and
+// the lowest lane holding it wins, i.e. the lowest expert index among equal
+// probabilities, as the reference's strict '>' scan picks.  Weights = p / (sum
+// of the selected p, added in slot order).  No LDS: every exchange is a DPP
+// move or a readlane, so one token costs a few hundred instructions.
+template <int PER>
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int tokens,
                                                           int experts, int top_k, int* __restrict__ ids,
                                                           float* __restrict__ weights) {
-    constexpr int PER_LANE = kRouterMaxExperts / kWave;
     const int lane = threadIdx.x & (kWave - 1);
     const int token = blockIdx.x * 4 + threadIdx.x / kWave;
-    if (token >= tokens) return;
+    if (token >= tokens) return;  // whole waves leave together
     const float* row = logits + static_cast<size_t>(token) * experts;
-    float p[PER_LANE];
-    float maximum = -INFINITY;
+    const int first = PER * lane;
+    float p[PER];
 #pragma unroll
-    for (int j = 0; j < PER_LANE; ++j) {
-        const int e = lane + kWave * j;
-        p[j] = e < experts ? row[e] : -INFINITY;
-        maximum = maximum < p[j] ? p[j] : maximum;  // std::max(maximum, logit)
-    }
+    for (int j = 0; j < PER; ++j) p[j] = first + j < experts ? row[first + j] : -INFINITY;
+    float local_max = -INFINITY;
 #pragma unroll
-    for (int offset = kWave / 2; offset > 0; offset >>= 1) {
-        const float other = __shfl_xor(maximum, offset);
-        maximum = maximum < other ? other : maximum;
-    }
-    float total = 0.0f;
+    for (int j = 0; j < PER; ++j) local_max = local_max < p[j] ? p[j] : local_max;
+    const float maximum = wave_max_f32(local_max);
+    float local_sum = 0.0f;
 #pragma unroll
-    for (int j = 0; j < PER_LANE; ++j) {
-        const int e = lane + kWave * j;
-        p[j] = e < experts ? expf(p[j] - maximum) : 0.0f;
-        total += p[j];
+    for (int j = 0; j < PER; ++j) {
+        p[j] = first + j < experts ? expf(p[j] - maximum) : 0.0f;
+        local_sum += p[j];
     }
-    total = group_sum<kWave>(total);
+    const float total = wave_sum_f32(local_sum);
+    uint32_t key[PER];
 #pragma unroll
-    for (int j = 0; j < PER_LANE; ++j) {
-        const int e = lane + kWave * j;
-        p[j] = e < experts ? p[j] / total : -1.0f;  // -1: never selected
-    }
+    for (int j = 0; j < PER; ++j) key[j] = first + j < experts ? __float_as_uint(p[j] / total) + 1u : 0u;
+
     float chosen[kRouterMaxTopK];
     int chosen_id[kRouterMaxTopK];
 #pragma unroll
@@ -82,23 +81,21 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
         chosen[slot] = 0.0f;
         chosen_id[slot] = 0;
         if (slot >= top_k) continue;
-        float best = -1.0f;
-        int best_id = 0x7fffffff;
+        uint32_t best = 0;
+        int best_j = 0;
 #pragma unroll
-        for (int j = 0; j < PER_LANE; ++j) {
-            if (p[j] > best) { best = p[j]; best_id = lane + kWave * j; }
+        for (int j = 0; j < PER; ++j)
+            if (key[j] > best) { best = key[j]; best_j = j; }
+        const uint32_t top = wave_max_u32(best);
+        const unsigned long long holders = __ballot(best == top);
+        const int winner = __builtin_ctzll(holders);
+        chosen[slot] = __uint_as_float(top - 1u);
+        chosen_id[slot] = PER * winner + static_cast<int>(read_lane_u32(static_cast<uint32_t>(best_j), winner));
+        if (lane == winner) {
+#pragma unroll
+            for (int j = 0; j < PER; ++j)
+                if (j == best_j) key[j] = 0u;
         }
-#pragma unroll
-        for (int offset = kWave / 2; offset > 0; offset >>= 1) {
-            const float ov = __shfl_xor(best, offset);
-            const int oi = __shfl_xor(best_id, offset);
-            if (ov > best || (ov == best && oi < best_id)) { best = ov; best_id = oi; }
-        }
-        chosen[slot] = best;
-        chosen_id[slot] = best_id;
-#pragma unroll
-        for (int j = 0; j < PER_LANE; ++j)
-            if (lane + kWave * j == best_id) p[j] = -1.0f;
     }
     float selected_total = 0.0f;
 #pragma unroll
@@ -347,14 +344,6 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     else Y[idx] = acc;
 }
 
-// Decode (one token): the down projection of every selected expert, with
-// SwiGLU applied to its input on the way into LDS (engine.cpp:415-416) and
-// the slot-order combine (engine.cpp:411, 418-419: out = 0, then
-// out += w * d per slot), in one kernel.  Wave gw computes the output rows
-// i = gw, gw + GW, ...: for each, the rows (slot s, i) of the top_k experts,
-// G = 64 / LPR slots at a time (one row group of LPR lanes per slot, one lane
-// per 32-weight block of a pass), then lane 0 adds the slots' results in
-// slot order from zero.  Slots whose id is out of range are skipped.
 // combine_kernel over four consecutive outputs per thread (16-byte loads and
 // stores; H % 4 == 0, d and Y 16-byte aligned), same arithmetic per element.
 __global__ __launch_bounds__(256) void combine4_kernel(const float* __restrict__ d,
@@ -385,10 +374,18 @@ __global__ __launch_bounds__(256) void combine4_kernel(const float* __restrict__
     *out = acc;
 }
 
+// Decode (one token): the down projection of every selected expert, its
+// input h = silu(g) * u (engine.cpp:415-416, from the paired gate_up matvec)
+// staged in LDS, and the slot-order combine (engine.cpp:411, 418-419:
+// out = 0, then out += w * d per slot), in one kernel.  Wave gw computes the output rows
+// i = gw, gw + GW, ...: for each, the rows (slot s, i) of the top_k experts,
+// G = 64 / LPR slots at a time (one row group of LPR lanes per slot, one lane
+// per 32-weight block of a pass), then lane 0 adds the slots' results in
+// slot order from zero.  Slots whose id is out of range are skipped.
 template <uint32_t QT, int LPR>
 __global__ __launch_bounds__(512) void moe_down_combine_kernel(
     const uint8_t* __restrict__ down, size_t expert_bytes, size_t row_bytes, int experts,
-    const int* __restrict__ ids, const float* __restrict__ weights, int top_k, const float* __restrict__ gu,
+    const int* __restrict__ ids, const float* __restrict__ weights, int top_k, const float* __restrict__ h,
     int I, int H, float* __restrict__ Y, int accumulate) {
     using S = PipeShape<QT, LPR>;
     constexpr int BB = S::BB, G = S::G, J = S::J;
@@ -408,13 +405,60 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
     const int li = lane % LPR;
     uint8_t* const wl = lds_dyn + top_k * xs_bytes + wave * S::WAVE_LDS;
 
-    // h = silu(gate) * up for every slot, into the padded x layout.
-    for (int c = threadIdx.x; c < top_k * I; c += blockDim.x) {
-        const int slot = c / I, j = c - slot * I;
-        const float* row = gu + static_cast<size_t>(slot) * 2 * I;
-        *reinterpret_cast<float*>(lds_dyn + slot * xs_bytes + x_block_offset(j >> 5) + 4 * (j & 31)) =
-            silu_ref(row[j]) * row[I + j];
+    const int npass = (bpr + LPR - 1) / LPR;
+    const int groups = (top_k + G - 1) / G;
+    const int my_steps = gw < H ? (H - gw + GW - 1) / GW * npass : 0;
+    // The selected experts (uniform); an id out of range reads as zeros.
+    int expert[IT * G];
+#pragma unroll
+    for (int slot = 0; slot < IT * G; ++slot) {
+        const int e = slot < top_k ? __builtin_amdgcn_readfirstlane(ids[slot]) : -1;
+        expert[slot] = e >= 0 && e < experts ? e : -1;
     }
+    // Weight segments of one step (output row i, pass) for every slot group;
+    // `live` false gives zeros without touching memory.
+    u32x4 pre[IT][G][J];
+    auto issue = [&](int i, int pass, int it, bool live) {
+        const int b0 = pass * LPR;
+        const int nblk = min(LPR, bpr - b0);
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) {
+            const int e = expert[it * G + gg];
+            const bool ok = live && e >= 0;
+            const uint8_t* src = ok ? down + static_cast<size_t>(e) * expert_bytes + static_cast<size_t>(i) * row_bytes +
+                                          static_cast<size_t>(b0) * BB
+                                    : down;
+            const __amdgpu_buffer_rsrc_t rsrc =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src), 0, ok ? nblk * BB : 0, kBufferFlags);
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                pre[it][gg][j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * lane + 1024 * j, 0, kNonTemporal);
+        }
+    };
+    // h of every slot into the padded x layout: its loads go out first (they
+    // return from L2), then the first step's weights, whose latency overlaps
+    // the copy and the Q4 references.
+    constexpr int kHPerThread = 8;
+    float hv[kHPerThread];
+    const int hn = top_k * I;
+#pragma unroll
+    for (int k = 0; k < kHPerThread; ++k) {
+        const int c = threadIdx.x + k * static_cast<int>(blockDim.x);
+        hv[k] = c < hn ? h[c] : 0.0f;
+    }
+#pragma unroll
+    for (int it = 0; it < IT; ++it)
+        if (it < groups) issue(gw, 0, it, my_steps > 0);
+    auto put_h = [&](int c, float v) {
+        const int slot = c / I, j = c - slot * I;
+        *reinterpret_cast<float*>(lds_dyn + slot * xs_bytes + x_block_offset(j >> 5) + 4 * (j & 31)) = v;
+    };
+#pragma unroll
+    for (int k = 0; k < kHPerThread; ++k) {
+        const int c = threadIdx.x + k * static_cast<int>(blockDim.x);
+        if (c < hn) put_h(c, hv[k]);
+    }
+    for (int c = threadIdx.x + kHPerThread * static_cast<int>(blockDim.x); c < hn; c += blockDim.x) put_h(c, h[c]);
     __syncthreads();
     if (Q4) {
         for (int c = threadIdx.x; c < top_k * bpr; c += blockDim.x) {
@@ -426,80 +470,69 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
         __syncthreads();
     }
 
-    const int npass = (bpr + LPR - 1) / LPR;
-    const int groups = (top_k + G - 1) / G;
-    for (int i = gw; i < H; i += GW) {
-        float acc[IT];
+    float acc[IT];
+    int ci = gw, cp = 0;  // current step: output row, pass
+    for (int s = 0; s < my_steps; ++s) {
+        int ni = ci, np = cp + 1;
+        if (np == npass) { np = 0; ni += GW; }
+        const bool more = s + 1 < my_steps;
+        const int b0 = cp * LPR;
+        const int nblk = min(LPR, bpr - b0);
+        const int col = li < nblk ? b0 + li : 0;
+        if (cp == 0) {
 #pragma unroll
-        for (int it = 0; it < IT; ++it) acc[it] = 0.0f;
-        for (int pass = 0; pass < npass; ++pass) {
-            const int b0 = pass * LPR;
-            const int nblk = min(LPR, bpr - b0);
-            const int col = li < nblk ? b0 + li : 0;
-#pragma unroll
-            for (int it = 0; it < IT; ++it) {
-                if (it >= groups) break;
-                u32x4 pre[G][J];
-#pragma unroll
-                for (int gg = 0; gg < G; ++gg) {
-                    const int slot = it * G + gg;
-                    const int e = slot < top_k ? __builtin_amdgcn_readfirstlane(ids[slot]) : -1;
-                    const bool ok = e >= 0 && e < experts;
-                    const uint8_t* src = ok ? down + static_cast<size_t>(e) * expert_bytes +
-                                                  static_cast<size_t>(i) * row_bytes + static_cast<size_t>(b0) * BB
-                                            : down;
-                    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-                        const_cast<uint8_t*>(src), 0, ok ? nblk * BB : 0, kBufferFlags);
-#pragma unroll
-                    for (int j = 0; j < J; ++j)
-                        pre[gg][j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * lane + 1024 * j, 0, kNonTemporal);
-                }
-                // x of this lane's slot, block col.
-                const int my_slot = it * G + g;
-                const uint8_t* xs = lds_dyn + (my_slot < top_k ? my_slot : 0) * xs_bytes;
-                float xv[32];
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const f32x4 t = *reinterpret_cast<const f32x4*>(xs + x_block_offset(col) + 16 * q);
-                    xv[4 * q + 0] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
-                }
-                const float xref = Q4 ? reinterpret_cast<const float*>(xs + ref_off)[col] : 0.0f;
-#pragma unroll
-                for (int gg = 0; gg < G; ++gg)
-#pragma unroll
-                    for (int j = 0; j < J; ++j)
-                        *reinterpret_cast<u32x4*>(wl + gg * S::SEGP + 1024 * j + 16 * lane) = pre[gg][j];
-                wave_lds_sync();
-                if (li < nblk && my_slot < top_k) {
-                    const uint32_t p = g * S::SEGP + li * BB;
-                    acc[it] += Q4 ? block_dot_q4_mix(wl, p, xv, xref) : block_dot_q8(wl, p, xv);
-                }
-                wave_lds_sync();
-            }
+            for (int it = 0; it < IT; ++it) acc[it] = 0.0f;
         }
-        // Slot results to lane 0, then the ordered combine.
-        float out = 0.0f;
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             if (it >= groups) break;
-            const float total = group_sum<LPR>(acc[it]);
+            // x of this lane's slot, block col.
+            const int my_slot = it * G + g;
+            const uint8_t* xs = lds_dyn + (my_slot < top_k ? my_slot : 0) * xs_bytes;
+            float xv[32];
 #pragma unroll
-            for (int gg = 0; gg < G; ++gg) {
-                const int slot = it * G + gg;
-                const float d = __shfl(total, gg * LPR);
-                if (slot < top_k) {
-                    const int e = ids[slot];
-                    if (e >= 0 && e < experts) out = fmaf(weights[slot], d, out);
+            for (int q = 0; q < 8; ++q) {
+                const f32x4 t = *reinterpret_cast<const f32x4*>(xs + x_block_offset(col) + 16 * q);
+                xv[4 * q + 0] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
+            }
+            const float xref = Q4 ? reinterpret_cast<const float*>(xs + ref_off)[col] : 0.0f;
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+                for (int j = 0; j < J; ++j)
+                    *reinterpret_cast<u32x4*>(wl + gg * S::SEGP + 1024 * j + 16 * lane) = pre[it][gg][j];
+            issue(ni, np, it, more);  // the next step's segments of this slot group
+            wave_lds_sync();
+            if (li < nblk && my_slot < top_k) {
+                const uint32_t p = g * S::SEGP + li * BB;
+                acc[it] += Q4 ? block_dot_q4_mix(wl, p, xv, xref) : block_dot_q8(wl, p, xv);
+            }
+            wave_lds_sync();
+        }
+        if (cp == npass - 1) {
+            // Slot results to lane 0, then the ordered combine.
+            float out = 0.0f;
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                if (it >= groups) break;
+                const float total = group_sum<LPR>(acc[it]);
+#pragma unroll
+                for (int gg = 0; gg < G; ++gg) {
+                    const int slot = it * G + gg;
+                    const float d = __shfl(total, gg * LPR);
+                    if (slot < top_k && expert[slot] >= 0) out = fmaf(weights[slot], d, out);
                 }
             }
+            if (lane == 0) Y[ci] = accumulate ? Y[ci] + out : out;
         }
-        if (lane == 0) Y[i] = accumulate ? Y[i] + out : out;
+        ci = ni;
+        cp = np;
     }
 }
 
 template <uint32_t QT, int LPR>
 int launch_moe_down(const uint8_t* down, int experts, int H, int I, const int* ids, const float* weights,
-                    int top_k, const float* gu, float* Y, int accumulate, hipStream_t stream) {
+                    int top_k, const float* h, float* Y, int accumulate, hipStream_t stream) {
     using S = PipeShape<QT, LPR>;
     constexpr int kWaves = 8;
     const size_t row_bytes = static_cast<size_t>(I / kBlock) * (QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes);
@@ -512,7 +545,7 @@ int launch_moe_down(const uint8_t* down, int experts, int H, int I, const int* i
     if (lds > 64 * 1024 && !lds_ready) return Q3X_HIP_ERUNTIME;
     const int grid = std::min((H + kWaves - 1) / kWaves, kCUs * 2);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWaves * kWave), lds, stream, down, row_bytes * H, row_bytes,
-                       experts, ids, weights, top_k, gu, I, H, Y, accumulate);
+                       experts, ids, weights, top_k, h, I, H, Y, accumulate);
     return launch_status();
 }
 
@@ -521,21 +554,24 @@ int moe_decode(const uint8_t* gate_up, const uint8_t* down, int experts, int H, 
                const int* ids, const float* weights, int top_k, float* Y, int accumulate,
                uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
     constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
-    float* gu = reinterpret_cast<float*>(ws + L.gu);
+    float* h = reinterpret_cast<float*>(ws + L.gu);  // [top_k, I]
     const size_t gu_row = static_cast<size_t>(H / kBlock) * BB;
     const size_t down_row = static_cast<size_t>(I / kBlock) * BB;
     const bool staged = aligned(gate_up, 16) && aligned(X, 16) && gu_row % 16 == 0 && aligned(down, 16) &&
                         down_row % 16 == 0;
     if (staged) {
-        ExpertRows gate{gate_up, gu_row * 2 * I, gu_row, 2 * I, experts, ids, top_k, X, gu, {}};
-        int status = launch_pipe_for<QT>(gate, top_k * 2 * I, H / kBlock, stream);
+        ExpertGateUpRows gate{};
+        static_cast<ExpertRows&>(gate) = ExpertRows{gate_up, gu_row * 2 * I, gu_row, 2 * I, experts, ids, top_k, X, h, {}};
+        gate.I = I;
+        // One 64-lane row group, two row iterations (gate, up) per step.
+        int status = launch_pipe<QT, 64, 2>(gate, top_k * 2 * I, H / kBlock, 16, stream, 2);
         if (status == Q3X_HIP_OK) {
             const int bpr = I / kBlock;
-            status = bpr <= 16   ? launch_moe_down<QT, 16>(down, experts, H, I, ids, weights, top_k, gu, Y,
+            status = bpr <= 16   ? launch_moe_down<QT, 16>(down, experts, H, I, ids, weights, top_k, h, Y,
                                                            accumulate, stream)
-                     : bpr <= 32 ? launch_moe_down<QT, 32>(down, experts, H, I, ids, weights, top_k, gu, Y,
+                     : bpr <= 32 ? launch_moe_down<QT, 32>(down, experts, H, I, ids, weights, top_k, h, Y,
                                                            accumulate, stream)
-                                 : launch_moe_down<QT, 64>(down, experts, H, I, ids, weights, top_k, gu, Y,
+                                 : launch_moe_down<QT, 64>(down, experts, H, I, ids, weights, top_k, h, Y,
                                                            accumulate, stream);
         }
         if (status != Q3X_HIP_ENOTSUP) return status;
@@ -628,8 +664,14 @@ extern "C" int q3x_hip_router_topk(const float* logits, int tokens, int experts,
     if (!logits || !ids || !weights || tokens <= 0 || experts <= 0 || experts > kRouterMaxExperts ||
         top_k <= 0 || top_k > experts || top_k > kRouterMaxTopK)
         return Q3X_HIP_EINVAL;
-    hipLaunchKernelGGL(router_topk_kernel, dim3((tokens + 3) / 4), dim3(256), 0, stream, logits, tokens,
-                       experts, top_k, ids, weights);
+    const dim3 grid((tokens + 3) / 4), block(256);
+    if (experts <= 4 * kWave)
+        hipLaunchKernelGGL(router_topk_kernel<4>, grid, block, 0, stream, logits, tokens, experts, top_k, ids, weights);
+    else if (experts <= 8 * kWave)
+        hipLaunchKernelGGL(router_topk_kernel<8>, grid, block, 0, stream, logits, tokens, experts, top_k, ids, weights);
+    else
+        hipLaunchKernelGGL(router_topk_kernel<16>, grid, block, 0, stream, logits, tokens, experts, top_k, ids,
+                           weights);
     return launch_status();
 }
 

@@ -20,6 +20,7 @@ __device__ __forceinline__ float silu_ref(float x) { return x * sigmoid_ref(x); 
 template <bool ACCUMULATE>
 struct DenseRows {
     static constexpr bool kSharedInput = true;  // every row reads x
+    static constexpr bool kSwiGLUPairs = false;  // rows are stored one by one
     const uint8_t* w;
     size_t row_bytes;
     const float* x;
@@ -39,6 +40,7 @@ struct DenseRows {
 // launch): y[r] = W[r] x, or y[r] += W[r] x when `accumulate`.
 struct OneMatrix {
     static constexpr bool kSharedInput = true;
+    static constexpr bool kSwiGLUPairs = false;
     const uint8_t* w;  // null: every row reads as zeros (an expert id out of range)
     size_t row_bytes;
     const float* x;
@@ -160,7 +162,9 @@ struct ExpertRows {
         for (int s = 0; s < kMaxSlots; ++s)
             wave_end[s] = static_cast<int>((static_cast<long long>(GW) * (s < slots ? s + 1 : slots)) / slots);
     }
-    __device__ OneMatrix for_wave(int& gw, int& GW, int& nrows) const {
+    // The slot of wave gw; gw and GW become the wave's index and the wave
+    // count within that slot.
+    __device__ int slot_of_wave(int& gw, int& GW) const {
         int s = 0;
 #pragma unroll
         for (int i = 1; i < kMaxSlots; ++i)
@@ -174,10 +178,61 @@ struct ExpertRows {
         }
         gw -= first;
         GW = last - first;
-        nrows = rows_per_expert;
+        return s;
+    }
+    // Expert matrix of slot s (null when its id is out of range).
+    __device__ const uint8_t* expert_of_slot(int s) const {
         const int e = __builtin_amdgcn_readfirstlane(ids[s]);
-        const uint8_t* w = e >= 0 && e < experts ? pool + static_cast<size_t>(e) * expert_bytes : nullptr;
-        return OneMatrix{w, row_bytes, x, y + static_cast<size_t>(s) * rows_per_expert, false, pool};
+        return e >= 0 && e < experts ? pool + static_cast<size_t>(e) * expert_bytes : nullptr;
+    }
+    __device__ OneMatrix for_wave(int& gw, int& GW, int& nrows) const {
+        const int s = slot_of_wave(gw, GW);
+        nrows = rows_per_expert;
+        return OneMatrix{expert_of_slot(s), row_bytes, x, y + static_cast<size_t>(s) * rows_per_expert, false, pool};
+    }
+};
+
+// A wave's share of ExpertGateUpRows: the gate rows [0, I) and up rows
+// [I, 2I) of one expert's gate_up matrix, numbered so that the two row
+// iterations of a step (virtual rows v and v + GW, v = gw + 2b * GW) are gate
+// row q and up row q of the same q = gw + b * GW; the step stores
+// h[q] = silu(gate . x) * (up . x) (engine.cpp:413-416).  Pairs q >= I read
+// zeros and store nothing.
+struct GateUpPairs {
+    static constexpr bool kSharedInput = true;
+    static constexpr bool kSwiGLUPairs = true;
+    const uint8_t* w;  // null: expert id out of range (rows read as zeros)
+    size_t row_bytes;
+    const float* x;
+    float* h;
+    int I;
+    int GW;  // the waves of this slot: the stride of the wave's rows
+    const uint8_t* any_w;
+    __device__ int pair(int v) const { return v % GW + (v / GW / 2) * GW; }
+    __device__ const uint8_t* row(int v) const {
+        const int q = pair(v);
+        if (!w || q >= I) return nullptr;
+        return w + static_cast<size_t>((v / GW) % 2 * I + q) * row_bytes;
+    }
+    __device__ const uint8_t* any() const { return any_w; }
+    __device__ const float* input(int) const { return x; }
+    __device__ void store_pair(int v_gate, float gate, float up) const {
+        const int q = pair(v_gate);
+        if (q < I) h[q] = silu_ref(gate) * up;
+    }
+};
+
+// The decode step's gate_up matvec with SwiGLU applied: the experts of
+// ExpertRows (waves split evenly over the slots), each slot's result
+// h[slot * I + q] = silu(G_e[q] . x) * (U_e[q] . x).  For the pipelined
+// kernel with one row group of 64 lanes and two row iterations per step.
+struct ExpertGateUpRows : ExpertRows {
+    int I;
+    __device__ GateUpPairs for_wave(int& gw, int& GW, int& nrows) const {
+        const int s = slot_of_wave(gw, GW);
+        // Virtual rows: two per pair, every wave the same number of steps.
+        nrows = 2 * GW * ((I + GW - 1) / GW);
+        return GateUpPairs{expert_of_slot(s), row_bytes, x, y + static_cast<size_t>(s) * I, I, GW, pool};
     }
 };
 
