@@ -92,14 +92,6 @@ __device__ __forceinline__ float sbyte(uint32_t v) {
     return static_cast<float>(static_cast<int8_t>(v >> (8 * K)));
 }
 
-// Sum over groups of `width` consecutive lanes (width a power of two <= 64).
-template <int WIDTH>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int offset = WIDTH / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, WIDTH);
-    return v;
-}
-
 // Lane exchange inside rows of 16 lanes through DPP (no LDS round trip).
 // Controls (gfx9): quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E,
 // row_half_mirror (lane i <- 7-i of its 8) = 0x141, row_mirror (i <- 15-i) =
@@ -145,6 +137,28 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     v += dpp_f32<0x141>(v);
     v += dpp_f32<0x140>(v);
     return (read_lane_f32(v, 0) + read_lane_f32(v, 16)) + (read_lane_f32(v, 32) + read_lane_f32(v, 48));
+}
+
+// Sum over groups of WIDTH consecutive lanes (16, 32 or 64), returned to
+// every lane of the group: DPP sums inside each row of 16 lanes (pairs,
+// quads, eights, rows), then the row sums are added as scalars --
+// (r0 + r1) for a 32-lane group, (r0 + r1) + (r2 + r3) for the wave.  A
+// fixed order, so results are deterministic.  Call with every lane active.
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(WIDTH == 16 || WIDTH == 32 || WIDTH == 64, "group of 16, 32 or 64 lanes");
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    if constexpr (WIDTH == 16) {
+        return v;
+    } else {
+        const float r0 = read_lane_f32(v, 0), r1 = read_lane_f32(v, 16);
+        const float r2 = read_lane_f32(v, 32), r3 = read_lane_f32(v, 48);
+        if constexpr (WIDTH == 32) return (threadIdx.x & 32) ? r2 + r3 : r0 + r1;
+        else return (r0 + r1) + (r2 + r3);
+    }
 }
 
 // Orders LDS traffic of one wavefront: every lane's earlier LDS writes are

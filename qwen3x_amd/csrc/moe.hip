@@ -519,7 +519,7 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
 #pragma unroll
                 for (int gg = 0; gg < G; ++gg) {
                     const int slot = it * G + gg;
-                    const float d = __shfl(total, gg * LPR);
+                    const float d = read_lane_f32(total, gg * LPR);
                     if (slot < top_k && expert[slot] >= 0) out = fmaf(weights[slot], d, out);
                 }
             }
