@@ -269,12 +269,14 @@ __device__ __forceinline__ float q4_mix_reference(const float* xb) {
 }
 
 // Software-pipelined streaming kernel for inputs shared by every row (x held
-// in LDS, once per workgroup).  A wave works on G = 64 / LPR rows at a time,
+// in LDS, once per workgroup).  D: steps in flight per wave (a ring of
+// register buffers); WPE: minimum waves per SIMD the build must allow (8
+// caps it at 64 VGPRs).  A wave works on G = 64 / LPR rows at a time,
 // LPR lanes per row, one lane per 32-weight block column of an LPR-block
 // pass; it owns the strided rows gw, gw + GW, ... in batches of G * R.  A
 // step is one (batch, pass): its G * R row segments arrive in registers by
-// 16-byte buffer loads issued one step ahead, so the loads of step s+1 are in
-// flight while step s computes.  The G segments of a row iteration are
+// 16-byte buffer loads issued D steps ahead, so the loads of steps s+1..s+D
+// are in flight while step s computes.  The G segments of a row iteration are
 // written to the wave's LDS slice (reused iteration after iteration: LDS
 // executes a wave's operations in issue order) and read back block-wise.
 // Rows past the matrix, and the prefetch after the last step, use an empty
@@ -297,8 +299,8 @@ __host__ __device__ constexpr uint32_t pipe_x_bytes(uint32_t qt, int bpr) {
            (qt == Q3X_HIP_MATRIX_Q4_0 ? ((4u * bpr + 15u) & ~15u) : 0u);
 }
 
-template <uint32_t QT, int LPR, int R, class Rows>
-__global__ __launch_bounds__(1024) void mv_pipe_kernel(Rows all_rows, int nrows, int bpr) {
+template <uint32_t QT, int LPR, int R, int D, class Rows, int WPE>
+__global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int nrows, int bpr) {
     using S = PipeShape<QT, LPR>;
     constexpr int BB = S::BB, G = S::G, J = S::J, RS = G * R;
     constexpr bool Q4 = QT == Q3X_HIP_MATRIX_Q4_0;
@@ -320,10 +322,11 @@ __global__ __launch_bounds__(1024) void mv_pipe_kernel(Rows all_rows, int nrows,
     const int my_rows = gw < nrows ? (nrows - gw + GW - 1) / GW : 0;
     const int steps = (my_rows + RS - 1) / RS * npass;
 
-    u32x4 pre[RS][J];
-    // Loads of row i of step (batch b, pass p) into pre[i]; `live` false
+    // Ring of D steps in flight: step s lives in pre[s % D].
+    u32x4 pre[D][RS][J];
+    // Loads of row i of step (batch b, pass p) into pre[d][i]; `live` false
     // gives zeros.
-    auto issue_row = [&](int b, int p, int i, bool live) {
+    auto issue_row = [&](int d, int b, int p, int i, bool live) {
         const int row = gw + (b * RS + i) * GW;
         const int b0 = p * LPR;
         const uint8_t* base = live && row < nrows ? rows.row(row) : nullptr;  // null: expert id out of range
@@ -333,10 +336,15 @@ __global__ __launch_bounds__(1024) void mv_pipe_kernel(Rows all_rows, int nrows,
             __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src), 0, bytes, kBufferFlags);
 #pragma unroll
         for (int j = 0; j < J; ++j)
-            pre[i][j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * lane + 1024 * j, 0, kNonTemporal);
+            pre[d][i][j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * lane + 1024 * j, 0, kNonTemporal);
     };
+    int qb = 0, qp = 0;  // batch and pass of the next step to request
 #pragma unroll
-    for (int i = 0; i < RS; ++i) issue_row(0, 0, i, steps > 0);
+    for (int d = 0; d < D; ++d) {
+#pragma unroll
+        for (int i = 0; i < RS; ++i) issue_row(d, qb, qp, i, d < steps);
+        if (++qp == npass) { qp = 0; ++qb; }
+    }
 
     // x into LDS once per workgroup (overlaps the first weight loads), then
     // the per-block references for Q4_0.
@@ -356,60 +364,63 @@ __global__ __launch_bounds__(1024) void mv_pipe_kernel(Rows all_rows, int nrows,
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
     int cb = 0, cp = 0;  // current batch and pass
-    for (int s = 0; s < steps; ++s) {
-        int nb = cb, np = cp + 1;
-        if (np == npass) { np = 0; ++nb; }
-        const bool more = s + 1 < steps;
-        const int b0 = cp * LPR;
-        const int nblk = min(LPR, bpr - b0);
-        const int col = li < nblk ? b0 + li : 0;
-        float xv[32];
-        {
-            const uint8_t* xs = xl + x_block_offset(col);
+    for (int s0 = 0; s0 < steps; s0 += D) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const f32x4 t = *reinterpret_cast<const f32x4*>(xs + 16 * i);
-                xv[4 * i + 0] = t.x; xv[4 * i + 1] = t.y; xv[4 * i + 2] = t.z; xv[4 * i + 3] = t.w;
-            }
-        }
-        const float xref = Q4 ? sxl[col] : 0.0f;
+        for (int d = 0; d < D; ++d) {
+            const int s = s0 + d;
+            if (s >= steps) break;
+            const bool more = s + D < steps;
+            const int b0 = cp * LPR;
+            const int nblk = min(LPR, bpr - b0);
+            const int col = li < nblk ? b0 + li : 0;
+            float xv[32];
+            {
+                const uint8_t* xs = xl + x_block_offset(col);
 #pragma unroll
-        for (int it = 0; it < R; ++it) {
-#pragma unroll
-            for (int gg = 0; gg < G; ++gg) {
-#pragma unroll
-                for (int j = 0; j < J; ++j)
-                    *reinterpret_cast<u32x4*>(wl + gg * S::SEGP + 1024 * j + 16 * lane) = pre[it * G + gg][j];
-                issue_row(nb, np, it * G + gg, more);
-            }
-            wave_lds_sync();
-            if (li < nblk) {
-                const uint32_t p = g * S::SEGP + li * BB;
-                acc[it] += Q4 ? block_dot_q4_mix(wl, p, xv, xref) : block_dot_q8(wl, p, xv);
-            }
-            wave_lds_sync();
-        }
-        if (cp == npass - 1) {
-            if constexpr (decltype(rows)::kSwiGLUPairs) {
-                // Iteration 0 is a gate row, iteration 1 its up row.
-                static_assert(R == 2 && G == 1, "SwiGLU pairs need two row iterations of one row group");
-                const float gate = group_sum<LPR>(acc[0]);
-                const float up = group_sum<LPR>(acc[1]);
-                const int row = gw + cb * RS * GW;
-                if (li == 0 && row < nrows) rows.store_pair(row, gate, up);
-                acc[0] = acc[1] = 0.0f;
-            } else {
-#pragma unroll
-                for (int it = 0; it < R; ++it) {
-                    const float total = group_sum<LPR>(acc[it]);
-                    const int row = gw + (cb * RS + it * G + g) * GW;
-                    if (li == 0 && row < nrows) rows.store(row, rows.previous(row) + total);
-                    acc[it] = 0.0f;
+                for (int i = 0; i < 8; ++i) {
+                    const f32x4 t = *reinterpret_cast<const f32x4*>(xs + 16 * i);
+                    xv[4 * i + 0] = t.x; xv[4 * i + 1] = t.y; xv[4 * i + 2] = t.z; xv[4 * i + 3] = t.w;
                 }
             }
+            const float xref = Q4 ? sxl[col] : 0.0f;
+#pragma unroll
+            for (int it = 0; it < R; ++it) {
+#pragma unroll
+                for (int gg = 0; gg < G; ++gg) {
+#pragma unroll
+                    for (int j = 0; j < J; ++j)
+                        *reinterpret_cast<u32x4*>(wl + gg * S::SEGP + 1024 * j + 16 * lane) = pre[d][it * G + gg][j];
+                    issue_row(d, qb, qp, it * G + gg, more);  // step s + D into the slot just emptied
+                }
+                wave_lds_sync();
+                if (li < nblk) {
+                    const uint32_t p = g * S::SEGP + li * BB;
+                    acc[it] += Q4 ? block_dot_q4_mix(wl, p, xv, xref) : block_dot_q8(wl, p, xv);
+                }
+                wave_lds_sync();
+            }
+            if (++qp == npass) { qp = 0; ++qb; }
+            if (cp == npass - 1) {
+                if constexpr (decltype(rows)::kSwiGLUPairs) {
+                    // Iteration 0 is a gate row, iteration 1 its up row.
+                    static_assert(R == 2 && G == 1, "SwiGLU pairs need two row iterations of one row group");
+                    const float gate = group_sum<LPR>(acc[0]);
+                    const float up = group_sum<LPR>(acc[1]);
+                    const int row = gw + cb * RS * GW;
+                    if (li == 0 && row < nrows) rows.store_pair(row, gate, up);
+                    acc[0] = acc[1] = 0.0f;
+                } else {
+#pragma unroll
+                    for (int it = 0; it < R; ++it) {
+                        const float total = group_sum<LPR>(acc[it]);
+                        const int row = gw + (cb * RS + it * G + g) * GW;
+                        if (li == 0 && row < nrows) rows.store(row, rows.previous(row) + total);
+                        acc[it] = 0.0f;
+                    }
+                }
+            }
+            if (++cp == npass) { cp = 0; ++cb; }
         }
-        cb = nb;
-        cp = np;
     }
 }
 
@@ -524,10 +535,10 @@ inline int launch_staged(const Rows& rows, int nrows, int bpr, hipStream_t strea
 // fewest that the resident waves allow, and the grid then shrinks so that
 // every wave gets B full batches (balanced), spreading the waves over all
 // CUs (fewer per workgroup) when there are fewer than 256 workgroups' worth.
-template <uint32_t QT, int LPR, int R, class Rows>
+template <uint32_t QT, int LPR, int R, class Rows, int D = 1, int WPE = 4>
 inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_t stream, int per_cu = 1) {
     using S = PipeShape<QT, LPR>;
-    auto kernel = mv_pipe_kernel<QT, LPR, R, Rows>;
+    auto kernel = mv_pipe_kernel<QT, LPR, R, D, Rows, WPE>;
     static const bool lds_ready =
         hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(kLdsPerCU)) == hipSuccess;
@@ -554,15 +565,24 @@ inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_
 }
 
 // Shapes measured on MI355X (rows per step x waves per workgroup x
-// workgroups per CU): Q8_0 streams best with one row per step; Q4_0, whose
-// rows are half as long, with two; large matrices gain from a second
-// 16-wave workgroup per CU (more, shorter waves: the grid drains evenly).
+// workgroups per CU x prefetch depth): Q8_0 streams best with one row per
+// step; Q4_0, whose rows are half as long, with two; large matrices gain from
+// a grid of two 16-wave workgroups per CU (more, shorter waves: the grid
+// drains evenly).  Prefetching two or three steps ahead measured slower at
+// every size (the registers cost more occupancy than the extra bytes in
+// flight gain), so the launches use one.
 template <uint32_t QT, class Rows>
 inline int launch_pipe_for(const Rows& rows, int nrows, int bpr, hipStream_t stream) {
     if (bpr <= 16) return launch_pipe<QT, 16, 1>(rows, nrows, bpr, 16, stream);
     if (bpr <= 32) return launch_pipe<QT, 32, 1>(rows, nrows, bpr, 16, stream);
-    if (QT == Q3X_HIP_MATRIX_Q8_0)
+    if (QT == Q3X_HIP_MATRIX_Q8_0) {
+        // 16K-64K rows (e.g. a gate|up pair): a 64-VGPR build, so that two
+        // 16-wave workgroups are resident per CU (the default build needs 68
+        // VGPRs, 7 waves per SIMD); taller matrices stream better without.
+        if (nrows >= 16384 && nrows <= 65536)
+            return launch_pipe<QT, 64, 1, Rows, 1, 8>(rows, nrows, bpr, 16, stream, 2);
         return launch_pipe<QT, 64, 1>(rows, nrows, bpr, 16, stream, nrows >= 8192 ? 2 : 1);
+    }
     // Short Q4_0 rows that 64-block passes would leave partly idle (e.g. 160
     // blocks = 2.5 passes) take 32 lanes per row (two rows per pass).  The
     // lanes per row depend on the row length only, so the per-row reduction

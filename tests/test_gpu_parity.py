@@ -192,6 +192,9 @@ def test_mv_zero_rows_are_exactly_zero():
     (Q8_0, 2048, [1, 7, 100, 2049, 33, 5, 64, 900], [True, False] * 4),  # 8 matrices
     (Q4_0, 512, [70, 3], [False, True]),                       # 16 lanes per row
     (Q8_0, 96, [5, 3], [False, True]),                         # rows not 16-byte multiples: generic path
+    # 21288 rows together take the 64-VGPR build of 16K-64K-row Q8_0 launches,
+    # each matrix alone the default build: same arithmetic, same bits
+    (Q8_0, 1024, [12288, 9000], [False, True]),
 ])
 def test_mv_multi_equals_separate_mv(type_, cols, rows_list, acc):
     torch = _torch()
