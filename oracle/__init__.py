@@ -38,6 +38,8 @@ _SIGS = {
     "q3xo_router_top_k": (_I, [_P, _I, _I, _P, _P, _P]),
     "q3xo_moe_routed": (_I, [_P, _P, _U, _I, _I, _I, _P, _I, _P, _P, _I, _P, _I]),
     "q3xo_quantize": (_I, [_U, _P, _S, _P]),
+    "q3xo_mv_bf16": (_I, [_P, _I, _I, _P, _P]),
+    "q3xo_moe_layer": (_I, [_P, _P, _P, _P, _P, _P, _P, _U, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _I]),
 }
 _REF_SIGS = {
     "q3xr_quantized_bytes": (_I, [_U, _I, _I, ctypes.POINTER(_S)]),
@@ -47,6 +49,8 @@ _REF_SIGS = {
     "q3xr_sigmoid": (_F, [_F]),
     "q3xr_silu": (_F, [_F]),
     "q3xr_moe_q4": (None, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P]),
+    "q3xr_mv_bf16": (None, [_P, _I, _I, _P, _P]),
+    "q3xr_moe_layer": (None, [_U, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
 }
 
 _lib = None
@@ -164,6 +168,35 @@ def moe_routed(gate_up: np.ndarray, down: np.ndarray, type_: int, experts: int, 
     assert lib().q3xo_moe_routed(_p(gate_up), _p(down), type_, experts, H, I, _p(X), T, _p(ids), _p(weights),
                                  top_k, _p(Y), threads or default_threads())
     return Y
+
+
+def mv_bf16(weights: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """y = W x for a BF16 matrix given as uint16 [rows, cols] (engine.cpp:200-212)."""
+    weights = np.ascontiguousarray(weights, np.uint16)
+    x = np.ascontiguousarray(x, np.float32)
+    rows, cols = weights.shape
+    y = np.empty(rows, np.float32)
+    assert lib().q3xo_mv_bf16(_p(weights), rows, cols, _p(x), _p(y))
+    return y
+
+
+def moe_layer(router: np.ndarray, gate_up: np.ndarray, down: np.ndarray, shared_gate: np.ndarray,
+              shared_up: np.ndarray, shared_down: np.ndarray, shared_scale: np.ndarray, type_: int,
+              experts: int, H: int, I: int, shared_I: int, top_k: int, X: np.ndarray,
+              threads: int | None = None):
+    """The whole MoE layer (engine.cpp:406-430) for every row of X.
+    Returns (Y [T, H], ids [T, top_k], weights [T, top_k])."""
+    X = np.ascontiguousarray(np.atleast_2d(X), np.float32)
+    T = X.shape[0]
+    Y = np.empty((T, H), np.float32)
+    ids = np.empty((T, top_k), np.int32)
+    weights = np.empty((T, top_k), np.float32)
+    router = np.ascontiguousarray(router, np.uint16)
+    shared_scale = np.ascontiguousarray(shared_scale, np.uint16)
+    assert lib().q3xo_moe_layer(_p(router), _p(gate_up), _p(down), _p(shared_gate), _p(shared_up),
+                                _p(shared_down), _p(shared_scale), type_, experts, H, I, shared_I, top_k,
+                                _p(X), T, _p(Y), _p(ids), _p(weights), threads or default_threads())
+    return Y, ids, weights
 
 
 def quantize(type_: int, values: np.ndarray) -> np.ndarray:

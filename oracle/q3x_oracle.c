@@ -314,6 +314,124 @@ int q3xo_moe_routed(const void* gate_up, const void* down, uint32_t type,
     return 1;
 }
 
+/* ---- the BF16 matvec and the whole MoE layer ---- */
+
+/* engine.cpp:181-185 */
+static float bf16_value(uint16_t value) {
+    const uint32_t bits = (uint32_t)value << 16;
+    float result;
+    memcpy(&result, &bits, sizeof(result));
+    return result;
+}
+
+/* engine.cpp:200-205: sum += f32(a) * b, contracted to an FMA by the build. */
+static float dot_bf16(const uint16_t* a, const float* b, int n) {
+    float sum = 0.0f;
+    for (int i = 0; i < n; ++i) sum = fmaf(bf16_value(a[i]), b[i], sum);
+    return sum;
+}
+
+/* engine.cpp:207-212 (the BF16 branch of mv) */
+int q3xo_mv_bf16(const uint16_t* weights, int rows, int cols, const float* x, float* y) {
+    if (rows <= 0 || cols <= 0) return 0;
+    for (int r = 0; r < rows; ++r) y[r] = dot_bf16(weights + (size_t)r * cols, x, cols);
+    return 1;
+}
+
+typedef struct {
+    const uint16_t* router; const uint8_t* gate_up; const uint8_t* down;
+    const uint8_t* shared_gate; const uint8_t* shared_up; const uint8_t* shared_down;
+    const uint16_t* shared_scale; uint32_t type;
+    int experts, H, I, shared_I, top_k;
+    const float* X; float* Y; int* ids; float* weights;
+    size_t gate_up_stride, down_stride;
+    int t0, t1; int ok;
+} layer_job;
+
+/* engine.cpp:406-430 for tokens [t0, t1). */
+static void* layer_worker(void* arg) {
+    layer_job* job = (layer_job*)arg;
+    const int H = job->H, I = job->I, SI = job->shared_I, E = job->experts, K = job->top_k;
+    /* logits, probabilities, gate_up (2I), delta (H) */
+    float* logits = (float*)malloc(sizeof(float) * ((size_t)2 * E + 2 * I + H));
+    if (!logits) { job->ok = 0; return NULL; }
+    float* probabilities = logits + E;
+    float* gate_up = probabilities + E;
+    float* delta = gate_up + 2 * I;
+    int ids[64];
+    float weights[64];
+    for (int t = job->t0; t < job->t1 && job->ok; ++t) {
+        const float* input = job->X + (size_t)t * H;
+        float* out = job->Y + (size_t)t * H;
+        q3xo_mv_bf16(job->router, E, H, input, logits);                       /* :408 */
+        if (!q3xo_router_top_k(logits, E, K, ids, weights, probabilities)) {  /* :409 */
+            job->ok = 0;
+            break;
+        }
+        for (int i = 0; i < H; ++i) out[i] = 0.0f;                            /* :411 */
+        for (int slot = 0; slot < K; ++slot) {                                /* :412-420 */
+            const int expert = ids[slot];
+            q3xo_mv_rows(job->gate_up + (size_t)expert * job->gate_up_stride, job->type, 0, 2 * I, H,
+                         input, gate_up);
+            for (int i = 0; i < I; ++i) gate_up[i] = q3xo_silu(gate_up[i]) * gate_up[I + i];
+            q3xo_mv_rows(job->down + (size_t)expert * job->down_stride, job->type, 0, H, I, gate_up, delta);
+            for (int i = 0; i < H; ++i) out[i] = fmaf(weights[slot], delta[i], out[i]);
+        }
+        /* :422-429: gate into gate_up[0, SI), up into gate_up[I, I + SI) */
+        q3xo_mv_rows(job->shared_gate, job->type, 0, SI, H, input, gate_up);
+        q3xo_mv_rows(job->shared_up, job->type, 0, SI, H, input, gate_up + I);
+        for (int i = 0; i < SI; ++i) gate_up[i] = q3xo_silu(gate_up[i]) * gate_up[I + i];
+        q3xo_mv_rows(job->shared_down, job->type, 0, H, SI, gate_up, delta);
+        const float scale = q3xo_sigmoid(dot_bf16(job->shared_scale, input, H));
+        for (int i = 0; i < H; ++i) out[i] = fmaf(scale, delta[i], out[i]);
+        for (int slot = 0; slot < K; ++slot) {
+            if (job->ids) job->ids[(size_t)t * K + slot] = ids[slot];
+            if (job->weights) job->weights[(size_t)t * K + slot] = weights[slot];
+        }
+    }
+    free(logits);
+    return NULL;
+}
+
+int q3xo_moe_layer(const uint16_t* router, const void* gate_up, const void* down,
+                   const void* shared_gate, const void* shared_up, const void* shared_down,
+                   const uint16_t* shared_scale, uint32_t type, int experts, int H, int I,
+                   int shared_I, int top_k, const float* X, int tokens, float* Y, int* ids,
+                   float* weights, int threads) {
+    size_t gu_bytes, down_bytes, sg_bytes, sd_bytes;
+    if (experts <= 0 || tokens <= 0 || top_k <= 0 || top_k > experts || top_k > 64) return 0;
+    if (shared_I <= 0 || shared_I > I) return 0;
+    if (!q3xo_quantized_bytes(type, 2 * I, H, &gu_bytes)) return 0;
+    if (!q3xo_quantized_bytes(type, H, I, &down_bytes)) return 0;
+    if (!q3xo_quantized_bytes(type, shared_I, H, &sg_bytes)) return 0;
+    if (!q3xo_quantized_bytes(type, H, shared_I, &sd_bytes)) return 0;
+    if (threads < 1) threads = 1;
+    if (threads > tokens) threads = tokens;
+    if (threads > 256) threads = 256;
+    layer_job jobs[256];
+    pthread_t tids[256];
+    for (int t = 0; t < threads; ++t) {
+        layer_job* j = &jobs[t];
+        j->router = router; j->gate_up = (const uint8_t*)gate_up; j->down = (const uint8_t*)down;
+        j->shared_gate = (const uint8_t*)shared_gate; j->shared_up = (const uint8_t*)shared_up;
+        j->shared_down = (const uint8_t*)shared_down; j->shared_scale = shared_scale; j->type = type;
+        j->experts = experts; j->H = H; j->I = I; j->shared_I = shared_I; j->top_k = top_k;
+        j->X = X; j->Y = Y; j->ids = ids; j->weights = weights;
+        j->gate_up_stride = gu_bytes; j->down_stride = down_bytes;
+        j->t0 = (int)((long long)tokens * t / threads);
+        j->t1 = (int)((long long)tokens * (t + 1) / threads);
+        j->ok = 1;
+    }
+    if (threads == 1) {
+        layer_worker(&jobs[0]);
+    } else {
+        for (int t = 0; t < threads; ++t) pthread_create(&tids[t], NULL, layer_worker, &jobs[t]);
+        for (int t = 0; t < threads; ++t) pthread_join(tids[t], NULL);
+    }
+    for (int t = 0; t < threads; ++t) if (!jobs[t].ok) return 0;
+    return 1;
+}
+
 /* ---- scripts/pack_weights.py:299-343 quantizers on float32 values ---- */
 
 /* numpy float32 -> float16 cast: IEEE round-to-nearest-even, overflow to inf. */

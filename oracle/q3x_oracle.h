@@ -59,6 +59,20 @@ int q3xo_moe_routed(const void* gate_up, const void* down, uint32_t type,
                     int experts, int H, int I, const float* X, int tokens,
                     const int* ids, const float* weights, int top_k, float* Y,
                     int threads);
+/* y[r] = BF16 row r . x for r < rows (engine.cpp:181-212: f32(bf16) is the
+ * value's bits shifted up 16, the dot a sequential FMA chain).  1 = ok. */
+int q3xo_mv_bf16(const uint16_t* weights, int rows, int cols, const float* x, float* y);
+/* The whole MoE layer of engine.cpp:406-430 for `tokens` tokens: BF16 router
+ * [E, H] -> top_k -> routed experts (as q3xo_moe_routed) -> shared expert
+ * (shared_gate/up [shared_I, H], shared_down [H, shared_I], same type as the
+ * experts) scaled by sigmoid(BF16 shared_scale [1, H] . x) and added last.
+ * ids/weights (optional, [tokens, top_k]) receive the routing.  Requires
+ * shared_I <= I (the reference reuses its 2I gate_up buffer).  1 = ok. */
+int q3xo_moe_layer(const uint16_t* router, const void* gate_up, const void* down,
+                   const void* shared_gate, const void* shared_up, const void* shared_down,
+                   const uint16_t* shared_scale, uint32_t type, int experts, int H, int I,
+                   int shared_I, int top_k, const float* X, int tokens, float* Y, int* ids,
+                   float* weights, int threads);
 /* pack_weights.py quantizers applied to float32 values (n % 32 == 0).
  * 1 = ok, 0 = partial block or non-finite input. */
 int q3xo_quantize(uint32_t type, const float* values, size_t n, void* out);

@@ -78,4 +78,40 @@ void q3xr_moe_q4(const uint16_t* router, const void* gate_up, const void* down,
     for (int slot = 0; slot < top_k; ++slot) ids[slot] = work.expert_ids[slot];
 }
 
+
+// engine.cpp:207-212, the BF16 branch of mv().
+void q3xr_mv_bf16(const uint16_t* weights, int rows, int cols, const float* x, float* y) {
+    q3x_backend::mv({weights, rows, cols, q3x_model::MATRIX_BF16}, x, y);
+}
+
+// engine.cpp:406-430 for one token with every weight given: BF16 router
+// [E, H] and shared_scale [1, H]; experts gate_up [E, 2I, H], down [E, H, I]
+// and the shared expert (gate/up [shared_I, H], down [H, shared_I]) of
+// `type`.  shared_I <= I (moe() writes the shared up output at
+// ffn_gate_up + I).  `ids` receives the selected experts.
+void q3xr_moe_layer(uint32_t type, const uint16_t* router, const void* gate_up, const void* down,
+                    const void* shared_gate, const void* shared_up, const void* shared_down,
+                    const uint16_t* shared_scale, int experts, int H, int I, int shared_I, int top_k,
+                    const float* input, float* out, int* ids) {
+    const auto t = static_cast<q3x_model::MatrixType>(type);
+    // Work (engine.cpp:84-110) sizes delta_output, which moe() reuses for the
+    // down outputs of H floats, as VH * VD: take VD = H.
+    const q3x_model::ModelConfig config {
+        1, "synthetic-MoE", 64, H, I, 1,
+        1, 1, 1, 32, 16, 1, 1, 32, H, 4,
+        experts, top_k, shared_I, t, false,
+    };
+    q3x_backend::MoeWeights weights {
+        {router, experts, H, q3x_model::MATRIX_BF16},
+        {gate_up, experts, 2 * I, H, t},
+        {down, experts, H, I, t},
+        {shared_gate, shared_I, H, t},
+        {shared_up, shared_I, H, t},
+        {shared_down, H, shared_I, t},
+        {shared_scale, 1, H, q3x_model::MATRIX_BF16},
+    };
+    q3x_backend::Work work(config);
+    q3x_backend::moe(weights, input, work, out, config);
+    for (int slot = 0; slot < top_k; ++slot) ids[slot] = work.expert_ids[slot];
+}
 }  // extern "C"

@@ -8,7 +8,11 @@ Each .npz holds seeded inputs and the reference's outputs for them:
   silu.npz                   engine.cpp sigmoid / silu
   moe_q4_0.npz               engine.cpp moe() with a BF16 router and a zero
                              shared expert (routed experts only)
-Run: python tests/golden/make_golden.py   (needs the reference build)
+  moe_layer_q8_0.npz         engine.cpp moe() with every weight real (BF16
+                             router and shared-expert gate, Q8_0 experts and
+                             shared expert) and the BF16 mv() of the router
+Run: python tests/golden/make_golden.py [fixture ...]   (needs the reference
+build; with names, only those fixtures are written)
 """
 import os
 import sys
@@ -85,15 +89,47 @@ def moe_fixture(ref):
                         logits=logits, ids=ids, Y=Y, shape=np.array([E, H, I, k], np.int64))
 
 
+def moe_layer_fixture(ref):
+    rng = np.random.default_rng(20261213)
+    E, H, I, SI, k, T = 8, 64, 64, 32, 3, 4
+    bf16 = lambda rows, cols, s: (rng.normal(0, s, (rows, cols)).astype(np.float32).view(np.uint32)  # noqa: E731
+                                  >> 16).astype(np.uint16)
+    router = bf16(E, H, 0.5)
+    scale = bf16(1, H, 0.05)
+    gate_up = random_blocks(rng, Q8_0, E * 2 * I, H)
+    down = random_blocks(rng, Q8_0, E * H, I)
+    sg = random_blocks(rng, Q8_0, SI, H)
+    su = random_blocks(rng, Q8_0, SI, H)
+    sd = random_blocks(rng, Q8_0, H, SI)
+    X = rng.normal(0, 1, (T, H)).astype(np.float32)
+    logits = np.empty((T, E), np.float32)
+    ids = np.empty((T, k), np.int32)
+    Y = np.empty((T, H), np.float32)
+    for t in range(T):
+        ref.q3xr_mv_bf16(p(router), E, H, p(X[t]), p(logits[t]))
+        ref.q3xr_moe_layer(Q8_0, p(router), p(gate_up), p(down), p(sg), p(su), p(sd), p(scale), E, H, I, SI, k,
+                           p(X[t]), p(Y[t]), p(ids[t]))
+    np.savez_compressed(os.path.join(HERE, "moe_layer_q8_0.npz"), router=router, shared_scale=scale,
+                        gate_up=gate_up, down=down, shared_gate=sg, shared_up=su, shared_down=sd, X=X,
+                        logits=logits, ids=ids, Y=Y, shape=np.array([E, H, I, SI, k], np.int64))
+
+
+FIXTURES = {
+    "mv_q8_0": lambda ref: mv_fixture(ref, Q8_0, "mv_q8_0.npz"),
+    "mv_q4_0": lambda ref: mv_fixture(ref, Q4_0, "mv_q4_0.npz"),
+    "router": router_fixture,
+    "silu": silu_fixture,
+    "moe_q4_0": moe_fixture,
+    "moe_layer_q8_0": moe_layer_fixture,
+}
+
+
 def main():
     ref = oracle.ref()
     if ref is None:
         raise SystemExit("oracle/_ref/libq3x_ref.so is missing: run `make -C oracle ref` first")
-    mv_fixture(ref, Q8_0, "mv_q8_0.npz")
-    mv_fixture(ref, Q4_0, "mv_q4_0.npz")
-    router_fixture(ref)
-    silu_fixture(ref)
-    moe_fixture(ref)
+    for name in sys.argv[1:] or FIXTURES:
+        FIXTURES[name](ref)
     print("golden fixtures written to", HERE)
 
 

@@ -62,6 +62,18 @@ def test_moe_matches_reference_fixture():
     assert np.array_equal(bits(Y + np.float32(0.0)), bits(f["Y"]))
 
 
+def test_moe_layer_matches_reference_fixture():
+    # engine.cpp moe() with every weight real, and the BF16 router mv().
+    f = load("moe_layer_q8_0.npz")
+    E, H, I, SI, k = (int(v) for v in f["shape"])
+    for t in range(f["X"].shape[0]):
+        assert np.array_equal(bits(oracle.mv_bf16(f["router"], f["X"][t])), bits(f["logits"][t]))
+    Y, ids, _ = oracle.moe_layer(f["router"], f["gate_up"], f["down"], f["shared_gate"], f["shared_up"],
+                                 f["shared_down"], f["shared_scale"], Q8_0, E, H, I, SI, k, f["X"], threads=1)
+    assert np.array_equal(ids, f["ids"])
+    assert np.array_equal(bits(Y), bits(f["Y"]))
+
+
 @pytest.mark.parametrize("type_,key", [(Q8_0, "q8_0"), (Q4_0, "q4_0")])
 def test_quantizer_matches_reference_packer_fixture(type_, key):
     # Vectors from scripts/pack_weights.py quantize_q8_0 / quantize_q4_0

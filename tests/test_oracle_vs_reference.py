@@ -102,3 +102,47 @@ def test_moe_routed_bit_exact_against_reference_moe(experts, H, I, top_k):
         y = oracle.moe_routed(gate_up, down, Q4_0, experts, H, I, x, ids, weights, threads=1)
         # shared expert adds sigmoid(0) * 0: -0.0 becomes +0.0, nothing else changes
         assert np.array_equal(bits(y[0] + np.float32(0.0)), bits(out_r))
+
+
+def bf16_matrix(rng, rows, cols, scale):
+    """Random BF16 values (float32 truncated to its top 16 bits) as uint16."""
+    return (rng.normal(0, scale, (rows, cols)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 64), (256, 2048), (7, 1000)])
+def test_mv_bf16_bit_exact(rows, cols):
+    rng = np.random.default_rng(rows * 7 + cols)
+    w = bf16_matrix(rng, rows, cols, 0.05)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    y_ref = np.empty(rows, np.float32)
+    ref.q3xr_mv_bf16(_p(w), rows, cols, _p(x), _p(y_ref))
+    assert np.array_equal(bits(oracle.mv_bf16(w, x)), bits(y_ref))
+
+
+@pytest.mark.parametrize("type_,experts,H,I,shared_I,top_k", [
+    (Q4_0, 8, 64, 32, 32, 2),
+    (Q8_0, 16, 256, 64, 32, 8),        # shared expert narrower than the routed ones
+    (Q4_0, 256, 2048, 512, 512, 8),    # 35B-A3B shapes
+])
+def test_moe_layer_bit_exact_against_reference_moe(type_, experts, H, I, shared_I, top_k):
+    # The reference moe() (engine.cpp:406-430) with every weight real: BF16
+    # router and shared-expert gate, routed experts and shared expert of one
+    # quantised type; the oracle restates the whole layer.
+    rng = np.random.default_rng(experts + H + I + shared_I)
+    router = bf16_matrix(rng, experts, H, 0.5)
+    scale = bf16_matrix(rng, 1, H, 0.05)
+    gate_up = random_blocks(rng, type_, experts * 2 * I, H)
+    down = random_blocks(rng, type_, experts * H, I)
+    sg = random_blocks(rng, type_, shared_I, H)
+    su = random_blocks(rng, type_, shared_I, H)
+    sd = random_blocks(rng, type_, H, shared_I)
+    X = rng.normal(0, 1, (3 if experts < 256 else 1, H)).astype(np.float32)
+    Y, ids, _ = oracle.moe_layer(router, gate_up, down, sg, su, sd, scale, type_, experts, H, I, shared_I,
+                                 top_k, X, threads=1)
+    for t in range(X.shape[0]):
+        out_r = np.empty(H, np.float32)
+        ids_r = np.empty(top_k, np.int32)
+        ref.q3xr_moe_layer(type_, _p(router), _p(gate_up), _p(down), _p(sg), _p(su), _p(sd), _p(scale), experts,
+                           H, I, shared_I, top_k, _p(X[t]), _p(out_r), _p(ids_r))
+        assert np.array_equal(ids[t], ids_r)
+        assert np.array_equal(bits(Y[t]), bits(out_r))
