@@ -131,6 +131,40 @@ int q3x_hip_moe_routed(const void* gate_up, const void* down, uint32_t type,
                        int accumulate, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
 
+/* The weights of one MoE layer (the reference's MoeWeights, engine.cu:97-101,
+ * engine.cpp:53-57; shapes as model.bin lays them out, engine.cpp:543-550).
+ * Every pointer is a device pointer; the struct itself is read on the host. */
+typedef struct q3x_hip_moe_layer_weights {
+    const void* router;       /* BF16 [experts, H] (mlp.gate), 16-byte aligned */
+    const void* gate_up;      /* type [experts, 2I, H] */
+    const void* down;         /* type [experts, H, I] */
+    const void* shared_gate;  /* type [shared_I, H] */
+    const void* shared_up;    /* type [shared_I, H] */
+    const void* shared_down;  /* type [H, shared_I] */
+    const void* shared_scale; /* BF16 [1, H] (mlp.shared_expert_gate), 16-byte aligned */
+    uint32_t type;            /* Q8_0 or Q4_0: routed and shared experts */
+    int experts, top_k, H, I, shared_I;
+} q3x_hip_moe_layer_weights;
+
+/* Bytes of caller-owned workspace q3x_hip_moe_layer needs for `tokens`. */
+size_t q3x_hip_moe_layer_workspace_bytes(const q3x_hip_moe_layer_weights* layer, int tokens);
+
+/* The whole MoE layer for every token t (engine.cpp:406-430; CUDA moe(),
+ * engine.cu:1709-1736):
+ *   logits = router X[t] (BF16 matvec), top_k routing as q3x_hip_router_topk,
+ *   Y[t] = sum_slot w_slot Down_e(silu(G_e X[t]) * U_e X[t])      (slot order)
+ *   Y[t] += sigmoid(shared_scale . X[t]) *
+ *           shared_down(silu(shared_gate X[t]) * shared_up X[t])  (added last)
+ * Y is overwritten.  ids / weights ([tokens, top_k], device) receive the
+ * routing when not NULL.  Requires 1 <= top_k <= min(experts, 8), experts <=
+ * 1024, H, I, shared_I multiples of 32, shared_I <= I (the reference reuses
+ * its 2I gate_up buffer for the shared expert, engine.cpp:100-102, 422-423),
+ * X 16-byte aligned.  Replaces the routed path's caller-side router matvec,
+ * shared expert and scaled add (engine.cu:1711, 1728-1735). */
+int q3x_hip_moe_layer(const q3x_hip_moe_layer_weights* layer, const float* X, int tokens, float* Y,
+                      int* ids, float* weights, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+
 /* dst = Q8_0/Q4_0 blocks of src[rows, cols] (FP32), the quantizers of the
  * reference's packer (scripts/pack_weights.py:299-343) applied to FP32 input:
  * Q8_0 d = max|w|/127, q = clip(copysign(floor(|w/d| + 0.5)), +-127);

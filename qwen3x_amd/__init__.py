@@ -45,10 +45,21 @@ SIGNATURES = {
     "q3x_hip_moe_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),
     "q3x_hip_moe_routed": (_I, [_P, _P, _U, _I, _I, _I, _P, _I, _P, _P, _I, _P, _I, _P, _S, _P]),
     "q3x_hip_quantize": (_I, [_U, _P, _I, _I, _P, _P]),
+    "q3x_hip_moe_layer_workspace_bytes": (_S, [_P, _I]),
+    "q3x_hip_moe_layer": (_I, [_P, _P, _I, _P, _P, _P, _P, _S, _P]),
 }
 
 
 MV_MULTI_MAX = 8
+
+
+class MoeLayerWeights(ctypes.Structure):
+    """struct q3x_hip_moe_layer_weights of include/q3x_hip.h."""
+    _fields_ = [("router", ctypes.c_void_p), ("gate_up", ctypes.c_void_p), ("down", ctypes.c_void_p),
+                ("shared_gate", ctypes.c_void_p), ("shared_up", ctypes.c_void_p),
+                ("shared_down", ctypes.c_void_p), ("shared_scale", ctypes.c_void_p), ("type", ctypes.c_uint32),
+                ("experts", ctypes.c_int), ("top_k", ctypes.c_int), ("H", ctypes.c_int), ("I", ctypes.c_int),
+                ("shared_I", ctypes.c_int)]
 
 
 class MvItem(ctypes.Structure):
@@ -221,6 +232,52 @@ def moe_routed(gate_up: ExpertLinear, down: ExpertLinear, X, tokens: int, ids, w
            lib().q3x_hip_moe_routed(_ptr(gate_up.weight), _ptr(down.weight), gate_up.type, gate_up.experts, H, I,
                                     _ptr(X), tokens, _ptr(ids), _ptr(weights), top_k, _ptr(Y), int(accumulate),
                                     _ptr(workspace), workspace.numel(), _stream(stream)))
+    return Y
+
+
+@dataclass
+class MoeLayer:
+    """The weights of one MoE layer (reference MoeWeights, engine.cu:97-101):
+    BF16 router [experts, H] and shared_scale [1, H] as uint16 device tensors,
+    routed experts gate_up [experts, 2I, H] / down [experts, H, I] and the
+    shared expert gate/up [shared_I, H] / down [H, shared_I] as uint8 block
+    tensors of `type`."""
+    router: "object"
+    gate_up: "object"
+    down: "object"
+    shared_gate: "object"
+    shared_up: "object"
+    shared_down: "object"
+    shared_scale: "object"
+    type: int
+    experts: int
+    top_k: int
+    H: int
+    I: int
+    shared_I: int
+
+    def c_struct(self) -> MoeLayerWeights:
+        return MoeLayerWeights(_ptr(self.router), _ptr(self.gate_up), _ptr(self.down), _ptr(self.shared_gate),
+                               _ptr(self.shared_up), _ptr(self.shared_down), _ptr(self.shared_scale), self.type,
+                               self.experts, self.top_k, self.H, self.I, self.shared_I)
+
+
+def moe_layer_workspace_bytes(layer: MoeLayer, tokens: int) -> int:
+    return lib().q3x_hip_moe_layer_workspace_bytes(ctypes.byref(layer.c_struct()), tokens)
+
+
+def moe_layer(layer: MoeLayer, X, tokens: int, Y, ids=None, weights=None, workspace=None, stream=None):
+    """The whole MoE layer (engine.cpp:406-430): Y = routed experts + sigmoid-gated shared expert."""
+    torch = _torch()
+    _need_device(X, Y, layer.router, layer.gate_up, layer.down, layer.shared_gate, layer.shared_up,
+                 layer.shared_down, layer.shared_scale)
+    if workspace is None:
+        workspace = torch.empty(moe_layer_workspace_bytes(layer, tokens), dtype=torch.uint8, device=X.device)
+    c = layer.c_struct()
+    _check("q3x_hip_moe_layer",
+           lib().q3x_hip_moe_layer(ctypes.byref(c), _ptr(X), tokens, _ptr(Y), _ptr(ids) if ids is not None else None,
+                                   _ptr(weights) if weights is not None else None, _ptr(workspace),
+                                   workspace.numel(), _stream(stream)))
     return Y
 
 

@@ -1,5 +1,6 @@
-// gemm.h -- FP32-MFMA GEMM with on-the-fly Q8_0 / Q4_0 weight dequantisation
-// (prefill), shared by the dense prefill entry point and the MoE grouped GEMM.
+// gemm.h -- FP32-MFMA GEMM with on-the-fly Q8_0 / Q4_0 (or BF16) weight
+// conversion (prefill), shared by the dense prefill entry point, the MoE
+// grouped GEMM and the MoE layer's router and shared expert.
 //
 // C[m, n] = sum_k A[m, k] * B[k, n] with A = activations (tokens x cols, FP32,
 // row-major) and B = W^T (W = weight rows x cols, quantised).  MFMA's M
@@ -40,11 +41,22 @@ struct GemmTile {
 // (16-byte stores without bank conflicts); for Q4_0 that permutes the k order
 // inside a block, and the activation tile is stored with the same
 // permutation (a_chunk), so the products pair up unchanged.
+// BF16 (a router matrix): a "block" is 32 consecutive BF16 values (64 B),
+// raw[1 + i] holds two of them and a value is its bits shifted up 16
+// (engine.cpp:181-185), so the conversion is exact.
 template <uint32_t QT, int PARTS>
 struct BlockPart {
+    static constexpr bool kBF16 = QT == Q3X_HIP_MATRIX_BF16;
     static constexpr int N = 32 / PARTS;                    // elements
-    static constexpr int HALVES = QT == Q3X_HIP_MATRIX_Q8_0 ? N / 2 : N / 4;
+    static constexpr int HALVES = QT == Q3X_HIP_MATRIX_Q4_0 ? N / 4 : N / 2;
     __device__ static __forceinline__ void load(const uint8_t* blk, int part, uint32_t* raw) {
+        if constexpr (kBF16) {
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(blk);  // 4-byte aligned
+            raw[0] = 0;
+#pragma unroll
+            for (int i = 0; i < HALVES; ++i) raw[1 + i] = w[HALVES * part + i];
+            return;
+        }
         const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
         raw[0] = h[0];
 #pragma unroll
@@ -52,6 +64,14 @@ struct BlockPart {
     }
     // out[e] for e < N, in the column order of column().
     __device__ static __forceinline__ void dequant(const uint32_t* raw, float* out) {
+        if constexpr (kBF16) {
+#pragma unroll
+            for (int i = 0; i < HALVES; ++i) {
+                out[2 * i + 0] = __uint_as_float(raw[1 + i] << 16);
+                out[2 * i + 1] = __uint_as_float(raw[1 + i] & 0xffff0000u);
+            }
+            return;
+        }
         const float d = f16_fast(raw[0]);
 #pragma unroll
         for (int i = 0; i < HALVES; ++i) {
@@ -75,7 +95,7 @@ struct BlockPart {
     // 4c..4c+3).  Q4_0 with two parts: elements 0-7 | 16-23 | 8-15 | 24-31
     // go to columns 0-7 | 8-15 | 16-23 | 24-31, i.e. chunks 2,3 <-> 4,5.
     __device__ static __forceinline__ int a_chunk(int c) {
-        if (QT == Q3X_HIP_MATRIX_Q8_0 || PARTS == 1) return c;
+        if (QT != Q3X_HIP_MATRIX_Q4_0 || PARTS == 1) return c;
         return (c & 1) | ((c & 2) << 1) | ((c & 4) >> 1);
     }
 };
@@ -88,7 +108,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
     constexpr int NT = WM * WN * kWave;   // threads
     constexpr int BM = WM * TM * 32;
     constexpr int BN = WN * TN * 32;
-    constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
+    constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : QT == Q3X_HIP_MATRIX_Q4_0 ? kQ4Bytes : kBF16Bytes;
     // A tile load: BM rows x 8 float4 per stage.
     constexpr int A_VEC = BM * 8;
     constexpr int A_PER_T = (A_VEC + NT - 1) / NT;

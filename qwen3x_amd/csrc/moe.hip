@@ -374,22 +374,36 @@ __global__ __launch_bounds__(256) void combine4_kernel(const float* __restrict__
     *out = acc;
 }
 
+// The MoE layer's shared expert (engine.cpp:422-429) as the decode kernels
+// see it: gate / up [I, H], down [H, I], and the logit whose sigmoid weighs
+// its output.  down == nullptr: routed experts only.
+struct SharedExpert {
+    const uint8_t* gate = nullptr;
+    const uint8_t* up = nullptr;
+    const uint8_t* down = nullptr;
+    int I = 0;
+    const float* logit = nullptr;
+};
+
 // Decode (one token): the down projection of every selected expert, its
 // input h = silu(g) * u (engine.cpp:415-416, from the paired gate_up matvec)
 // staged in LDS, and the slot-order combine (engine.cpp:411, 418-419:
-// out = 0, then out += w * d per slot), in one kernel.  Wave gw computes the output rows
-// i = gw, gw + GW, ...: for each, the rows (slot s, i) of the top_k experts,
-// G = 64 / LPR slots at a time (one row group of LPR lanes per slot, one lane
-// per 32-weight block of a pass), then lane 0 adds the slots' results in
-// slot order from zero.  Slots whose id is out of range are skipped.
+// out = 0, then out += w * d per slot), in one kernel.  Wave gw computes the
+// output rows i = gw, gw + GW, ...: for each, the rows (slot s, i) of the
+// top_k experts, G = 64 / LPR slots at a time (one row group of LPR lanes per
+// slot, one lane per 32-weight block of a pass), then lane 0 adds the slots'
+// results in slot order from zero.  Slots whose id is out of range are
+// skipped.  With a shared expert, it is one more slot after the routed ones
+// (its h zero past shared.I), added last with weight sigmoid(*shared.logit)
+// (engine.cpp:427-429).
 template <uint32_t QT, int LPR>
 __global__ __launch_bounds__(512) void moe_down_combine_kernel(
     const uint8_t* __restrict__ down, size_t expert_bytes, size_t row_bytes, int experts,
     const int* __restrict__ ids, const float* __restrict__ weights, int top_k, const float* __restrict__ h,
-    int I, int H, float* __restrict__ Y, int accumulate) {
+    int I, int H, float* __restrict__ Y, int accumulate, SharedExpert shared) {
     using S = PipeShape<QT, LPR>;
     constexpr int BB = S::BB, G = S::G, J = S::J;
-    constexpr int IT = (kRouterMaxTopK + G - 1) / G;  // slot groups at most
+    constexpr int IT = (kRouterMaxTopK + 1 + G - 1) / G;  // slot groups at most
     constexpr bool Q4 = QT == Q3X_HIP_MATRIX_Q4_0;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
 
@@ -403,18 +417,23 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
     const int GW = gridDim.x * wpb;
     const int g = lane / LPR;
     const int li = lane % LPR;
-    uint8_t* const wl = lds_dyn + top_k * xs_bytes + wave * S::WAVE_LDS;
+    const bool has_shared = shared.down != nullptr;
+    const int slots = top_k + (has_shared ? 1 : 0);
+    uint8_t* const wl = lds_dyn + slots * xs_bytes + wave * S::WAVE_LDS;
 
     const int npass = (bpr + LPR - 1) / LPR;
-    const int groups = (top_k + G - 1) / G;
+    const int groups = (slots + G - 1) / G;
     const int my_steps = gw < H ? (H - gw + GW - 1) / GW * npass : 0;
+    constexpr int kShared = -2;
     // The selected experts (uniform); an id out of range reads as zeros.
     int expert[IT * G];
 #pragma unroll
     for (int slot = 0; slot < IT * G; ++slot) {
         const int e = slot < top_k ? __builtin_amdgcn_readfirstlane(ids[slot]) : -1;
-        expert[slot] = e >= 0 && e < experts ? e : -1;
+        expert[slot] = slot == top_k && has_shared ? kShared : e >= 0 && e < experts ? e : -1;
     }
+    const size_t shared_row_bytes = static_cast<size_t>(shared.I / kBlock) * BB;
+    const int shared_bpr = shared.I / kBlock;
     // Weight segments of one step (output row i, pass) for every slot group;
     // `live` false gives zeros without touching memory.
     u32x4 pre[IT][G][J];
@@ -424,12 +443,18 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
 #pragma unroll
         for (int gg = 0; gg < G; ++gg) {
             const int e = expert[it * G + gg];
-            const bool ok = live && e >= 0;
-            const uint8_t* src = ok ? down + static_cast<size_t>(e) * expert_bytes + static_cast<size_t>(i) * row_bytes +
-                                          static_cast<size_t>(b0) * BB
-                                    : down;
+            const uint8_t* src = down;
+            int bytes = 0;
+            if (live && e >= 0) {
+                src = down + static_cast<size_t>(e) * expert_bytes + static_cast<size_t>(i) * row_bytes +
+                      static_cast<size_t>(b0) * BB;
+                bytes = nblk * BB;
+            } else if (live && e == kShared && b0 < shared_bpr) {
+                src = shared.down + static_cast<size_t>(i) * shared_row_bytes + static_cast<size_t>(b0) * BB;
+                bytes = min(LPR, shared_bpr - b0) * BB;
+            }
             const __amdgpu_buffer_rsrc_t rsrc =
-                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src), 0, ok ? nblk * BB : 0, kBufferFlags);
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src), 0, bytes, kBufferFlags);
 #pragma unroll
             for (int j = 0; j < J; ++j)
                 pre[it][gg][j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * lane + 1024 * j, 0, kNonTemporal);
@@ -440,11 +465,13 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
     // the copy and the Q4 references.
     constexpr int kHPerThread = 8;
     float hv[kHPerThread];
-    const int hn = top_k * I;
+    const int hn = slots * I;
+    // The shared slot's h holds shared.I values; the rest of its row is zero.
+    auto h_at = [&](int c) { return c >= top_k * I + shared.I ? 0.0f : h[c]; };
 #pragma unroll
     for (int k = 0; k < kHPerThread; ++k) {
         const int c = threadIdx.x + k * static_cast<int>(blockDim.x);
-        hv[k] = c < hn ? h[c] : 0.0f;
+        hv[k] = c < hn ? h_at(c) : 0.0f;
     }
 #pragma unroll
     for (int it = 0; it < IT; ++it)
@@ -458,10 +485,11 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
         const int c = threadIdx.x + k * static_cast<int>(blockDim.x);
         if (c < hn) put_h(c, hv[k]);
     }
-    for (int c = threadIdx.x + kHPerThread * static_cast<int>(blockDim.x); c < hn; c += blockDim.x) put_h(c, h[c]);
+    for (int c = threadIdx.x + kHPerThread * static_cast<int>(blockDim.x); c < hn; c += blockDim.x)
+        put_h(c, h_at(c));
     __syncthreads();
     if (Q4) {
-        for (int c = threadIdx.x; c < top_k * bpr; c += blockDim.x) {
+        for (int c = threadIdx.x; c < slots * bpr; c += blockDim.x) {
             const int slot = c / bpr, b = c - slot * bpr;
             uint8_t* xs = lds_dyn + slot * xs_bytes;
             reinterpret_cast<float*>(xs + ref_off)[b] =
@@ -470,6 +498,7 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
         __syncthreads();
     }
 
+    const float shared_weight = has_shared ? sigmoid_ref(*shared.logit) : 0.0f;
     float acc[IT];
     int ci = gw, cp = 0;  // current step: output row, pass
     for (int s = 0; s < my_steps; ++s) {
@@ -488,7 +517,7 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
             if (it >= groups) break;
             // x of this lane's slot, block col.
             const int my_slot = it * G + g;
-            const uint8_t* xs = lds_dyn + (my_slot < top_k ? my_slot : 0) * xs_bytes;
+            const uint8_t* xs = lds_dyn + (my_slot < slots ? my_slot : 0) * xs_bytes;
             float xv[32];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
@@ -503,7 +532,7 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
                     *reinterpret_cast<u32x4*>(wl + gg * S::SEGP + 1024 * j + 16 * lane) = pre[it][gg][j];
             issue(ni, np, it, more);  // the next step's segments of this slot group
             wave_lds_sync();
-            if (li < nblk && my_slot < top_k) {
+            if (li < nblk && my_slot < slots) {
                 const uint32_t p = g * S::SEGP + li * BB;
                 acc[it] += Q4 ? block_dot_q4_mix(wl, p, xv, xref) : block_dot_q8(wl, p, xv);
             }
@@ -521,6 +550,7 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
                     const int slot = it * G + gg;
                     const float d = read_lane_f32(total, gg * LPR);
                     if (slot < top_k && expert[slot] >= 0) out = fmaf(weights[slot], d, out);
+                    if (expert[slot] == kShared) out = fmaf(shared_weight, d, out);
                 }
             }
             if (lane == 0) Y[ci] = accumulate ? Y[ci] + out : out;
@@ -532,11 +562,13 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
 
 template <uint32_t QT, int LPR>
 int launch_moe_down(const uint8_t* down, int experts, int H, int I, const int* ids, const float* weights,
-                    int top_k, const float* h, float* Y, int accumulate, hipStream_t stream) {
+                    int top_k, const float* h, float* Y, int accumulate, const SharedExpert& shared,
+                    hipStream_t stream) {
     using S = PipeShape<QT, LPR>;
     constexpr int kWaves = 8;
     const size_t row_bytes = static_cast<size_t>(I / kBlock) * (QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes);
-    const size_t lds = static_cast<size_t>(top_k) * pipe_x_bytes(QT, I / kBlock) + kWaves * S::WAVE_LDS;
+    const int slots = top_k + (shared.down ? 1 : 0);
+    const size_t lds = static_cast<size_t>(slots) * pipe_x_bytes(QT, I / kBlock) + kWaves * S::WAVE_LDS;
     if (lds > kLdsPerCU) return Q3X_HIP_ENOTSUP;
     auto kernel = moe_down_combine_kernel<QT, LPR>;
     static const bool lds_ready =
@@ -545,34 +577,41 @@ int launch_moe_down(const uint8_t* down, int experts, int H, int I, const int* i
     if (lds > 64 * 1024 && !lds_ready) return Q3X_HIP_ERUNTIME;
     const int grid = std::min((H + kWaves - 1) / kWaves, kCUs * 2);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWaves * kWave), lds, stream, down, row_bytes * H, row_bytes,
-                       experts, ids, weights, top_k, h, I, H, Y, accumulate);
+                       experts, ids, weights, top_k, h, I, H, Y, accumulate, shared);
     return launch_status();
 }
 
 template <uint32_t QT>
 int moe_decode(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
                const int* ids, const float* weights, int top_k, float* Y, int accumulate,
-               uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
+               uint8_t* ws, const MoeLayout& L, const SharedExpert& shared, hipStream_t stream) {
     constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
-    float* h = reinterpret_cast<float*>(ws + L.gu);  // [top_k, I]
+    float* h = reinterpret_cast<float*>(ws + L.gu);  // [top_k (+1), I]
     const size_t gu_row = static_cast<size_t>(H / kBlock) * BB;
     const size_t down_row = static_cast<size_t>(I / kBlock) * BB;
+    const size_t shared_down_row = static_cast<size_t>(shared.I / kBlock) * BB;
+    const bool shared_ok = !shared.down || (aligned(shared.gate, 16) && aligned(shared.up, 16) &&
+                                            aligned(shared.down, 16) && shared_down_row % 16 == 0);
     const bool staged = aligned(gate_up, 16) && aligned(X, 16) && gu_row % 16 == 0 && aligned(down, 16) &&
-                        down_row % 16 == 0;
+                        down_row % 16 == 0 && shared_ok;
     if (staged) {
+        const int slots = top_k + (shared.down ? 1 : 0);
         ExpertGateUpRows gate{};
-        static_cast<ExpertRows&>(gate) = ExpertRows{gate_up, gu_row * 2 * I, gu_row, 2 * I, experts, ids, top_k, X, h, {}};
+        static_cast<ExpertRows&>(gate) = ExpertRows{gate_up, gu_row * 2 * I, gu_row, 2 * I, experts, ids, slots, X, h, {}};
         gate.I = I;
+        gate.shared_gate = shared.down ? shared.gate : nullptr;
+        gate.shared_up = shared.up;
+        gate.shared_I = shared.I;
         // One 64-lane row group, two row iterations (gate, up) per step.
-        int status = launch_pipe<QT, 64, 2>(gate, top_k * 2 * I, H / kBlock, 16, stream, 2);
+        int status = launch_pipe<QT, 64, 2>(gate, slots * 2 * I, H / kBlock, 16, stream, 2);
         if (status == Q3X_HIP_OK) {
             const int bpr = I / kBlock;
             status = bpr <= 16   ? launch_moe_down<QT, 16>(down, experts, H, I, ids, weights, top_k, h, Y,
-                                                           accumulate, stream)
+                                                           accumulate, shared, stream)
                      : bpr <= 32 ? launch_moe_down<QT, 32>(down, experts, H, I, ids, weights, top_k, h, Y,
-                                                           accumulate, stream)
+                                                           accumulate, shared, stream)
                                  : launch_moe_down<QT, 64>(down, experts, H, I, ids, weights, top_k, h, Y,
-                                                           accumulate, stream);
+                                                           accumulate, shared, stream);
         }
         if (status != Q3X_HIP_ENOTSUP) return status;
     }
@@ -655,15 +694,149 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
     return launch_status();
 }
 
-}  // namespace q3x
+// ------------------------------------------------------------ MoE layer ----
+//
+// q3x_hip_moe_layer: the whole MoE layer of engine.cpp:406-430 (CUDA moe(),
+// engine.cu:1709-1736): BF16 router matvec, top_k, routed experts, shared
+// expert scaled by sigmoid(shared_scale . x) and added after the routed sum.
 
-using namespace q3x;
+// logits[r] = router[r] . x for r < experts and *gate_logit = gate_row . x
+// (engine.cpp:408, 427, the BF16 branch of mv :200-212): one wave per row,
+// eight BF16 values per lane per step, fixed-order DPP sum.  Rows and x
+// 16-byte aligned, H % 8 == 0.
+__global__ __launch_bounds__(256) void router_gemv_bf16_kernel(const uint16_t* __restrict__ router,
+                                                               const uint16_t* __restrict__ gate_row, int experts,
+                                                               int H, const float* __restrict__ x,
+                                                               float* __restrict__ logits,
+                                                               float* __restrict__ gate_logit) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int r = blockIdx.x * 4 + threadIdx.x / kWave;
+    if (r > experts) return;  // whole waves leave together
+    const uint16_t* row = r < experts ? router + static_cast<size_t>(r) * H : gate_row;
+    float acc = 0.0f;
+    for (int c = 8 * lane; c < H; c += 8 * kWave) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(row + c);
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(x + c);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(x + c + 4);
+        acc = fmaf(__uint_as_float(w.x << 16), x0.x, acc);
+        acc = fmaf(__uint_as_float(w.x & 0xffff0000u), x0.y, acc);
+        acc = fmaf(__uint_as_float(w.y << 16), x0.z, acc);
+        acc = fmaf(__uint_as_float(w.y & 0xffff0000u), x0.w, acc);
+        acc = fmaf(__uint_as_float(w.z << 16), x1.x, acc);
+        acc = fmaf(__uint_as_float(w.z & 0xffff0000u), x1.y, acc);
+        acc = fmaf(__uint_as_float(w.w << 16), x1.z, acc);
+        acc = fmaf(__uint_as_float(w.w & 0xffff0000u), x1.w, acc);
+    }
+    const float total = group_sum<kWave>(acc);
+    if (lane == 0) {
+        if (r < experts) logits[r] = total;
+        else *gate_logit = total;
+    }
+}
 
-extern "C" int q3x_hip_router_topk(const float* logits, int tokens, int experts, int top_k, int* ids,
-                                   float* weights, hipStream_t stream) {
-    if (!logits || !ids || !weights || tokens <= 0 || experts <= 0 || experts > kRouterMaxExperts ||
-        top_k <= 0 || top_k > experts || top_k > kRouterMaxTopK)
-        return Q3X_HIP_EINVAL;
+// Dense GEMM policies over the tokens X[count, cols] (1-D grid, tiles of BM
+// tokens); each adds its weight rows and its store.
+struct TokenTiles {
+    static constexpr bool kLinearGrid = true;
+    static constexpr bool kPairedColumns = false;
+    static constexpr bool kPartialTiles = false;
+    int tiles_x;
+    const float* X;
+    int cols;
+    int count;
+    __device__ bool tile(int ty, int bm, GemmTile& t) const {
+        t.m0 = ty * bm;
+        t.mcount = min(bm, count - t.m0);
+        t.group = 0;
+        return t.mcount > 0;
+    }
+    __device__ const float* a_row(const GemmTile& t, int m) const {
+        return X + static_cast<size_t>(t.m0 + m) * cols;
+    }
+    __device__ void store_pair(const GemmTile&, int, int, float, float) const {}
+};
+
+// The router and the shared-expert gate of every token in one BF16 GEMM over
+// experts + 1 rows: logits[t, e] for e < experts, gate_logit[t] for the last.
+struct RouterGemm : TokenTiles {
+    const uint8_t* router;
+    const uint8_t* gate_row;
+    size_t row_bytes;
+    int experts;
+    float* logits;
+    float* gate_logit;
+    __device__ const uint8_t* b_row(const GemmTile&, int n) const {
+        return n < experts ? router + static_cast<size_t>(n) * row_bytes : gate_row;
+    }
+    __device__ void store(const GemmTile& t, int m, int n, float v) const {
+        const int token = t.m0 + m;
+        if (n < experts) logits[static_cast<size_t>(token) * experts + n] = v;
+        else gate_logit[token] = v;
+    }
+};
+
+// out[t * out_stride + col0 + n] = W[n] . x_t.
+struct StridedGemm : TokenTiles {
+    const uint8_t* w;
+    size_t row_bytes;
+    float* out;
+    int out_stride;
+    int col0;
+    __device__ const uint8_t* b_row(const GemmTile&, int n) const { return w + static_cast<size_t>(n) * row_bytes; }
+    __device__ void store(const GemmTile& t, int m, int n, float v) const {
+        out[static_cast<size_t>(t.m0 + m) * out_stride + col0 + n] = v;
+    }
+};
+
+// The shared expert's gate and up GEMMs with SwiGLU in the epilogue, paired
+// as in GroupedGateUp: h[t, j] = silu(gate_j . x_t) * (up_j . x_t)
+// (engine.cpp:422-425).  Launched over 2I rows; I % 64 == 0.
+struct PairedGateUpGemm : TokenTiles {
+    static constexpr bool kPairedColumns = true;
+    const uint8_t* gate;
+    const uint8_t* up;
+    size_t row_bytes;
+    int I;
+    float* h;
+    __device__ const uint8_t* b_row(const GemmTile&, int n) const {
+        const int j = GroupedGateUp::out_col(n);
+        return ((n & 16) ? up : gate) + static_cast<size_t>(j) * row_bytes;
+    }
+    __device__ void store(const GemmTile&, int, int, float) const {}
+    __device__ void store_pair(const GemmTile& t, int m, int n, float g, float u) const {
+        h[static_cast<size_t>(t.m0 + m) * I + GroupedGateUp::out_col(n)] = silu_ref(g) * u;
+    }
+};
+
+// The shared expert's down GEMM added to the routed output (engine.cpp:
+// 426-429): Y[t, n] = fma(sigmoid(gate_logit[t]), shared_down[n] . h_t, Y[t, n]).
+struct SharedDownAdd : TokenTiles {
+    const uint8_t* w;
+    size_t row_bytes;
+    float* Y;
+    int H;
+    const float* gate_logit;
+    __device__ const uint8_t* b_row(const GemmTile&, int n) const { return w + static_cast<size_t>(n) * row_bytes; }
+    __device__ void store(const GemmTile& t, int m, int n, float v) const {
+        const int token = t.m0 + m;
+        float* p = Y + static_cast<size_t>(token) * H + n;
+        *p = fmaf(sigmoid_ref(gate_logit[token]), v, *p);
+    }
+};
+
+template <uint32_t QT, int WM, int WN, int TM, int TN, class P>
+int launch_token_gemm(P pol, int rows, hipStream_t stream) {
+    constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
+    pol.tiles_x = (rows + BN - 1) / BN;
+    const long long tiles = static_cast<long long>(pol.tiles_x) * ((pol.count + BM - 1) / BM);
+    if (tiles > 0x7fffffffLL) return Q3X_HIP_EINVAL;
+    hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, WN, TM, TN, P>), dim3(static_cast<unsigned>(tiles)),
+                       dim3(WM * WN * kWave), 0, stream, pol, rows, pol.cols);
+    return launch_status();
+}
+
+inline int launch_router_topk(const float* logits, int tokens, int experts, int top_k, int* ids, float* weights,
+                              hipStream_t stream) {
     const dim3 grid((tokens + 3) / 4), block(256);
     if (experts <= 4 * kWave)
         hipLaunchKernelGGL(router_topk_kernel<4>, grid, block, 0, stream, logits, tokens, experts, top_k, ids, weights);
@@ -673,6 +846,114 @@ extern "C" int q3x_hip_router_topk(const float* logits, int tokens, int experts,
         hipLaunchKernelGGL(router_topk_kernel<16>, grid, block, 0, stream, logits, tokens, experts, top_k, ids,
                            weights);
     return launch_status();
+}
+
+struct MoeLayerLayout {
+    size_t logits, gate, ids, weights, gu_s, h_s, routed, total;
+    MoeLayout R;
+};
+
+inline MoeLayerLayout moe_layer_layout(int tokens, int experts, int top_k, int H, int I, int shared_I) {
+    MoeLayerLayout L{};
+    const size_t T = static_cast<size_t>(tokens);
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t at = off; off = align_up(off + bytes, 256); return at; };
+    L.logits = take(sizeof(float) * T * experts);
+    L.gate = take(sizeof(float) * T);
+    L.ids = take(sizeof(int) * T * top_k);
+    L.weights = take(sizeof(float) * T * top_k);
+    L.gu_s = take(sizeof(float) * T * 2 * shared_I);
+    L.h_s = take(sizeof(float) * T * shared_I);
+    L.R = moe_layout(tokens, experts, top_k, H, I);
+    L.routed = take(L.R.total);
+    L.total = off;
+    return L;
+}
+
+template <uint32_t QT>
+int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens, float* Y, int* ids,
+                  float* weights, uint8_t* ws, const MoeLayerLayout& L, hipStream_t stream) {
+    constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
+    const int E = w.experts, H = w.H, I = w.I, SI = w.shared_I, K = w.top_k;
+    float* logits = reinterpret_cast<float*>(ws + L.logits);
+    float* gate = reinterpret_cast<float*>(ws + L.gate);
+    int* sel = ids ? ids : reinterpret_cast<int*>(ws + L.ids);
+    float* wts = weights ? weights : reinterpret_cast<float*>(ws + L.weights);
+    uint8_t* rws = ws + L.routed;
+    const auto* router = static_cast<const uint8_t*>(w.router);
+    const auto* gate_row = static_cast<const uint8_t*>(w.shared_scale);
+    const auto* gate_up = static_cast<const uint8_t*>(w.gate_up);
+    const auto* down = static_cast<const uint8_t*>(w.down);
+    const auto* sg = static_cast<const uint8_t*>(w.shared_gate);
+    const auto* su = static_cast<const uint8_t*>(w.shared_up);
+    const auto* sd = static_cast<const uint8_t*>(w.shared_down);
+    int status;
+
+    // Router logits and the shared expert's gate logit.
+    if (tokens == 1) {
+        hipLaunchKernelGGL(router_gemv_bf16_kernel, dim3((E + 1 + 3) / 4), dim3(256), 0, stream,
+                           reinterpret_cast<const uint16_t*>(router), reinterpret_cast<const uint16_t*>(gate_row),
+                           E, H, X, logits, gate);
+        status = launch_status();
+    } else {
+        RouterGemm g{};
+        g.X = X; g.cols = H; g.count = tokens;
+        g.router = router; g.gate_row = gate_row; g.row_bytes = static_cast<size_t>(H) * 2; g.experts = E;
+        g.logits = logits; g.gate_logit = gate;
+        status = launch_token_gemm<Q3X_HIP_MATRIX_BF16, 2, 4, 1, 1>(g, E + 1, stream);
+    }
+    if (status != Q3X_HIP_OK) return status;
+    if ((status = launch_router_topk(logits, tokens, E, K, sel, wts, stream)) != Q3X_HIP_OK) return status;
+
+    // Decode: routed and shared experts in two launches.
+    if (tokens == 1) {
+        const SharedExpert shared{sg, su, sd, SI, gate};
+        status = moe_decode<QT>(gate_up, down, E, H, I, X, sel, wts, K, Y, 0, rws, L.R, shared, stream);
+        if (status != Q3X_HIP_ENOTSUP) return status;
+    }
+    // Prefill (or an unaligned decode): the grouped routed experts write Y,
+    // then the shared expert's GEMMs add to it.
+    status = moe_grouped<QT>(gate_up, down, E, H, I, X, tokens, sel, wts, K, Y, 0, rws, L.R, stream);
+    if (status != Q3X_HIP_OK) return status;
+    const size_t gu_row = static_cast<size_t>(H / kBlock) * BB;
+    const size_t sd_row = static_cast<size_t>(SI / kBlock) * BB;
+    float* h_s = reinterpret_cast<float*>(ws + L.h_s);
+    if (SI % 64 == 0) {
+        PairedGateUpGemm g{};
+        g.X = X; g.cols = H; g.count = tokens;
+        g.gate = sg; g.up = su; g.row_bytes = gu_row; g.I = SI; g.h = h_s;
+        status = launch_token_gemm<QT, 2, 4, 1, 1>(g, 2 * SI, stream);
+        if (status != Q3X_HIP_OK) return status;
+    } else {
+        float* gu_s = reinterpret_cast<float*>(ws + L.gu_s);
+        StridedGemm g{};
+        g.X = X; g.cols = H; g.count = tokens;
+        g.row_bytes = gu_row; g.out = gu_s; g.out_stride = 2 * SI;
+        g.w = sg; g.col0 = 0;
+        if ((status = launch_token_gemm<QT, 2, 4, 1, 1>(g, SI, stream)) != Q3X_HIP_OK) return status;
+        g.w = su; g.col0 = SI;
+        if ((status = launch_token_gemm<QT, 2, 4, 1, 1>(g, SI, stream)) != Q3X_HIP_OK) return status;
+        const size_t n = static_cast<size_t>(tokens) * SI;
+        hipLaunchKernelGGL(swiglu_kernel, dim3(static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 65536))),
+                           dim3(256), 0, stream, gu_s, h_s, SI, tokens, nullptr);
+        if ((status = launch_status()) != Q3X_HIP_OK) return status;
+    }
+    SharedDownAdd g{};
+    g.X = h_s; g.cols = SI; g.count = tokens;
+    g.w = sd; g.row_bytes = sd_row; g.Y = Y; g.H = H; g.gate_logit = gate;
+    return launch_token_gemm<QT, 2, 4, 1, 1>(g, H, stream);
+}
+
+}  // namespace q3x
+
+using namespace q3x;
+
+extern "C" int q3x_hip_router_topk(const float* logits, int tokens, int experts, int top_k, int* ids,
+                                   float* weights, hipStream_t stream) {
+    if (!logits || !ids || !weights || tokens <= 0 || experts <= 0 || experts > kRouterMaxExperts ||
+        top_k <= 0 || top_k > experts || top_k > kRouterMaxTopK)
+        return Q3X_HIP_EINVAL;
+    return launch_router_topk(logits, tokens, experts, top_k, ids, weights, stream);
 }
 
 static bool moe_shape_ok(uint32_t type, int experts, int H, int I, int tokens, int top_k) {
@@ -710,9 +991,9 @@ extern "C" int q3x_hip_moe_routed(const void* gate_up, const void* down, uint32_
     if (tokens == 1) {
         const int status = type == Q3X_HIP_MATRIX_Q8_0
                                ? moe_decode<Q3X_HIP_MATRIX_Q8_0>(gu, dn, experts, H, I, X, ids, weights, top_k, Y,
-                                                                 accumulate, ws, L, stream)
+                                                                 accumulate, ws, L, SharedExpert{}, stream)
                                : moe_decode<Q3X_HIP_MATRIX_Q4_0>(gu, dn, experts, H, I, X, ids, weights, top_k, Y,
-                                                                 accumulate, ws, L, stream);
+                                                                 accumulate, ws, L, SharedExpert{}, stream);
         if (status != Q3X_HIP_ENOTSUP) return status;
     }
     return type == Q3X_HIP_MATRIX_Q8_0
@@ -720,4 +1001,41 @@ extern "C" int q3x_hip_moe_routed(const void* gate_up, const void* down, uint32_
                                                   accumulate, ws, L, stream)
                : moe_grouped<Q3X_HIP_MATRIX_Q4_0>(gu, dn, experts, H, I, X, tokens, ids, weights, top_k, Y,
                                                   accumulate, ws, L, stream);
+}
+
+static bool moe_layer_ok(const q3x_hip_moe_layer_weights* w, int tokens) {
+    if (!w || !w->router || !w->gate_up || !w->down || !w->shared_gate || !w->shared_up || !w->shared_down ||
+        !w->shared_scale || !is_quant_type(w->type))
+        return false;
+    if (w->shared_I <= 0 || w->shared_I > w->I || w->shared_I % kBlock != 0 || w->top_k > kRouterMaxTopK)
+        return false;
+    size_t bytes;
+    if (!quantized_size(w->type, w->shared_I, w->H, &bytes) || !quantized_size(w->type, w->H, w->shared_I, &bytes))
+        return false;
+    return moe_shape_ok(w->type, w->experts, w->H, w->I, tokens, w->top_k);
+}
+
+extern "C" size_t q3x_hip_moe_layer_workspace_bytes(const q3x_hip_moe_layer_weights* layer, int tokens) {
+    if (!layer || tokens <= 0 || layer->experts <= 0 || layer->top_k <= 0 || layer->H <= 0 || layer->I <= 0 ||
+        layer->shared_I <= 0)
+        return 0;
+    return moe_layer_layout(tokens, layer->experts, layer->top_k, layer->H, layer->I, layer->shared_I).total;
+}
+
+extern "C" int q3x_hip_moe_layer(const q3x_hip_moe_layer_weights* layer, const float* X, int tokens, float* Y,
+                                 int* ids, float* weights, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream) {
+    if (layer && layer->type == Q3X_HIP_MATRIX_BF16) return Q3X_HIP_ENOTSUP;
+    if (!X || !Y || !workspace || !moe_layer_ok(layer, tokens)) return Q3X_HIP_EINVAL;
+    const q3x_hip_moe_layer_weights& w = *layer;
+    const MoeLayerLayout L = moe_layer_layout(tokens, w.experts, w.top_k, w.H, w.I, w.shared_I);
+    if (workspace_bytes < L.total || !aligned(workspace, 256)) return Q3X_HIP_EINVAL;
+    if (!aligned(w.router, 16) || !aligned(w.shared_scale, 16) || !aligned(X, 16)) return Q3X_HIP_EINVAL;
+    if (!aligned(w.gate_up, 2) || !aligned(w.down, 2) || !aligned(w.shared_gate, 2) || !aligned(w.shared_up, 2) ||
+        !aligned(w.shared_down, 2))
+        return Q3X_HIP_EINVAL;
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    return w.type == Q3X_HIP_MATRIX_Q8_0
+               ? moe_layer_run<Q3X_HIP_MATRIX_Q8_0>(w, X, tokens, Y, ids, weights, ws, L, stream)
+               : moe_layer_run<Q3X_HIP_MATRIX_Q4_0>(w, X, tokens, Y, ids, weights, ws, L, stream);
 }

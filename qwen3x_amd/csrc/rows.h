@@ -145,7 +145,7 @@ struct MultiRows {
 // slots, engine.cu:1198, 1235).  The result of virtual row r goes to y[r].
 struct ExpertRows {
     static constexpr bool kSharedInput = true;
-    static constexpr int kMaxSlots = 8;
+    static constexpr int kMaxSlots = 9;  // top_k <= 8, plus a shared expert
     const uint8_t* pool;
     size_t expert_bytes;
     size_t row_bytes;
@@ -192,16 +192,17 @@ struct ExpertRows {
     }
 };
 
-// A wave's share of ExpertGateUpRows: the gate rows [0, I) and up rows
-// [I, 2I) of one expert's gate_up matrix, numbered so that the two row
-// iterations of a step (virtual rows v and v + GW, v = gw + 2b * GW) are gate
-// row q and up row q of the same q = gw + b * GW; the step stores
-// h[q] = silu(gate . x) * (up . x) (engine.cpp:413-416).  Pairs q >= I read
-// zeros and store nothing.
+// A wave's share of ExpertGateUpRows: the gate rows and up rows of one
+// expert (rows [0, I) and [I, 2I) of its gate_up matrix, or the shared
+// expert's two matrices), numbered so that the two row iterations of a step
+// (virtual rows v and v + GW, v = gw + 2b * GW) are gate row q and up row q of
+// the same q = gw + b * GW; the step stores h[q] = silu(gate . x) * (up . x)
+// (engine.cpp:413-416, 422-425).  Pairs q >= I read zeros and store nothing.
 struct GateUpPairs {
     static constexpr bool kSharedInput = true;
     static constexpr bool kSwiGLUPairs = true;
-    const uint8_t* w;  // null: expert id out of range (rows read as zeros)
+    const uint8_t* gate;  // null: expert id out of range (rows read as zeros)
+    const uint8_t* up;
     size_t row_bytes;
     const float* x;
     float* h;
@@ -211,28 +212,40 @@ struct GateUpPairs {
     __device__ int pair(int v) const { return v % GW + (v / GW / 2) * GW; }
     __device__ const uint8_t* row(int v) const {
         const int q = pair(v);
-        if (!w || q >= I) return nullptr;
-        return w + static_cast<size_t>((v / GW) % 2 * I + q) * row_bytes;
+        const uint8_t* base = (v / GW) % 2 ? up : gate;
+        if (!base || q >= I) return nullptr;
+        return base + static_cast<size_t>(q) * row_bytes;
     }
     __device__ const uint8_t* any() const { return any_w; }
     __device__ const float* input(int) const { return x; }
-    __device__ void store_pair(int v_gate, float gate, float up) const {
+    __device__ void store_pair(int v_gate, float gate_dot, float up_dot) const {
         const int q = pair(v_gate);
-        if (q < I) h[q] = silu_ref(gate) * up;
+        if (q < I) h[q] = silu_ref(gate_dot) * up_dot;
     }
 };
 
 // The decode step's gate_up matvec with SwiGLU applied: the experts of
 // ExpertRows (waves split evenly over the slots), each slot's result
-// h[slot * I + q] = silu(G_e[q] . x) * (U_e[q] . x).  For the pipelined
-// kernel with one row group of 64 lanes and two row iterations per step.
+// h[slot * I + q] = silu(G_e[q] . x) * (U_e[q] . x).  With shared_gate set,
+// the last slot is the shared expert (shared_gate / shared_up, shared_I <= I
+// rows).  For the pipelined kernel with one row group of 64 lanes and two row
+// iterations per step.
 struct ExpertGateUpRows : ExpertRows {
     int I;
+    const uint8_t* shared_gate;
+    const uint8_t* shared_up;
+    int shared_I;
     __device__ GateUpPairs for_wave(int& gw, int& GW, int& nrows) const {
         const int s = slot_of_wave(gw, GW);
+        const bool shared = shared_gate && s == slots - 1;
+        const int rows = shared ? shared_I : I;
         // Virtual rows: two per pair, every wave the same number of steps.
-        nrows = 2 * GW * ((I + GW - 1) / GW);
-        return GateUpPairs{expert_of_slot(s), row_bytes, x, y + static_cast<size_t>(s) * I, I, GW, pool};
+        nrows = 2 * GW * ((rows + GW - 1) / GW);
+        float* h = y + static_cast<size_t>(s) * I;
+        if (shared) return GateUpPairs{shared_gate, shared_up, row_bytes, x, h, rows, GW, pool};
+        const uint8_t* w = expert_of_slot(s);
+        const uint8_t* up = w ? w + static_cast<size_t>(I) * row_bytes : nullptr;
+        return GateUpPairs{w, up, row_bytes, x, h, rows, GW, pool};
     }
 };
 

@@ -96,6 +96,44 @@ def test_invalid_arguments_are_rejected_without_device_work():
     assert lib.q3x_hip_quantize(2, P, 4, 48, P, N) == q3x.EINVAL
 
 
+def test_moe_layer_invalid_arguments_are_rejected_without_device_work():
+    lib = q3x.lib()
+    P = 0x1000  # never dereferenced: validation fails first
+    N = None
+
+    def layer(**kw):
+        f = dict(router=P, gate_up=P, down=P, shared_gate=P, shared_up=P, shared_down=P, shared_scale=P, type=2,
+                 experts=256, top_k=8, H=2048, I=512, shared_I=512)
+        f.update(kw)
+        return q3x.MoeLayerWeights(*(f[name] for name, _ in q3x.MoeLayerWeights._fields_))
+
+    good = layer()
+    ws = lib.q3x_hip_moe_layer_workspace_bytes(ctypes.byref(good), 16)
+    assert ws > 0
+    call = lambda lw, X=P, T=16, Y=P, w=ws: lib.q3x_hip_moe_layer(ctypes.byref(lw), X, T, Y, N, N, P, w, N)  # noqa
+    assert call(good, w=ws - 1) == q3x.EINVAL                     # workspace too small
+    assert call(good, X=N) == q3x.EINVAL
+    assert call(good, Y=N) == q3x.EINVAL
+    assert call(good, T=0) == q3x.EINVAL
+    assert call(layer(shared_I=1024)) == q3x.EINVAL               # shared_I > I
+    assert call(layer(shared_I=48)) == q3x.EINVAL                 # not a multiple of 32
+    assert call(layer(top_k=9)) == q3x.EINVAL
+    assert call(layer(router=None)) == q3x.EINVAL
+    assert call(layer(shared_scale=None)) == q3x.EINVAL
+    assert call(layer(router=P + 2)) == q3x.EINVAL                # BF16 router must be 16-byte aligned
+    assert call(layer(type=0)) == q3x.ENOTSUP                     # BF16 experts: caller's own path
+    assert lib.q3x_hip_moe_layer(N, P, 16, P, N, N, P, ws, N) == q3x.EINVAL
+    assert lib.q3x_hip_moe_layer_workspace_bytes(N, 16) == 0
+    assert lib.q3x_hip_moe_layer_workspace_bytes(ctypes.byref(good), 0) == 0
+
+
+def test_moe_layer_workspace_covers_the_routed_workspace():
+    lw = q3x.MoeLayerWeights(1, 1, 1, 1, 1, 1, 1, 2, 256, 8, 2048, 512, 512)
+    for T in (1, 2048):
+        layer_ws = q3x.lib().q3x_hip_moe_layer_workspace_bytes(ctypes.byref(lw), T)
+        assert layer_ws >= q3x.moe_workspace_bytes(T, 256, 8, 2048, 512) + 4 * T * (256 + 1 + 2 * 8 + 3 * 512)
+
+
 def test_moe_workspace_sizes():
     decode = q3x.moe_workspace_bytes(1, 256, 8, 2048, 512)
     assert decode >= 4 * 8 * (2 * 512 + 512 + 2048)
