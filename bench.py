@@ -357,6 +357,31 @@ def extra_configs(torch, q3x, wl, only=None):
                                                     "router_ms": router_ms,
                                                     "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
             del logits, X, ids, wts, Y, wsb
+        # The whole MoE layer (engine.cpp:406-430): BF16 router, top-k,
+        # routed experts and the sigmoid-gated shared expert, one call.
+        layer = wl.moe_layer_weights(4)
+        E, H, I, SI = layer.experts, layer.H, layer.I, layer.shared_I
+        shared_bytes = layer.shared_gate.numel() + layer.shared_up.numel() + layer.shared_down.numel()
+        for T in (1, 2048):
+            X = wl.activations(4, T, H, salt=9)
+            Y = torch.empty((T, H), dtype=torch.float32, device="cuda")
+            wsl = torch.empty(q3x.moe_layer_workspace_bytes(layer, T), dtype=torch.uint8, device="cuda")
+            ms = time_graph(torch, lambda i: q3x.moe_layer(layer, X, T, Y, workspace=wsl), 20 if T == 1 else 1,
+                            10 if T == 1 else 5)
+            if T == 1:
+                per_expert = (moe.gate_up.numel() + moe.down.numel()) // moe.experts
+                alg = 2 * (E + 1) * H + k * per_expert + shared_bytes
+                out["cfg4_q4_moe_layer_decode"] = {
+                    "GBps": alg / (ms * 1e-3) / 1e9, "us": ms * 1e3, "bytes": alg,
+                    "note": "router GEMV (BF16 256x2048) + shared-expert gate + top-8 + 8 routed experts + "
+                            "shared expert (Q4_0 512): 4 launches"}
+            else:
+                flops = 2.0 * T * ((E + 1) * H + k * 3 * I * H + 3 * SI * H)
+                out["cfg4_q4_moe_layer_prefill_T2048"] = {
+                    "TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
+                    "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+            del X, Y, wsl
+        del layer
     return out
 
 

@@ -396,14 +396,14 @@ struct SharedExpert {
 // skipped.  With a shared expert, it is one more slot after the routed ones
 // (its h zero past shared.I), added last with weight sigmoid(*shared.logit)
 // (engine.cpp:427-429).
-template <uint32_t QT, int LPR>
+template <uint32_t QT, int LPR, int MAXS>
 __global__ __launch_bounds__(512) void moe_down_combine_kernel(
     const uint8_t* __restrict__ down, size_t expert_bytes, size_t row_bytes, int experts,
     const int* __restrict__ ids, const float* __restrict__ weights, int top_k, const float* __restrict__ h,
     int I, int H, float* __restrict__ Y, int accumulate, SharedExpert shared) {
     using S = PipeShape<QT, LPR>;
     constexpr int BB = S::BB, G = S::G, J = S::J;
-    constexpr int IT = (kRouterMaxTopK + 1 + G - 1) / G;  // slot groups at most
+    constexpr int IT = (MAXS + G - 1) / G;  // slot groups at most (MAXS: top_k, +1 with a shared expert)
     constexpr bool Q4 = QT == Q3X_HIP_MATRIX_Q4_0;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
 
@@ -417,7 +417,8 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
     const int GW = gridDim.x * wpb;
     const int g = lane / LPR;
     const int li = lane % LPR;
-    const bool has_shared = shared.down != nullptr;
+    // Only the build with a slot to spare carries the shared expert's code.
+    const bool has_shared = MAXS > kRouterMaxTopK && shared.down != nullptr;
     const int slots = top_k + (has_shared ? 1 : 0);
     uint8_t* const wl = lds_dyn + slots * xs_bytes + wave * S::WAVE_LDS;
 
@@ -570,10 +571,14 @@ int launch_moe_down(const uint8_t* down, int experts, int H, int I, const int* i
     const int slots = top_k + (shared.down ? 1 : 0);
     const size_t lds = static_cast<size_t>(slots) * pipe_x_bytes(QT, I / kBlock) + kWaves * S::WAVE_LDS;
     if (lds > kLdsPerCU) return Q3X_HIP_ENOTSUP;
-    auto kernel = moe_down_combine_kernel<QT, LPR>;
+    // Slot capacity: the routed experts alone keep the smaller register set.
+    auto kernel = shared.down ? moe_down_combine_kernel<QT, LPR, kRouterMaxTopK + 1>
+                              : moe_down_combine_kernel<QT, LPR, kRouterMaxTopK>;
     static const bool lds_ready =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(kLdsPerCU)) == hipSuccess;
+        hipFuncSetAttribute(reinterpret_cast<const void*>(moe_down_combine_kernel<QT, LPR, kRouterMaxTopK + 1>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsPerCU)) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(moe_down_combine_kernel<QT, LPR, kRouterMaxTopK>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsPerCU)) == hipSuccess;
     if (lds > 64 * 1024 && !lds_ready) return Q3X_HIP_ERUNTIME;
     const int grid = std::min((H + kWaves - 1) / kWaves, kCUs * 2);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWaves * kWave), lds, stream, down, row_bytes * H, row_bytes,

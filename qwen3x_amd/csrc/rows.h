@@ -212,7 +212,10 @@ struct GateUpPairs {
     __device__ int pair(int v) const { return v % GW + (v / GW / 2) * GW; }
     __device__ const uint8_t* row(int v) const {
         const int q = pair(v);
-        const uint8_t* base = (v / GW) % 2 ? up : gate;
+        // gate or up by arithmetic, not a select of the two members (which
+        // the compiler turns into an indexed load from a private copy).
+        const uintptr_t g = reinterpret_cast<uintptr_t>(gate), u = reinterpret_cast<uintptr_t>(up);
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(g + static_cast<uintptr_t>((v / GW) % 2) * (u - g));
         if (!base || q >= I) return nullptr;
         return base + static_cast<size_t>(q) * row_bytes;
     }

@@ -77,4 +77,40 @@ void moe_routed(const ExpertLinear& gate_up, const ExpertLinear& down, const flo
                                      output, add ? 1 : 0, workspace, workspace_bytes, stream));
 }
 
+namespace {
+
+q3x_hip_moe_layer_weights layer_of(const MoeWeights& w, int top_k) {
+    const bool ok = w.router.type == MATRIX_BF16 && w.shared_scale.type == MATRIX_BF16 &&
+                    w.gate_up.type == w.down.type && w.shared_gate.type == w.gate_up.type &&
+                    w.shared_up.type == w.gate_up.type && w.shared_down.type == w.gate_up.type &&
+                    w.router.rows == w.gate_up.experts && w.router.columns == w.gate_up.columns &&
+                    w.down.experts == w.gate_up.experts && w.down.rows == w.gate_up.columns &&
+                    w.gate_up.rows == 2 * w.down.columns && w.shared_gate.columns == w.gate_up.columns &&
+                    w.shared_up.rows == w.shared_gate.rows && w.shared_up.columns == w.gate_up.columns &&
+                    w.shared_down.rows == w.gate_up.columns && w.shared_down.columns == w.shared_gate.rows &&
+                    w.shared_scale.rows == 1 && w.shared_scale.columns == w.gate_up.columns;
+    if (!ok) {
+        std::fprintf(stderr, "moe: the layer's matrices do not match (engine.cu:97-101 shapes)\n");
+        std::abort();
+    }
+    return q3x_hip_moe_layer_weights{w.router.weight, w.gate_up.weight, w.down.weight, w.shared_gate.weight,
+                                     w.shared_up.weight, w.shared_down.weight, w.shared_scale.weight,
+                                     w.gate_up.type, w.gate_up.experts, top_k, w.gate_up.columns,
+                                     w.down.columns, w.shared_gate.rows};
+}
+
+}  // namespace
+
+size_t moe_workspace_bytes(const MoeWeights& weights, int top_k, int tokens) {
+    const q3x_hip_moe_layer_weights layer = layer_of(weights, top_k);
+    return q3x_hip_moe_layer_workspace_bytes(&layer, tokens);
+}
+
+void moe(const MoeWeights& weights, const float* input, int tokens, float* output, int top_k, int* ids,
+         float* routing_weights, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    const q3x_hip_moe_layer_weights layer = layer_of(weights, top_k);
+    Q3X_HIP_CHECK(q3x_hip_moe_layer(&layer, input, tokens, output, ids, routing_weights, workspace,
+                                    workspace_bytes, stream));
+}
+
 }  // namespace qwen3x_hip

@@ -1,7 +1,7 @@
 // hip_ops.h -- C++ host interface of the HIP backend's quantized matmul, in
 // the shape of the reference CUDA backend's host helpers so an arch/hip
 // engine can call it exactly where engine.cu calls mv / mv_add / batch_mv /
-// moe.  Every function enqueues on `stream` and, like the reference (CUDA_OK
+// moe (the routed part, or the whole layer).  Every function enqueues on `stream` and, like the reference (CUDA_OK
 // and Q3X_ASSERT, arch/cuda/engine.cu:48-56, internal.h:76-85), reports and
 // aborts on any error.  The work itself is done by the C ABI in q3x_hip.h.
 #pragma once
@@ -62,5 +62,20 @@ size_t moe_workspace_bytes(int tokens, int experts, int top_k, int H, int I);
 void moe_routed(const ExpertLinear& gate_up, const ExpertLinear& down, const float* input, int tokens,
                 const int* ids, const float* weights, int top_k, float* output, bool add, void* workspace,
                 size_t workspace_bytes, hipStream_t stream);
+
+// engine.cu:97-101: router BF16 [experts, H]; routed experts; shared expert
+// gate / up [shared_I, H], down [H, shared_I]; shared_scale BF16 [1, H].
+struct MoeWeights {
+    Linear router;
+    ExpertLinear gate_up, down;
+    Linear shared_gate, shared_up, shared_down, shared_scale;
+};
+
+// The whole MoE layer of `tokens` tokens (engine.cu:1709-1736 moe()):
+// output = routed experts + sigmoid(shared_scale x) * shared expert(x).
+// ids / weights ([tokens, top_k], device) receive the routing when not null.
+size_t moe_workspace_bytes(const MoeWeights& weights, int top_k, int tokens);
+void moe(const MoeWeights& weights, const float* input, int tokens, float* output, int top_k, int* ids,
+         float* routing_weights, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 }  // namespace qwen3x_hip

@@ -5,7 +5,7 @@
 // router_test :109-131, expert_moe_test :62-107), tests/q8_cpu_test.cpp
 // (fixed 2x64 Q8_0 vector and embed, :271-318; plus the projection helper of
 // engine.cu:1607-1619 on the same matrix) and tests/q4_cpu_test.cpp
-// (q4_math_test :138-178).  Exit 0 = pass, 77 = no GPU (the reference CI's
+// (q4_math_test :138-178, moe_test :217-276 -- the whole MoE layer).  Exit 0 = pass, 77 = no GPU (the reference CI's
 // skip code, .github/workflows/ci.yml:53-55), anything else = failure.
 #include <cmath>
 #include <cstdio>
@@ -291,6 +291,93 @@ void expert_moe_test() {
     HIP_OK(hipFree(gate)); HIP_OK(hipFree(down));
 }
 
+uint16_t bf16(float value) {  // tests/q4_cpu_test.cpp:203-208
+    uint32_t bits = 0;
+    std::memcpy(&bits, &value, sizeof(bits));
+    return static_cast<uint16_t>(bits >> 16);
+}
+
+float sigmoid(float x) {  // engine.cpp:187-190
+    if (x >= 0.0f) return 1.0f / (1.0f + std::exp(-x));
+    const float e = std::exp(x);
+    return e / (1.0f + e);
+}
+
+void fill_constant_q4(Q4Block* blocks, size_t count, uint16_t scale) {
+    for (size_t i = 0; i < count; ++i) {
+        blocks[i].scale = scale;
+        std::memset(blocks[i].values, 0x99, sizeof(blocks[i].values));
+    }
+}
+
+// tests/q4_cpu_test.cpp:217-276 (moe_test): the whole layer -- BF16 router,
+// constant 0x99 experts, shared expert and its sigmoid gate -- against the
+// closed form, through qwen3x_hip::moe (one token, then three equal tokens).
+void moe_layer_test() {
+    constexpr int EXPERTS = 4, TOP_K = 2, H = 32, I = 32;
+    std::vector<uint16_t> router(EXPERTS * H);
+    const float router_values[EXPERTS] = {-0.125f, 0.0625f, 0.125f, -0.0625f};
+    for (int e = 0; e < EXPERTS; ++e)
+        for (int c = 0; c < H; ++c) router[e * H + c] = bf16(router_values[e]);
+    std::vector<Q4Block> gate_up(EXPERTS * 2 * I), down(EXPERTS * H);
+    const uint16_t scales[EXPERTS] = {0x3400, 0x3800, 0x3c00, 0x4000};
+    for (int e = 0; e < EXPERTS; ++e) {
+        fill_constant_q4(gate_up.data() + e * 2 * I, 2 * I, scales[e]);
+        fill_constant_q4(down.data() + e * H, H, scales[e]);
+    }
+    std::vector<Q4Block> shared_gate(I), shared_up(I), shared_down(H);
+    fill_constant_q4(shared_gate.data(), I, 0x3400);
+    fill_constant_q4(shared_up.data(), I, 0x3400);
+    fill_constant_q4(shared_down.data(), H, 0x3400);
+    std::vector<uint16_t> shared_scale(H, bf16(0.03125f));
+
+    const qwen3x_hip::MatrixType q4 = qwen3x_hip::MATRIX_Q4_0, b16 = qwen3x_hip::MATRIX_BF16;
+    auto* d_router = device_copy(router.data(), router.size());
+    auto* d_gate_up = device_copy(gate_up.data(), gate_up.size());
+    auto* d_down = device_copy(down.data(), down.size());
+    auto* d_sg = device_copy(shared_gate.data(), shared_gate.size());
+    auto* d_su = device_copy(shared_up.data(), shared_up.size());
+    auto* d_sd = device_copy(shared_down.data(), shared_down.size());
+    auto* d_scale = device_copy(shared_scale.data(), shared_scale.size());
+    const qwen3x_hip::MoeWeights weights{
+        {d_router, EXPERTS, H, b16}, {d_gate_up, EXPERTS, 2 * I, H, q4}, {d_down, EXPERTS, H, I, q4},
+        {d_sg, I, H, q4},            {d_su, I, H, q4},                    {d_sd, H, I, q4},
+        {d_scale, 1, H, b16},
+    };
+
+    const float logits[EXPERTS] = {-4.0f, 2.0f, 4.0f, -2.0f};
+    const float p1 = std::exp(logits[1] - logits[2]);
+    const float expert1 = 0.5f * I * silu(0.5f * H) * (0.5f * H);
+    const float expert2 = 1.0f * I * silu(1.0f * H) * (1.0f * H);
+    const float routed = (p1 * expert1 + expert2) / (p1 + 1.0f);
+    const float shared_hidden = silu(0.25f * H) * (0.25f * H);
+    const float shared = sigmoid(1.0f) * 0.25f * I * shared_hidden;
+    const float expected = routed + shared;
+    for (int tokens : {1, 3}) {
+        std::vector<float> input(tokens * H, 1.0f);
+        auto* d_input = device_copy(input.data(), input.size());
+        float* output = device_floats(tokens * H);
+        int* ids = nullptr;
+        HIP_OK(hipMalloc(&ids, tokens * TOP_K * sizeof(int)));
+        const size_t ws_bytes = qwen3x_hip::moe_workspace_bytes(weights, TOP_K, tokens);
+        void* ws = nullptr;
+        HIP_OK(hipMalloc(&ws, ws_bytes));
+        qwen3x_hip::moe(weights, d_input, tokens, output, TOP_K, ids, nullptr, ws, ws_bytes, nullptr);
+        const auto actual = host_copy(output, tokens * H);
+        const auto chosen = host_copy(ids, tokens * TOP_K);
+        for (int t = 0; t < tokens; ++t) CHECK(chosen[t * TOP_K] == 2 && chosen[t * TOP_K + 1] == 1);
+        for (float v : actual) {
+            CHECK(std::isfinite(v));
+            CHECK(std::abs(v - expected) < 1e-2f);
+        }
+        HIP_OK(hipFree(d_input)); HIP_OK(hipFree(output)); HIP_OK(hipFree(ids)); HIP_OK(hipFree(ws));
+    }
+    for (void* p : {static_cast<void*>(d_router), static_cast<void*>(d_gate_up), static_cast<void*>(d_down),
+                    static_cast<void*>(d_sg), static_cast<void*>(d_su), static_cast<void*>(d_sd),
+                    static_cast<void*>(d_scale)})
+        HIP_OK(hipFree(p));
+}
+
 }  // namespace
 
 int main() {
@@ -304,6 +391,7 @@ int main() {
     q4_math_test();
     router_test();
     expert_moe_test();
+    moe_layer_test();
     HIP_OK(hipDeviceSynchronize());
     std::puts("q3x-hip-host-test: ok");
     return 0;

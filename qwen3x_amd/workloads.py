@@ -27,7 +27,7 @@ CONFIGS = {
     3: dict(name="q4_0_27b_ffn", type=q3x.MATRIX_Q4_0, tokens=(1, 512),
             mats=[("gate", 17408, 5120), ("up", 17408, 5120), ("down", 5120, 17408)]),
     4: dict(name="q4_0_moe_35b_a3b_routed", type=q3x.MATRIX_Q4_0, tokens=(1, 2048),
-            experts=256, H=2048, I=512, top_k=8),
+            experts=256, H=2048, I=512, top_k=8, shared_I=512),
 }
 
 
@@ -115,6 +115,27 @@ def moe_weights(index: int = 4, device="cuda") -> MoeWeights:
     gate_up = quantized_matrix(cfg["type"], E * 2 * I, H, seed + 1, device)
     down = quantized_matrix(cfg["type"], E * H, I, seed + 2, device)
     return MoeWeights(cfg["type"], E, H, I, gate_up, down)
+
+
+def bf16_matrix(rows: int, cols: int, seed: int, std: float, device="cuda"):
+    """BF16 bits (int16 tensor) of an N(0, std) FP32 matrix, truncated to BF16."""
+    return normal((rows, cols), seed, std, device).view(_torch().int16)[:, 1::2].contiguous()
+
+
+def moe_layer_weights(index: int = 4, device="cuda") -> q3x.MoeLayer:
+    """Config 4's routed experts plus the rest of the layer (engine.cpp:406-430):
+    a BF16 router with N(0, 1/H) weights (logits of N(0, 1) inputs come out
+    N(0, 1), as the routed-only benchmark feeds them), a BF16 shared-expert
+    gate and a shared expert of shared_I = 512 (the 35B-A3B configuration,
+    model_config.h) quantised like the experts."""
+    cfg = CONFIGS[index]
+    routed = moe_weights(index, device)
+    seed = (SEED_BASE + index) * 1000
+    E, H, I, SI, t = cfg["experts"], cfg["H"], cfg["I"], cfg["shared_I"], cfg["type"]
+    return q3x.MoeLayer(bf16_matrix(E, H, seed + 11, H ** -0.5, device), routed.gate_up, routed.down,
+                        quantized_matrix(t, SI, H, seed + 12, device), quantized_matrix(t, SI, H, seed + 13, device),
+                        quantized_matrix(t, H, SI, seed + 14, device), bf16_matrix(1, H, seed + 15, 0.02, device),
+                        t, E, cfg["top_k"], H, I, SI)
 
 
 def router_logits(index: int, tokens: int, experts: int, device="cuda"):

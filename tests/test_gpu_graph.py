@@ -1,6 +1,7 @@
 """HIP graph capture of the backend's launches: a decode step (projections,
 accumulating matvecs, lm_head-style matvec) and a routed-MoE decode are
-captured once and replayed several times, with eager work between replays;
+captured once and replayed several times, with eager work between replays
+(and the whole MoE layer, decode and prefill);
 every replay must equal the eager result bit for bit (the kernels are
 deterministic and record no memset nodes)."""
 import numpy as np
@@ -82,5 +83,29 @@ def test_moe_decode_graph_replays_bitwise():
     def run():
         q3x.router_top_k(logits, 1, E, k, ids, wts)
         q3x.moe_routed(gu, dn, X, 1, ids, wts, k, Y, workspace=ws)
+
+    replay_matches_eager(torch, run, [ids, wts, Y], lambda: Y.fill_(float("nan")))
+
+
+@pytest.mark.parametrize("tokens", [1, 7])
+def test_moe_layer_graph_replays_bitwise(tokens):
+    # The whole layer (router GEMV or GEMM, top-k, routed and shared experts).
+    torch = _torch()
+    rng = np.random.default_rng(7 + tokens)
+    E, H, I, SI, k = 16, 512, 256, 256, 4
+    bf16 = lambda r, c, s: dev((rng.normal(0, s, (r, c)).astype(np.float32).view(np.uint32) >> 16)  # noqa: E731
+                               .astype(np.uint16).view(np.int16))
+    layer = q3x.MoeLayer(bf16(E, H, 0.05), dev(random_blocks(rng, Q4_0, E * 2 * I, H)),
+                         dev(random_blocks(rng, Q4_0, E * H, I)), dev(random_blocks(rng, Q4_0, SI, H)),
+                         dev(random_blocks(rng, Q4_0, SI, H)), dev(random_blocks(rng, Q4_0, H, SI)),
+                         bf16(1, H, 0.05), Q4_0, E, k, H, I, SI)
+    X = dev(rng.normal(0, 1, (tokens, H)).astype(np.float32))
+    ids = torch.empty((tokens, k), dtype=torch.int32, device="cuda:0")
+    wts = torch.empty((tokens, k), dtype=torch.float32, device="cuda:0")
+    Y = torch.empty((tokens, H), dtype=torch.float32, device="cuda:0")
+    ws = torch.empty(q3x.moe_layer_workspace_bytes(layer, tokens), dtype=torch.uint8, device="cuda:0")
+
+    def run():
+        q3x.moe_layer(layer, X, tokens, Y, ids, wts, workspace=ws)
 
     replay_matches_eager(torch, run, [ids, wts, Y], lambda: Y.fill_(float("nan")))
