@@ -103,8 +103,11 @@ struct BlockPart {
 // WM x WN waves, each TM x TN tiles of 32x32.  Policy supplies the tile
 // geometry, A rows, weight rows and the output store (see dense / grouped
 // policies).  Grid: x = weight-row tiles (BN), y = A-row tiles (BM).
-template <uint32_t QT, int WM, int WN, int TM, int TN, class Policy>
+// PF: K stages whose global loads are in flight while a stage computes (1 or
+// 2; register sets a_reg / b_raw, stage s in set s % PF).
+template <uint32_t QT, int WM, int WN, int TM, int TN, class Policy, int PF = 1>
 __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, int rows, int cols) {
+    static_assert(PF == 1 || PF == 2, "one or two stages in flight");
     constexpr int NT = WM * WN * kWave;   // threads
     constexpr int BM = WM * TM * 32;
     constexpr int BN = WN * TN * 32;
@@ -161,36 +164,36 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
     }
 
     using Part = BlockPart<QT, PARTS>;
-    f32x4 a_reg[A_PER_T];
-    uint32_t b_raw[B_PASSES][1 + Part::HALVES];
-    auto load_stage = [&](int kb) {
+    f32x4 a_reg[PF][A_PER_T];
+    uint32_t b_raw[PF][B_PASSES][1 + Part::HALVES];
+    auto load_stage = [&](int kb, int r) {
 #pragma unroll
         for (int i = 0; i < A_PER_T; ++i)
-            a_reg[i] = a_src[i] ? *reinterpret_cast<const f32x4*>(a_src[i] + 32 * kb)
-                                : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            a_reg[r][i] = a_src[i] ? *reinterpret_cast<const f32x4*>(a_src[i] + 32 * kb)
+                                   : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int p = 0; p < B_PASSES; ++p) {
             if (b_src[p]) {
-                Part::load(b_src[p] + static_cast<size_t>(kb) * BB, b_part, b_raw[p]);
+                Part::load(b_src[p] + static_cast<size_t>(kb) * BB, b_part, b_raw[r][p]);
             } else {
 #pragma unroll
-                for (int e = 0; e <= Part::HALVES; ++e) b_raw[p][e] = 0u;
+                for (int e = 0; e <= Part::HALVES; ++e) b_raw[r][p][e] = 0u;
             }
         }
     };
-    auto store_stage = [&](int buf) {
+    auto store_stage = [&](int buf, int r) {
 #pragma unroll
         for (int i = 0; i < A_PER_T; ++i) {
             const int idx = tid + i * NT;
             if (idx < A_VEC)
-                *reinterpret_cast<f32x4*>(&As[buf][(idx >> 3) * kGemmLd + 4 * Part::a_chunk(idx & 7)]) = a_reg[i];
+                *reinterpret_cast<f32x4*>(&As[buf][(idx >> 3) * kGemmLd + 4 * Part::a_chunk(idx & 7)]) = a_reg[r][i];
         }
 #pragma unroll
         for (int p = 0; p < B_PASSES; ++p) {
             const int n = tid / PARTS + p * B_ROWS_PER_PASS;
             if (n < BN) {
                 float vals[PER_PART];
-                Part::dequant(b_raw[p], vals);
+                Part::dequant(b_raw[r][p], vals);
 #pragma unroll
                 for (int e = 0; e < PER_PART; e += 4) {
                     const int c = Part::column(b_part, e);
@@ -214,12 +217,12 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
     // of an expert's group) has nothing to compute: it only helps stage the
     // tiles, leaving the SIMD's matrix core to the other waves.
     const bool active = !Policy::kPartialTiles || wm * TM * 32 < tile.mcount;
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-    for (int kb = 0; kb < nblk; ++kb) {
+    // One K stage: MFMAs on LDS buffer kb & 1 while the loads of stage
+    // kb + PF are in flight; then stage kb + 1 (in registers) goes to the
+    // other buffer.
+    auto step = [&](int kb, int r_load, int r_store) {
         const int buf = kb & 1;
-        if (kb + 1 < nblk) load_stage(kb + 1);
+        if (kb + PF < nblk) load_stage(kb + PF, r_load);
         if (active) {
             f32x4 af[TM][4], bf[TN][4];
 #pragma unroll
@@ -244,8 +247,22 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
                                                                          bf[j][s >> 2][s & 3],
                                                                          acc[i][j], 0, 0, 0);
         }
-        if (kb + 1 < nblk) store_stage(buf ^ 1);
+        if (kb + 1 < nblk) store_stage(buf ^ 1, r_store);
         __syncthreads();
+    };
+    load_stage(0, 0);
+    if (PF == 2 && nblk > 1) load_stage(1, PF - 1);
+    store_stage(0, 0);
+    __syncthreads();
+    if constexpr (PF == 1) {
+        for (int kb = 0; kb < nblk; ++kb) step(kb, 0, 0);
+    } else {
+        // Stage s lives in register set s & 1: step kb loads kb + 2 into the
+        // set that held kb (already in LDS) and stores kb + 1 from the other.
+        for (int kb = 0; kb < nblk; kb += 2) {
+            step(kb, 0, 1);
+            if (kb + 1 < nblk) step(kb + 1, 1, 0);
+        }
     }
 
     // Accumulator layout of v_mfma_f32_32x32x2f32: register r of lane l holds

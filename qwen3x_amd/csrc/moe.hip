@@ -665,14 +665,14 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
                                                     tile_expert, tile_start, tile_count, ntiles, nullptr, 0};
         g1.I = I;
         g1.h = h;
-        hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGateUp>),
+        hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGateUp, 2>),
                            dim3(2 * I / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0, stream, g1, 2 * I,
                            H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
     } else {
         GroupedGemm g1{0, X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
                        ntiles, gu, 2 * I};
-        hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm>),
+        hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm, 2>),
                            dim3((2 * I + kGrpBN - 1) / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0,
                            stream, g1, 2 * I, H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
@@ -684,7 +684,7 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
     }
     GroupedGemm g2{0, h, I, nullptr, down, down_row * H, down_row, tile_expert, tile_start, tile_count,
                    ntiles, d, H};
-    hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm>),
+    hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm, 2>),
                        dim3((H + kGrpBN - 1) / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0,
                        stream, g2, H, I);
     if ((status = launch_status()) != Q3X_HIP_OK) return status;
@@ -835,7 +835,7 @@ int launch_token_gemm(P pol, int rows, hipStream_t stream) {
     pol.tiles_x = (rows + BN - 1) / BN;
     const long long tiles = static_cast<long long>(pol.tiles_x) * ((pol.count + BM - 1) / BM);
     if (tiles > 0x7fffffffLL) return Q3X_HIP_EINVAL;
-    hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, WN, TM, TN, P>), dim3(static_cast<unsigned>(tiles)),
+    hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, WN, TM, TN, P, 2>), dim3(static_cast<unsigned>(tiles)),
                        dim3(WM * WN * kWave), 0, stream, pol, rows, pol.cols);
     return launch_status();
 }
