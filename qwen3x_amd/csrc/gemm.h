@@ -32,41 +32,42 @@ struct GemmTile {
     int group;   // policy-defined (expert of a grouped tile)
 };
 
-// Raw halfwords of part `part` of PARTS of one block: raw[0] = fp16 scale,
-// raw[1..RAW_HALVES] = the part's value bytes two at a time.  Q8_0: elements
-// [part*N, part*N + N), N = 32/PARTS.  Q4_0: nibble bytes
+// Raw words of part `part` of PARTS of one block, loaded as whole dwords and
+// split only in dequant (after the stage's MFMAs, so the loads stay in
+// flight): raw[0] = fp16 scale, raw[1..WORDS] = the part's value bytes.
+// Q8_0: elements [part*N, part*N + N), N = 32/PARTS.  Q4_0: nibble bytes
 // [NB*part, NB*part + NB), NB = 16/PARTS, i.e. elements NB*part + j (low
-// nibbles) and 16 + NB*part + j (high nibbles).  `blk` is 2-byte aligned.
-// A part's N values go to the N consecutive LDS columns [part*N, part*N + N)
-// (16-byte stores without bank conflicts); for Q4_0 that permutes the k order
-// inside a block, and the activation tile is stored with the same
-// permutation (a_chunk), so the products pair up unchanged.
-// BF16 (a router matrix): a "block" is 32 consecutive BF16 values (64 B),
-// raw[1 + i] holds two of them and a value is its bits shifted up 16
-// (engine.cpp:181-185), so the conversion is exact.
+// nibbles) and 16 + NB*part + j (high nibbles).  `blk` is 2-byte aligned, so
+// the value words are read unaligned.  A part's N values go to the N
+// consecutive LDS columns [part*N, part*N + N) (16-byte stores without bank
+// conflicts); for Q4_0 that permutes the k order inside a block, and the
+// activation tile is stored with the same permutation (a_chunk), so the
+// products pair up unchanged.
+// BF16 (a router matrix): a "block" is 32 consecutive BF16 values (64 B,
+// 4-byte aligned), each word holds two of them and a value is its bits
+// shifted up 16 (engine.cpp:181-185), so the conversion is exact.
 template <uint32_t QT, int PARTS>
 struct BlockPart {
     static constexpr bool kBF16 = QT == Q3X_HIP_MATRIX_BF16;
-    static constexpr int N = 32 / PARTS;                    // elements
-    static constexpr int HALVES = QT == Q3X_HIP_MATRIX_Q4_0 ? N / 4 : N / 2;
+    static constexpr bool kQ4 = QT == Q3X_HIP_MATRIX_Q4_0;
+    static constexpr int N = 32 / PARTS;                                      // elements
+    static constexpr int WORDS = (kQ4 ? 16 : kBF16 ? 64 : 32) / PARTS / 4;   // value words
     __device__ static __forceinline__ void load(const uint8_t* blk, int part, uint32_t* raw) {
         if constexpr (kBF16) {
-            const uint32_t* w = reinterpret_cast<const uint32_t*>(blk);  // 4-byte aligned
             raw[0] = 0;
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(blk);
 #pragma unroll
-            for (int i = 0; i < HALVES; ++i) raw[1 + i] = w[HALVES * part + i];
-            return;
+            for (int i = 0; i < WORDS; ++i) raw[1 + i] = w[WORDS * part + i];
+        } else {
+            raw[0] = *reinterpret_cast<const uint16_t*>(blk);
+            __builtin_memcpy(raw + 1, blk + 2 + 4 * WORDS * part, 4 * WORDS);
         }
-        const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
-        raw[0] = h[0];
-#pragma unroll
-        for (int i = 0; i < HALVES; ++i) raw[1 + i] = h[1 + HALVES * part + i];
     }
     // out[e] for e < N, in the column order of column().
     __device__ static __forceinline__ void dequant(const uint32_t* raw, float* out) {
         if constexpr (kBF16) {
 #pragma unroll
-            for (int i = 0; i < HALVES; ++i) {
+            for (int i = 0; i < WORDS; ++i) {
                 out[2 * i + 0] = __uint_as_float(raw[1 + i] << 16);
                 out[2 * i + 1] = __uint_as_float(raw[1 + i] & 0xffff0000u);
             }
@@ -74,17 +75,16 @@ struct BlockPart {
         }
         const float d = f16_fast(raw[0]);
 #pragma unroll
-        for (int i = 0; i < HALVES; ++i) {
-            const uint32_t two = raw[1 + i];
-            if (QT == Q3X_HIP_MATRIX_Q8_0) {
-                out[2 * i + 0] = d * static_cast<float>(static_cast<int8_t>(two & 0xffu));
-                out[2 * i + 1] = d * static_cast<float>(static_cast<int8_t>(two >> 8));
-            } else {
+        for (int i = 0; i < WORDS; ++i) {
+            const uint32_t w = raw[1 + i];
 #pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    const uint32_t byte = (two >> (8 * b)) & 0xffu;
-                    out[2 * i + b] = d * static_cast<float>(static_cast<int>(byte & 15u) - 8);
-                    out[N / 2 + 2 * i + b] = d * static_cast<float>(static_cast<int>(byte >> 4) - 8);
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t byte = (w >> (8 * b)) & 0xffu;
+                if constexpr (kQ4) {
+                    out[4 * i + b] = d * static_cast<float>(static_cast<int>(byte & 15u) - 8);
+                    out[N / 2 + 4 * i + b] = d * static_cast<float>(static_cast<int>(byte >> 4) - 8);
+                } else {
+                    out[4 * i + b] = d * static_cast<float>(static_cast<int8_t>(byte));
                 }
             }
         }
@@ -100,11 +100,20 @@ struct BlockPart {
     }
 };
 
+// Policy::kMfma16 (optional, default false): each 32x32 tile is computed as
+// 2x2 blocks of 16x16 with v_mfma_f32_16x16x4_f32, so a wave skips the 16-row
+// halves that lie past the tile's valid rows (halving the padding work of
+// grouped tiles); same MFMA rate as the 32x32x2 form.
+template <class P, class = void>
+struct Mfma16 { static constexpr bool value = false; };
+template <class P>
+struct Mfma16<P, decltype(void(P::kMfma16))> { static constexpr bool value = P::kMfma16; };
+
 // WM x WN waves, each TM x TN tiles of 32x32.  Policy supplies the tile
 // geometry, A rows, weight rows and the output store (see dense / grouped
 // policies).  Grid: x = weight-row tiles (BN), y = A-row tiles (BM).
-// PF: K stages whose global loads are in flight while a stage computes (1 or
-// 2; register sets a_reg / b_raw, stage s in set s % PF).
+// PF: register sets for the stages ahead (1 or 2): while stage kb computes,
+// the loads of stages up to kb + 1 + PF are in flight.
 template <uint32_t QT, int WM, int WN, int TM, int TN, class Policy, int PF = 1>
 __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, int rows, int cols) {
     static_assert(PF == 1 || PF == 2, "one or two stages in flight");
@@ -147,39 +156,36 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
     const int wm = wave / WN, wn = wave % WN;
     const int li = lane & 31, kh = lane >> 5;
 
-    // Per-thread source pointers, fixed over K.
+    // Per-thread source pointers, fixed over K.  Every thread loads every
+    // stage, with no branch, so the compiler counts the loads in flight
+    // exactly (a load under a lane-dependent branch makes it wait for all of
+    // them): rows past the tile's valid A rows, past the matrix's weight rows
+    // or past the tile (threads with no row of their own) read a valid row
+    // instead.  An output row depends only on its own A row, a column only
+    // on its own weight row, and those outputs are never stored; the extra
+    // rows are not written to LDS either.
     const float* a_src[A_PER_T];
 #pragma unroll
     for (int i = 0; i < A_PER_T; ++i) {
-        const int idx = tid + i * NT;
-        const int m = idx >> 3;
-        a_src[i] = (idx < A_VEC && m < tile.mcount) ? pol.a_row(tile, m) + 4 * (idx & 7) : nullptr;
+        const int idx = min(tid + i * NT, A_VEC - 1);
+        a_src[i] = pol.a_row(tile, min(idx >> 3, tile.mcount - 1)) + 4 * (idx & 7);
     }
     const uint8_t* b_src[B_PASSES];
     const int b_part = tid % PARTS;
 #pragma unroll
     for (int p = 0; p < B_PASSES; ++p) {
-        const int n = tid / PARTS + p * B_ROWS_PER_PASS;
-        b_src[p] = (n < BN && n0 + n < rows) ? pol.b_row(tile, n0 + n) : nullptr;
+        const int n = min(tid / PARTS + p * B_ROWS_PER_PASS, BN - 1);
+        b_src[p] = pol.b_row(tile, min(n0 + n, rows - 1));
     }
 
     using Part = BlockPart<QT, PARTS>;
     f32x4 a_reg[PF][A_PER_T];
-    uint32_t b_raw[PF][B_PASSES][1 + Part::HALVES];
+    uint32_t b_raw[PF][B_PASSES][1 + Part::WORDS];
     auto load_stage = [&](int kb, int r) {
 #pragma unroll
-        for (int i = 0; i < A_PER_T; ++i)
-            a_reg[r][i] = a_src[i] ? *reinterpret_cast<const f32x4*>(a_src[i] + 32 * kb)
-                                   : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < A_PER_T; ++i) a_reg[r][i] = *reinterpret_cast<const f32x4*>(a_src[i] + 32 * kb);
 #pragma unroll
-        for (int p = 0; p < B_PASSES; ++p) {
-            if (b_src[p]) {
-                Part::load(b_src[p] + static_cast<size_t>(kb) * BB, b_part, b_raw[r][p]);
-            } else {
-#pragma unroll
-                for (int e = 0; e <= Part::HALVES; ++e) b_raw[r][p][e] = 0u;
-            }
-        }
+        for (int p = 0; p < B_PASSES; ++p) Part::load(b_src[p] + static_cast<size_t>(kb) * BB, b_part, b_raw[r][p]);
     };
     auto store_stage = [&](int buf, int r) {
 #pragma unroll
@@ -204,6 +210,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
         }
     };
 
+    constexpr bool M16 = Mfma16<Policy>::value;
     f32x16 acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -211,19 +218,70 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
         for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    // 16x16 form: acc16[i][mh][j][nh] is block (rows mh*16.., cols nh*16..)
+    // of tile (i, j); lane l holds rows 4*(l/16) + r, column l % 16.
+    f32x4 acc16[TM][2][TN][2];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int mh = 0; mh < 2; ++mh)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int nh = 0; nh < 2; ++nh) acc16[i][mh][j][nh] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int l16 = lane & 15, g16 = lane >> 4;
 
     const int nblk = cols / kBlock;
     // A wave whose A rows all lie past the tile's valid rows (the last tile
     // of an expert's group) has nothing to compute: it only helps stage the
     // tiles, leaving the SIMD's matrix core to the other waves.
     const bool active = !Policy::kPartialTiles || wm * TM * 32 < tile.mcount;
-    // One K stage: MFMAs on LDS buffer kb & 1 while the loads of stage
-    // kb + PF are in flight; then stage kb + 1 (in registers) goes to the
-    // other buffer.
-    auto step = [&](int kb, int r_load, int r_store) {
+    // One K stage kb: first stage kb + 1 (in registers since the previous
+    // stage) goes to the other LDS buffer, which the previous barrier freed;
+    // then the loads of stage kb + 1 + PF are issued into the register set
+    // just emptied; then the MFMAs of stage kb; then the barrier.  At the LDS
+    // store the only loads in flight are the ones it consumes (so the
+    // compiler waits for exactly those), and the new loads overlap a whole
+    // stage of MFMAs and the barrier.  Stage s lives in register set s % PF.
+    auto step = [&](int kb, int r) {
         const int buf = kb & 1;
-        if (kb + PF < nblk) load_stage(kb + PF, r_load);
-        if (active) {
+        if (kb + 1 < nblk) store_stage(buf ^ 1, r);
+        if (kb + 1 + PF < nblk) load_stage(kb + 1 + PF, r);
+        if (M16 && active) {
+            // Lane group g16 supplies k = 8 * g16 + s of MFMA step s (the same
+            // k order for both operands), i.e. 8 consecutive LDS columns.
+            f32x4 af[TM][2][2], bf[TN][2][2];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int mh = 0; mh < 2; ++mh) {
+                    const float* src = &As[buf][((wm * TM + i) * 32 + mh * 16 + l16) * kGemmLd + 8 * g16];
+                    af[i][mh][0] = *reinterpret_cast<const f32x4*>(src);
+                    af[i][mh][1] = *reinterpret_cast<const f32x4*>(src + 4);
+                }
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int nh = 0; nh < 2; ++nh) {
+                    const float* src = &Bs[buf][((wn * TN + j) * 32 + nh * 16 + l16) * kGemmLd + 8 * g16];
+                    bf[j][nh][0] = *reinterpret_cast<const f32x4*>(src);
+                    bf[j][nh][1] = *reinterpret_cast<const f32x4*>(src + 4);
+                }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int mh = 0; mh < 2; ++mh) {
+                    if (Policy::kPartialTiles && (wm * TM + i) * 32 + mh * 16 >= tile.mcount) continue;
+#pragma unroll
+                    for (int s = 0; s < 8; ++s)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j)
+#pragma unroll
+                            for (int nh = 0; nh < 2; ++nh)
+                                acc16[i][mh][j][nh] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                                    af[i][mh][s >> 2][s & 3], bf[j][nh][s >> 2][s & 3], acc16[i][mh][j][nh], 0, 0, 0);
+                }
+        } else if (active) {
             f32x4 af[TM][4], bf[TN][4];
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
@@ -247,24 +305,50 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
                                                                          bf[j][s >> 2][s & 3],
                                                                          acc[i][j], 0, 0, 0);
         }
-        if (kb + 1 < nblk) store_stage(buf ^ 1, r_store);
         __syncthreads();
     };
+    // Prologue: stage 0 into LDS buffer 0, stages 1..PF into registers.
     load_stage(0, 0);
-    if (PF == 2 && nblk > 1) load_stage(1, PF - 1);
     store_stage(0, 0);
+#pragma unroll
+    for (int q = 1; q <= PF; ++q)
+        if (q < nblk) load_stage(q, q % PF);
     __syncthreads();
     if constexpr (PF == 1) {
-        for (int kb = 0; kb < nblk; ++kb) step(kb, 0, 0);
+        for (int kb = 0; kb < nblk; ++kb) step(kb, 0);
     } else {
-        // Stage s lives in register set s & 1: step kb loads kb + 2 into the
-        // set that held kb (already in LDS) and stores kb + 1 from the other.
         for (int kb = 0; kb < nblk; kb += 2) {
-            step(kb, 0, 1);
-            if (kb + 1 < nblk) step(kb + 1, 1, 0);
+            step(kb, 1);                           // stage kb + 1 is in set 1
+            if (kb + 1 < nblk) step(kb + 1, 0);    // stage kb + 2 is in set 0
         }
     }
 
+    if constexpr (M16) {
+        // v_mfma_f32_16x16x4_f32: register r of lane l holds C[4*(l/16) + r][l%16].
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int mh = 0; mh < 2; ++mh)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int nb = n0 + (wn * TN + j) * 32 + l16;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int m = (wm * TM + i) * 32 + mh * 16 + 4 * g16 + r;
+                        if (m >= tile.mcount) continue;
+                        if constexpr (Policy::kPairedColumns) {
+                            // Column q < 16 and its partner q + 16 sit in the
+                            // same lane: blocks nh = 0 and nh = 1.
+                            if (nb < rows) pol.store_pair(tile, m, nb, acc16[i][mh][j][0][r], acc16[i][mh][j][1][r]);
+                        } else {
+#pragma unroll
+                            for (int nh = 0; nh < 2; ++nh)
+                                if (nb + 16 * nh < rows) pol.store(tile, m, nb + 16 * nh, acc16[i][mh][j][nh][r]);
+                        }
+                    }
+                }
+        return;
+    }
     // Accumulator layout of v_mfma_f32_32x32x2f32: register r of lane l holds
     // C[8*(r/4) + 4*(l/32) + r%4][l%32].
 #pragma unroll

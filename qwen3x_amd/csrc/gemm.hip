@@ -60,12 +60,12 @@ int launch_dense_gemm_tiles(const DenseGemm& base, hipStream_t stream) {
     return launch_status();
 }
 
-// Two K stages in flight (PF = 2) measured 4-5 % faster for the 8-wave
-// tiles and no faster for Q4_0's 64 x 64 tiles.
+// Register sets for the stages ahead (PF), measured per tile: two for Q8_0's
+// 64 x 128 tiles, one elsewhere (equal or faster, fewer registers).
 template <uint32_t QT>
 int launch_dense_gemm(const DenseGemm& g, hipStream_t stream) {
     const long long large = static_cast<long long>((g.rows + 127) / 128) * ((g.count + 127) / 128);
-    if (large >= 4LL * kCUs) return launch_dense_gemm_tiles<QT, 2, 4, 2, 1, 2>(g, stream);
+    if (large >= 4LL * kCUs) return launch_dense_gemm_tiles<QT, 2, 4, 2, 1, 1>(g, stream);
     if (QT == Q3X_HIP_MATRIX_Q8_0) return launch_dense_gemm_tiles<QT, 2, 4, 1, 1, 2>(g, stream);
     return launch_dense_gemm_tiles<QT, 2, 2, 1, 1, 1>(g, stream);
 }

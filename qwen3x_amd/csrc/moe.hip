@@ -33,6 +33,9 @@ constexpr int kChunk = 1024;               // pairs per grouping chunk
 // last tile but stream the weights twice as often per pair).
 constexpr int kGrpWM = 2, kGrpWN = 4, kGrpTM = 1, kGrpTN = 1;
 constexpr int kGrpBM = kGrpWM * kGrpTM * 32;
+// Register sets for the stages ahead in the 64 x 128 tile GEMMs (measured).
+template <uint32_t QT>
+constexpr int kTilePF = QT == Q3X_HIP_MATRIX_Q8_0 ? 2 : 1;
 constexpr int kGrpBN = kGrpWN * kGrpTN * 32;
 
 // ---------------------------------------------------------------- router ----
@@ -247,6 +250,7 @@ struct GroupedGemm {
     static constexpr bool kLinearGrid = false;
     static constexpr bool kPairedColumns = false;
     static constexpr bool kPartialTiles = true;  // every expert's last tile is short
+    static constexpr bool kMfma16 = true;        // skip 16-row halves past the valid pairs
     int tiles_x;  // unused (2-D grid)
     const float* A;
     int a_cols;
@@ -665,14 +669,14 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
                                                     tile_expert, tile_start, tile_count, ntiles, nullptr, 0};
         g1.I = I;
         g1.h = h;
-        hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGateUp, 2>),
+        hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGateUp, kTilePF<QT>>),
                            dim3(2 * I / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0, stream, g1, 2 * I,
                            H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
     } else {
         GroupedGemm g1{0, X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
                        ntiles, gu, 2 * I};
-        hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm, 2>),
+        hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm, kTilePF<QT>>),
                            dim3((2 * I + kGrpBN - 1) / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0,
                            stream, g1, 2 * I, H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
@@ -684,7 +688,7 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
     }
     GroupedGemm g2{0, h, I, nullptr, down, down_row * H, down_row, tile_expert, tile_start, tile_count,
                    ntiles, d, H};
-    hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm, 2>),
+    hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm, kTilePF<QT>>),
                        dim3((H + kGrpBN - 1) / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0,
                        stream, g2, H, I);
     if ((status = launch_status()) != Q3X_HIP_OK) return status;
@@ -835,7 +839,7 @@ int launch_token_gemm(P pol, int rows, hipStream_t stream) {
     pol.tiles_x = (rows + BN - 1) / BN;
     const long long tiles = static_cast<long long>(pol.tiles_x) * ((pol.count + BM - 1) / BM);
     if (tiles > 0x7fffffffLL) return Q3X_HIP_EINVAL;
-    hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, WN, TM, TN, P, 2>), dim3(static_cast<unsigned>(tiles)),
+    hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, WN, TM, TN, P, kTilePF<QT>>), dim3(static_cast<unsigned>(tiles)),
                        dim3(WM * WN * kWave), 0, stream, pol, rows, pol.cols);
     return launch_status();
 }
