@@ -175,6 +175,126 @@ int q3x_hip_moe_layer(const q3x_hip_moe_layer_weights* layer, const float* X, in
 int q3x_hip_quantize(uint32_t type, const float* src, int rows, int cols, void* dst,
                      hipStream_t stream);
 
+/* The same quantizers on BF16 src[rows, cols] (device, 16-byte aligned), the
+ * packer's own input: scripts/pack_weights.py:299-343 take little-endian
+ * BF16 rows and widen them to FP32 exactly (bits << 16) before quantizing,
+ * so dst equals q3x_hip_quantize of the widened values bit for bit. */
+int q3x_hip_quantize_bf16(uint32_t type, const uint16_t* src, int rows, int cols, void* dst,
+                          hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * model.bin -- the weight file the matmuls read (reference model_config.h,
+ * engine.cpp:455-559, arch/cuda/engine.cu:2007-2188, written by
+ * scripts/pack_weights.py).  A 72-byte header -- "Q3XMODL\0" and 16
+ * little-endian uint32 fields (model ID, V, H, I, N, AI, AH, KVH, AD, RD, KH,
+ * VH, KD, VD, CK, 262144) -- then every tensor of the model ID's fixed
+ * configuration in one fixed order, each starting at the next multiple of 64
+ * bytes, the file ending exactly where the last tensor ends.
+ * Unlike the matmul entry points above, q3x_hip_model_load reads a file and
+ * owns one device allocation until q3x_hip_model_free.
+ * ------------------------------------------------------------------------ */
+
+#define Q3X_HIP_MODEL_HEADER_BYTES 72
+
+enum {
+    Q3X_HIP_EMODEL = -4,     /* model.bin rejected; the message names why */
+    Q3X_HIP_TENSOR_F32 = 3,  /* element type of the FP32 vectors (after the matrix types) */
+};
+
+/* Tensor roles, named as the reference's Model / Layer fields
+ * (engine.cpp:31-64, 165-177). */
+enum {
+    Q3X_HIP_EMBEDDING = 0, Q3X_HIP_LM_HEAD, Q3X_HIP_FINAL_NORM,
+    Q3X_HIP_INPUT_NORM, Q3X_HIP_POST_NORM,
+    Q3X_HIP_DELTA_QKV, Q3X_HIP_DELTA_Z, Q3X_HIP_DELTA_A, Q3X_HIP_DELTA_B, Q3X_HIP_DELTA_CONV,
+    Q3X_HIP_DELTA_ALOG, Q3X_HIP_DELTA_DT, Q3X_HIP_DELTA_NORM, Q3X_HIP_DELTA_OUT,
+    Q3X_HIP_ATTN_Q, Q3X_HIP_ATTN_K, Q3X_HIP_ATTN_V, Q3X_HIP_ATTN_QNORM, Q3X_HIP_ATTN_KNORM,
+    Q3X_HIP_ATTN_OUT,
+    Q3X_HIP_FFN_GATE, Q3X_HIP_FFN_UP, Q3X_HIP_FFN_DOWN,
+    Q3X_HIP_MOE_ROUTER, Q3X_HIP_MOE_GATE_UP, Q3X_HIP_MOE_DOWN, Q3X_HIP_MOE_SHARED_GATE,
+    Q3X_HIP_MOE_SHARED_UP, Q3X_HIP_MOE_SHARED_DOWN, Q3X_HIP_MOE_SHARED_SCALE,
+    Q3X_HIP_TENSOR_ROLES
+};
+
+/* One supported model (the reference's ModelConfig, model_config.h:47-57):
+ * shapes, MoE sizes, the matrix type of its linear layers and whether
+ * lm_head shares the embedding's storage. */
+typedef struct q3x_hip_model_config {
+    uint32_t id;
+    const char* name;
+    int V, H, I, N;
+    int AI, AH, KVH, AD, RD;
+    int KH, VH, KD, VD, CK;
+    int experts, top_k, shared_I;
+    uint32_t matrix_type;
+    int tied_embeddings;
+} q3x_hip_model_config;
+
+/* One tensor of model.bin.  Matrices: [rows, cols] of `type` (an expert pool
+ * is `experts` such matrices back to back); vectors: rows 1, cols elements;
+ * the DeltaNet conv weight: rows DQKV, cols CK (BF16). */
+typedef struct q3x_hip_tensor {
+    uint32_t role;       /* Q3X_HIP_EMBEDDING ... */
+    int layer;           /* 0 .. N-1, or -1 outside the layers */
+    uint32_t type;       /* Q3X_HIP_MATRIX_BF16 / _Q8_0 / _Q4_0, or Q3X_HIP_TENSOR_F32 */
+    int experts;         /* 0, or the number of experts of a pool */
+    int rows, cols;
+    uint64_t offset;     /* from the start of the file: a multiple of 64 */
+    uint64_t bytes;
+} q3x_hip_tensor;
+
+/* Validates a model.bin from its first `header_bytes` (>= 72) bytes and its
+ * size, with the reference loader's checks and messages (engine.cpp:481-559):
+ * "bad model.bin" (shorter than the header), "wrong model.bin magic",
+ * "unsupported Qwen model ID", "Qwen model.bin header mismatch" (any of the
+ * 16 fields differs from the ID's configuration, model_config.h:115-141),
+ * "truncated model.bin" (a tensor ends past the file), "model.bin size does
+ * not match schema" (bytes left after the last tensor) -- Q3X_HIP_EMODEL with
+ * *error set.  On success *config (if not NULL) receives the configuration,
+ * *count the number of tensors and, when `tensors` is not NULL, tensors[0 ..
+ * count) the tensors in file order (capacity < count: Q3X_HIP_EINVAL).  A
+ * model with tied embeddings stores no lm_head.  Host only; reads nothing
+ * past the header. */
+int q3x_hip_model_layout(const void* header, size_t header_bytes, uint64_t file_size,
+                         q3x_hip_model_config* config, q3x_hip_tensor* tensors, size_t capacity,
+                         size_t* count, const char** error);
+
+typedef struct q3x_hip_model q3x_hip_model;
+
+/* Loads model.bin onto the current device (the CUDA loader, engine.cu:2032-
+ * 2188): opens `path` ("cannot open model.bin"), validates it as
+ * q3x_hip_model_layout before any device work, allocates one device buffer
+ * of the file's size and copies the whole file into it, so that tensor t
+ * lives at base + t.offset (64-byte aligned).  The copy overlaps file reads
+ * and host-to-device transfers through pinned staging buffers and is
+ * complete when the call returns.  Errors: Q3X_HIP_EMODEL (file rejected or
+ * unreadable), Q3X_HIP_ERUNTIME ("HIP model does not fit in device memory",
+ * "HIP model allocation failed", "HIP model upload failed"), Q3X_HIP_EINVAL;
+ * *error names the cause.  Release with q3x_hip_model_free. */
+int q3x_hip_model_load(const char* path, q3x_hip_model** model, const char** error);
+
+/* Frees the device buffer and the handle (NULL is a no-op).  Any work that
+ * reads the weights must have completed. */
+void q3x_hip_model_free(q3x_hip_model* model);
+
+/* The loaded model's configuration, tensor table (file order, owned by the
+ * handle) and device buffer (base, bytes = file size).  Outputs may be NULL. */
+int q3x_hip_model_info(const q3x_hip_model* model, q3x_hip_model_config* config,
+                       const q3x_hip_tensor** tensors, size_t* count, const void** base,
+                       uint64_t* bytes);
+
+/* Tensor `role` of `layer` (-1 for embedding, lm_head and final_norm) and its
+ * device address; a tied lm_head resolves to the embedding, as in
+ * engine.cpp:500.  Q3X_HIP_EINVAL when the model has no such tensor. */
+int q3x_hip_model_tensor(const q3x_hip_model* model, uint32_t role, int layer,
+                         q3x_hip_tensor* tensor, const void** data);
+
+/* The weights of MoE layer `layer` of a loaded MoE model, ready for
+ * q3x_hip_moe_layer (engine.cpp:543-550: router, routed pools, shared expert
+ * and its gate).  Q3X_HIP_EINVAL for a dense model or a layer out of range. */
+int q3x_hip_model_moe_layer(const q3x_hip_model* model, int layer,
+                            q3x_hip_moe_layer_weights* weights);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,7 @@ _REF_SIGS = {
     "q3xr_moe_q4": (None, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P]),
     "q3xr_mv_bf16": (None, [_P, _I, _I, _P, _P]),
     "q3xr_moe_layer": (None, [_U, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "q3xr_model_load": (_I, [ctypes.c_char_p, _P, _P, _S, ctypes.POINTER(_S), ctypes.POINTER(ctypes.c_char_p)]),
 }
 
 _lib = None
@@ -206,3 +207,19 @@ def quantize(type_: int, values: np.ndarray) -> np.ndarray:
     if not ok:
         raise ValueError("quantize: partial block or non-finite input")
     return out
+
+
+def ref_model_load(path: str, capacity: int = 4096):
+    """The reference's own loader (engine.cpp:481-559) on `path`, through the
+    reference build.  Returns (None, offsets [n], shapes [n, 4] = rows, cols,
+    experts, type with -1 for bare vectors) or (message, None, None)."""
+    offsets = np.zeros(capacity, np.uint64)
+    shapes = np.zeros((capacity, 4), np.int32)
+    count = ctypes.c_size_t(0)
+    error = ctypes.c_char_p()
+    ok = ref().q3xr_model_load(path.encode(), _p(offsets), _p(shapes), capacity, ctypes.byref(count),
+                               ctypes.byref(error))
+    if not ok:
+        return error.value.decode(), None, None
+    assert count.value <= capacity
+    return None, offsets[:count.value].copy(), shapes[:count.value].copy()

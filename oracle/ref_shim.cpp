@@ -114,4 +114,58 @@ void q3xr_moe_layer(uint32_t type, const uint16_t* router, const void* gate_up, 
     q3x_backend::moe(weights, input, work, out, config);
     for (int slot = 0; slot < top_k; ++slot) ids[slot] = work.expert_ids[slot];
 }
+// engine.cpp:481-559: the reference's own loader on the file at `path` (it
+// maps the file and reads nothing past the header).  On success returns 1 and
+// lists every tensor it bound, in file order: the offset from the start of
+// the file and (rows, cols, experts, type), with -1 for the fields a bare
+// vector pointer lacks.  On failure returns 0 with the reference's message.
+int q3xr_model_load(const char* path, uint64_t* offsets, int* shapes, size_t capacity, size_t* count,
+                    const char** error) {
+    q3x_backend::Model model;
+    const char* message = nullptr;
+    *count = 0;
+    if (!model.load(path, &message)) {
+        *error = message;
+        return 0;
+    }
+    size_t n = 0;
+    auto put = [&](const void* p, int rows, int cols, int experts, int type) {
+        if (n < capacity) {
+            offsets[n] = static_cast<uint64_t>(static_cast<const uint8_t*>(p) - model.file);
+            int* s = shapes + 4 * n;
+            s[0] = rows; s[1] = cols; s[2] = experts; s[3] = type;
+        }
+        ++n;
+    };
+    auto linear = [&](const q3x_backend::Linear& l) { put(l.w, l.rows, l.cols, 0, l.type); };
+    auto pool = [&](const q3x_backend::ExpertLinear& e) { put(e.w, e.rows, e.cols, e.experts, e.type); };
+    auto vec = [&](const void* p) { put(p, -1, -1, -1, -1); };
+    const auto& c = *model.config;
+    linear(model.embedding);
+    if (!c.tied_embeddings) linear(model.lm_head);
+    vec(model.final_norm);
+    for (int i = 0; i < c.N; ++i) {
+        const q3x_backend::Layer& l = model.layer[i];
+        vec(l.input_norm);
+        if (i % c.AI != c.AI - 1) {
+            linear(l.delta.qkv); linear(l.delta.z); linear(l.delta.a); linear(l.delta.b);
+            vec(l.delta.conv); vec(l.delta.alog); vec(l.delta.dt); vec(l.delta.norm);
+            linear(l.delta.out);
+        } else {
+            linear(l.attention.q); linear(l.attention.k); linear(l.attention.v);
+            vec(l.attention.qnorm); vec(l.attention.knorm);
+            linear(l.attention.out);
+        }
+        vec(l.post_norm);
+        if (c.experts) {
+            linear(l.moe.router); pool(l.moe.gate_up); pool(l.moe.down);
+            linear(l.moe.shared_gate); linear(l.moe.shared_up); linear(l.moe.shared_down);
+            linear(l.moe.shared_scale);
+        } else {
+            linear(l.gate); linear(l.up); linear(l.down);
+        }
+    }
+    *count = n;
+    return 1;
+}
 }  // extern "C"

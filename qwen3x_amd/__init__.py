@@ -28,6 +28,16 @@ OK = 0
 EINVAL = -1
 ERUNTIME = -2
 ENOTSUP = -3
+EMODEL = -4
+
+TENSOR_F32 = 3
+MODEL_HEADER_BYTES = 72
+# Tensor roles of model.bin, in the order of include/q3x_hip.h's enumeration.
+TENSOR_ROLES = ("embedding", "lm_head", "final_norm", "input_norm", "post_norm",
+                "delta_qkv", "delta_z", "delta_a", "delta_b", "delta_conv", "delta_alog", "delta_dt",
+                "delta_norm", "delta_out", "attn_q", "attn_k", "attn_v", "attn_qnorm", "attn_knorm", "attn_out",
+                "ffn_gate", "ffn_up", "ffn_down", "moe_router", "moe_gate_up", "moe_down", "moe_shared_gate",
+                "moe_shared_up", "moe_shared_down", "moe_shared_scale")
 
 # Every entry point of include/q3x_hip.h: name -> (restype, argtypes).
 _P = ctypes.c_void_p
@@ -47,6 +57,15 @@ SIGNATURES = {
     "q3x_hip_quantize": (_I, [_U, _P, _I, _I, _P, _P]),
     "q3x_hip_moe_layer_workspace_bytes": (_S, [_P, _I]),
     "q3x_hip_moe_layer": (_I, [_P, _P, _I, _P, _P, _P, _P, _S, _P]),
+    "q3x_hip_quantize_bf16": (_I, [_U, _P, _I, _I, _P, _P]),
+    "q3x_hip_model_layout": (_I, [_P, _S, ctypes.c_uint64, _P, _P, _S, ctypes.POINTER(_S),
+                                  ctypes.POINTER(ctypes.c_char_p)]),
+    "q3x_hip_model_load": (_I, [ctypes.c_char_p, ctypes.POINTER(_P), ctypes.POINTER(ctypes.c_char_p)]),
+    "q3x_hip_model_free": (None, [_P]),
+    "q3x_hip_model_info": (_I, [_P, _P, ctypes.POINTER(_P), ctypes.POINTER(_S), ctypes.POINTER(_P),
+                                ctypes.POINTER(ctypes.c_uint64)]),
+    "q3x_hip_model_tensor": (_I, [_P, _U, _I, _P, ctypes.POINTER(_P)]),
+    "q3x_hip_model_moe_layer": (_I, [_P, _I, _P]),
 }
 
 
@@ -60,6 +79,24 @@ class MoeLayerWeights(ctypes.Structure):
                 ("shared_down", ctypes.c_void_p), ("shared_scale", ctypes.c_void_p), ("type", ctypes.c_uint32),
                 ("experts", ctypes.c_int), ("top_k", ctypes.c_int), ("H", ctypes.c_int), ("I", ctypes.c_int),
                 ("shared_I", ctypes.c_int)]
+
+
+class ModelConfig(ctypes.Structure):
+    """struct q3x_hip_model_config of include/q3x_hip.h (model_config.h:47-57)."""
+    _fields_ = [("id", ctypes.c_uint32), ("name", ctypes.c_char_p)] + \
+        [(f, ctypes.c_int) for f in ("V", "H", "I", "N", "AI", "AH", "KVH", "AD", "RD", "KH", "VH", "KD", "VD",
+                                     "CK", "experts", "top_k", "shared_I")] + \
+        [("matrix_type", ctypes.c_uint32), ("tied_embeddings", ctypes.c_int)]
+
+
+class Tensor(ctypes.Structure):
+    """struct q3x_hip_tensor of include/q3x_hip.h: one tensor of model.bin."""
+    _fields_ = [("role", ctypes.c_uint32), ("layer", ctypes.c_int), ("type", ctypes.c_uint32),
+                ("experts", ctypes.c_int), ("rows", ctypes.c_int), ("cols", ctypes.c_int),
+                ("offset", ctypes.c_uint64), ("bytes", ctypes.c_uint64)]
+
+    def key(self):
+        return TENSOR_ROLES[self.role], self.layer
 
 
 class MvItem(ctypes.Structure):
@@ -101,6 +138,18 @@ def strerror(code: int) -> str:
 def _check(func: str, code: int) -> None:
     if code != OK:
         raise Q3xHipError(func, code, strerror(code))
+
+
+class ModelError(Q3xHipError):
+    """model.bin rejected or not loaded; ``message`` is the loader's reason."""
+    def __init__(self, func: str, code: int, message: str):
+        super().__init__(func, code, message)
+        self.message = message
+
+
+def _check_model(func: str, code: int, error: ctypes.c_char_p) -> None:
+    if code != OK:
+        raise ModelError(func, code, error.value.decode() if error.value else strerror(code))
 
 
 def quantized_bytes(type_: int, rows: int, cols: int) -> Optional[int]:
@@ -286,3 +335,122 @@ def quantize(type_: int, src, rows: int, cols: int, dst, stream=None):
     _need_device(src, dst)
     _check("q3x_hip_quantize", lib().q3x_hip_quantize(type_, _ptr(src), rows, cols, _ptr(dst), _stream(stream)))
     return dst
+
+
+def quantize_bf16(type_: int, src, rows: int, cols: int, dst, stream=None):
+    """dst = Q8_0/Q4_0 blocks of BF16 src[rows, cols] (int16/uint16/bfloat16
+    device tensor), the packer's own input type."""
+    _need_device(src, dst)
+    _check("q3x_hip_quantize_bf16",
+           lib().q3x_hip_quantize_bf16(type_, _ptr(src), rows, cols, _ptr(dst), _stream(stream)))
+    return dst
+
+
+# ---------------------------------------------------------------- model.bin
+
+def model_layout(header: bytes, file_size: int):
+    """Validate a model.bin from its header bytes and size (engine.cpp:481-559
+    checks) and return (ModelConfig, [Tensor] in file order).  Host only.
+    Raises ModelError with the reference loader's message on rejection."""
+    buf = ctypes.create_string_buffer(bytes(header), max(len(header), 1))
+    config = ModelConfig()
+    count = ctypes.c_size_t(0)
+    error = ctypes.c_char_p()
+    _check_model("q3x_hip_model_layout",
+                 lib().q3x_hip_model_layout(buf, len(header), file_size, ctypes.byref(config), None, 0,
+                                            ctypes.byref(count), ctypes.byref(error)), error)
+    tensors = (Tensor * count.value)()
+    _check_model("q3x_hip_model_layout",
+                 lib().q3x_hip_model_layout(buf, len(header), file_size, None, tensors, count.value,
+                                            ctypes.byref(count), ctypes.byref(error)), error)
+    return config, list(tensors)
+
+
+class DeviceRegion:
+    """A device address range inside a loaded model, usable wherever the
+    wrappers take a device tensor (data_ptr / is_cuda); it keeps the model
+    alive while referenced."""
+    is_cuda = True
+
+    def __init__(self, model: "Model", address: int, nbytes: int):
+        self._model = model
+        self._address = address
+        self.nbytes = nbytes
+
+    def data_ptr(self) -> int:
+        if self._model.handle is None:
+            raise RuntimeError("the model was closed")
+        return self._address
+
+    def numel(self) -> int:
+        return self.nbytes
+
+
+class Model:
+    """model.bin loaded into one device buffer of the current device (the
+    reference's CUDA Model::load, arch/cuda/engine.cu:2032-2188)."""
+
+    def __init__(self, path: str):
+        handle = ctypes.c_void_p()
+        error = ctypes.c_char_p()
+        _check_model("q3x_hip_model_load",
+                     lib().q3x_hip_model_load(os.fsencode(path), ctypes.byref(handle), ctypes.byref(error)), error)
+        self.handle = handle
+        config = ModelConfig()
+        table = ctypes.c_void_p()
+        count = ctypes.c_size_t()
+        base = ctypes.c_void_p()
+        nbytes = ctypes.c_uint64()
+        _check("q3x_hip_model_info", lib().q3x_hip_model_info(handle, ctypes.byref(config), ctypes.byref(table),
+                                                              ctypes.byref(count), ctypes.byref(base),
+                                                              ctypes.byref(nbytes)))
+        self.config = config
+        self.tensors = list(ctypes.cast(table, ctypes.POINTER(Tensor * count.value)).contents)
+        self.base = base.value
+        self.nbytes = nbytes.value
+
+    def close(self):
+        if self.handle is not None:
+            lib().q3x_hip_model_free(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensor(self, role: str, layer: int = -1):
+        """(Tensor, DeviceRegion) of `role` in `layer`; a tied lm_head is the embedding."""
+        t = Tensor()
+        data = ctypes.c_void_p()
+        _check("q3x_hip_model_tensor", lib().q3x_hip_model_tensor(self.handle, TENSOR_ROLES.index(role), layer,
+                                                                  ctypes.byref(t), ctypes.byref(data)))
+        return t, DeviceRegion(self, data.value, t.bytes)
+
+    def linear(self, role: str, layer: int = -1) -> Linear:
+        t, region = self.tensor(role, layer)
+        return Linear(region, t.rows, t.cols, t.type)
+
+    def expert_linear(self, role: str, layer: int) -> ExpertLinear:
+        t, region = self.tensor(role, layer)
+        return ExpertLinear(region, t.experts, t.rows, t.cols, t.type)
+
+    def moe_layer(self, layer: int) -> MoeLayer:
+        """The MoE weights of `layer`, ready for moe_layer()."""
+        w = MoeLayerWeights()
+        _check("q3x_hip_model_moe_layer", lib().q3x_hip_model_moe_layer(self.handle, layer, ctypes.byref(w)))
+        c = self.config
+        H, I, S, E = c.H, c.I, c.shared_I, c.experts
+        qb = quantized_bytes
+        t = c.matrix_type
+        return MoeLayer(DeviceRegion(self, w.router, E * H * 2), DeviceRegion(self, w.gate_up, E * qb(t, 2 * I, H)),
+                        DeviceRegion(self, w.down, E * qb(t, H, I)), DeviceRegion(self, w.shared_gate, qb(t, S, H)),
+                        DeviceRegion(self, w.shared_up, qb(t, S, H)), DeviceRegion(self, w.shared_down, qb(t, H, S)),
+                        DeviceRegion(self, w.shared_scale, H * 2), t, E, c.top_k, H, I, S)

@@ -62,14 +62,39 @@ __device__ __forceinline__ uint16_t f32_to_f16_rne(float value) {
     return static_cast<uint16_t>(sign | half);
 }
 
+// The 32 values of block b as FP32: FP32 input as is, BF16 input widened
+// exactly (bits << 16), as the packer widens its BF16 rows
+// (scripts/pack_weights.py:303-305).
+__device__ __forceinline__ void load_block(const float* __restrict__ src, size_t b, float (&v)[32]) {
+    const float4* s4 = reinterpret_cast<const float4*>(src + b * 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 t = s4[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+}
+__device__ __forceinline__ void load_block(const uint16_t* __restrict__ src, size_t b, float (&v)[32]) {
+    const uint4* s4 = reinterpret_cast<const uint4*>(src + b * 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint4 t = s4[i];
+        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
+            v[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        }
+    }
+}
+
 // One thread per 32-value block: scripts/pack_weights.py:299-343 on FP32
 // values.  Q8_0: d = max|v| / 127 (FP32), inverse = 1/d (0 when d == 0),
 // q = clip(copysign(floor(|v * inverse| + 0.5), v * inverse), -127, 127).
 // Q4_0: m = the first value of largest magnitude, d = m / -8, inverse as
 // above, nibble = min(15, trunc(v * inverse + 8.5)); low nibbles hold
 // elements 0..15.  Both store d as fp16.
-template <uint32_t QT>
-__global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ src, size_t blocks,
+template <uint32_t QT, typename Src>
+__global__ __launch_bounds__(256) void quantize_kernel(const Src* __restrict__ src, size_t blocks,
                                                        uint8_t* __restrict__ dst) {
     // The packer rounds every operation separately (numpy): no FMA contraction.
 #pragma clang fp contract(off)
@@ -77,12 +102,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     for (size_t b = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; b < blocks;
          b += static_cast<size_t>(gridDim.x) * blockDim.x) {
         float v[32];
-        const float4* s4 = reinterpret_cast<const float4*>(src + b * 32);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 t = s4[i];
-            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-        }
+        load_block(src, b, v);
         uint8_t* out = dst + b * BB;
         if (QT == Q3X_HIP_MATRIX_Q8_0) {
             float maximum = 0.0f;
@@ -135,6 +155,7 @@ extern "C" const char* q3x_hip_strerror(int code) {
     case Q3X_HIP_EINVAL: return "invalid argument";
     case Q3X_HIP_ERUNTIME: return "HIP runtime error";
     case Q3X_HIP_ENOTSUP: return "matrix type not handled by this backend";
+    case Q3X_HIP_EMODEL: return "model.bin rejected";
     default: return "unknown error";
     }
 }
@@ -164,8 +185,10 @@ extern "C" int q3x_hip_dequant(const void* w, uint32_t type, int cols, int row0,
     return launch_status();
 }
 
-extern "C" int q3x_hip_quantize(uint32_t type, const float* src, int rows, int cols, void* dst,
-                                hipStream_t stream) {
+namespace {
+
+template <typename Src>
+int quantize_rows(uint32_t type, const Src* src, int rows, int cols, void* dst, hipStream_t stream) {
     if (type == Q3X_HIP_MATRIX_BF16) return Q3X_HIP_ENOTSUP;
     size_t bytes;
     if (!src || !dst || !quantized_size(type, rows, cols, &bytes) || !aligned(src, 16))
@@ -174,10 +197,22 @@ extern "C" int q3x_hip_quantize(uint32_t type, const float* src, int rows, int c
     const unsigned grid = static_cast<unsigned>(std::min<size_t>((blocks + 255) / 256, 1u << 20));
     uint8_t* out = static_cast<uint8_t*>(dst);
     if (type == Q3X_HIP_MATRIX_Q8_0)
-        hipLaunchKernelGGL(quantize_kernel<Q3X_HIP_MATRIX_Q8_0>, dim3(grid), dim3(256), 0, stream, src, blocks,
-                           out);
+        hipLaunchKernelGGL((quantize_kernel<Q3X_HIP_MATRIX_Q8_0, Src>), dim3(grid), dim3(256), 0, stream, src,
+                           blocks, out);
     else
-        hipLaunchKernelGGL(quantize_kernel<Q3X_HIP_MATRIX_Q4_0>, dim3(grid), dim3(256), 0, stream, src, blocks,
-                           out);
+        hipLaunchKernelGGL((quantize_kernel<Q3X_HIP_MATRIX_Q4_0, Src>), dim3(grid), dim3(256), 0, stream, src,
+                           blocks, out);
     return launch_status();
+}
+
+}  // namespace
+
+extern "C" int q3x_hip_quantize(uint32_t type, const float* src, int rows, int cols, void* dst,
+                                hipStream_t stream) {
+    return quantize_rows(type, src, rows, cols, dst, stream);
+}
+
+extern "C" int q3x_hip_quantize_bf16(uint32_t type, const uint16_t* src, int rows, int cols, void* dst,
+                                     hipStream_t stream) {
+    return quantize_rows(type, src, rows, cols, dst, stream);
 }

@@ -1,6 +1,7 @@
 // hip_ops.cpp -- see hip_ops.h.
 #include "hip_ops.h"
 
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 
@@ -111,6 +112,79 @@ void moe(const MoeWeights& weights, const float* input, int tokens, float* outpu
     const q3x_hip_moe_layer_weights layer = layer_of(weights, top_k);
     Q3X_HIP_CHECK(q3x_hip_moe_layer(&layer, input, tokens, output, ids, routing_weights, workspace,
                                     workspace_bytes, stream));
+}
+
+Model::~Model() {
+    delete[] layers;
+    q3x_hip_model_free(handle);
+}
+
+bool Model::load(const char* path, const char** error) {
+    q3x_hip_model* loaded = nullptr;
+    const char* message = nullptr;
+    if (q3x_hip_model_load(path, &loaded, &message) != Q3X_HIP_OK) {
+        *error = message ? message : "cannot load model.bin";
+        return false;
+    }
+    const q3x_hip_tensor* table = nullptr;
+    size_t count = 0;
+    const void* base = nullptr;
+    q3x_hip_model_config c{};
+    Q3X_HIP_CHECK(q3x_hip_model_info(loaded, &c, &table, &count, &base, nullptr));
+    Layer* bound = new Layer[c.N];
+    for (size_t i = 0; i < count; ++i) {
+        const q3x_hip_tensor& t = table[i];
+        const void* p = static_cast<const uint8_t*>(base) + t.offset;
+        const Linear linear{p, t.rows, t.cols, static_cast<MatrixType>(t.type)};
+        const ExpertLinear pool{p, t.experts, t.rows, t.cols, static_cast<MatrixType>(t.type)};
+        const uint16_t* bf16 = static_cast<const uint16_t*>(p);
+        const float* f32 = static_cast<const float*>(p);
+        if (t.layer < 0) {
+            if (t.role == Q3X_HIP_EMBEDDING) embedding = linear;
+            else if (t.role == Q3X_HIP_LM_HEAD) lm_head = linear;
+            else if (t.role == Q3X_HIP_FINAL_NORM) final_norm = bf16;
+            continue;
+        }
+        Layer& l = bound[t.layer];
+        switch (t.role) {
+        case Q3X_HIP_INPUT_NORM: l.input_norm = bf16; break;
+        case Q3X_HIP_POST_NORM: l.post_norm = bf16; break;
+        case Q3X_HIP_DELTA_QKV: l.delta.qkv = linear; break;
+        case Q3X_HIP_DELTA_Z: l.delta.z = linear; break;
+        case Q3X_HIP_DELTA_A: l.delta.a = linear; break;
+        case Q3X_HIP_DELTA_B: l.delta.b = linear; break;
+        case Q3X_HIP_DELTA_CONV: l.delta.conv = bf16; break;
+        case Q3X_HIP_DELTA_ALOG: l.delta.alog = f32; break;
+        case Q3X_HIP_DELTA_DT: l.delta.dt = bf16; break;
+        case Q3X_HIP_DELTA_NORM: l.delta.norm = f32; break;
+        case Q3X_HIP_DELTA_OUT: l.delta.out = linear; break;
+        case Q3X_HIP_ATTN_Q: l.attention.q = linear; break;
+        case Q3X_HIP_ATTN_K: l.attention.k = linear; break;
+        case Q3X_HIP_ATTN_V: l.attention.v = linear; break;
+        case Q3X_HIP_ATTN_QNORM: l.attention.qnorm = bf16; break;
+        case Q3X_HIP_ATTN_KNORM: l.attention.knorm = bf16; break;
+        case Q3X_HIP_ATTN_OUT: l.attention.out = linear; break;
+        case Q3X_HIP_FFN_GATE: l.gate = linear; break;
+        case Q3X_HIP_FFN_UP: l.up = linear; break;
+        case Q3X_HIP_FFN_DOWN: l.down = linear; break;
+        case Q3X_HIP_MOE_ROUTER: l.moe.router = linear; break;
+        case Q3X_HIP_MOE_GATE_UP: l.moe.gate_up = pool; break;
+        case Q3X_HIP_MOE_DOWN: l.moe.down = pool; break;
+        case Q3X_HIP_MOE_SHARED_GATE: l.moe.shared_gate = linear; break;
+        case Q3X_HIP_MOE_SHARED_UP: l.moe.shared_up = linear; break;
+        case Q3X_HIP_MOE_SHARED_DOWN: l.moe.shared_down = linear; break;
+        case Q3X_HIP_MOE_SHARED_SCALE: l.moe.shared_scale = linear; break;
+        default: Q3X_HIP_ASSERT(false);
+        }
+    }
+    if (c.tied_embeddings) lm_head = embedding;  // engine.cpp:500
+    delete[] layers;
+    q3x_hip_model_free(handle);
+    config = c;
+    layers = bound;
+    handle = loaded;
+    *error = nullptr;
+    return true;
 }
 
 }  // namespace qwen3x_hip

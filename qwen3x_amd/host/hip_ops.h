@@ -78,4 +78,44 @@ size_t moe_workspace_bytes(const MoeWeights& weights, int top_k, int tokens);
 void moe(const MoeWeights& weights, const float* input, int tokens, float* output, int top_k, int* ids,
          float* routing_weights, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+// The rest of a layer's weights as model.bin stores them (engine.cpp:37-64):
+// DeltaNet and attention projections, norms, and the dense FFN.  BF16
+// vectors are uint16 device pointers, FP32 vectors float device pointers.
+struct DeltaWeights {
+    Linear qkv, z, a, b, out;
+    const uint16_t* conv = nullptr;  // [DQKV, CK]
+    const float* alog = nullptr;     // [VH]
+    const uint16_t* dt = nullptr;    // [VH]
+    const float* norm = nullptr;     // [VD]
+};
+struct AttentionWeights {
+    Linear q, k, v, out;
+    const uint16_t *qnorm = nullptr, *knorm = nullptr;  // [AD]
+};
+struct Layer {
+    const uint16_t *input_norm = nullptr, *post_norm = nullptr;  // [H]
+    Linear gate, up, down;  // dense models
+    MoeWeights moe;         // MoE models
+    DeltaWeights delta;     // layers with i % AI != AI - 1
+    AttentionWeights attention;
+};
+
+// model.bin on the current device (the reference's CUDA Model::load,
+// engine.cu:2032-2188): one device buffer holding the whole file, every
+// field a device pointer into it.  load() returns false with the loader's
+// message (engine.cpp:481-559 messages) and leaves the model empty.
+struct Model {
+    q3x_hip_model_config config{};
+    Linear embedding, lm_head;  // lm_head == embedding for tied models
+    const uint16_t* final_norm = nullptr;
+    Layer* layers = nullptr;    // config.N layers
+    q3x_hip_model* handle = nullptr;
+
+    Model() = default;
+    Model(const Model&) = delete;
+    Model& operator=(const Model&) = delete;
+    ~Model();
+    bool load(const char* path, const char** error);
+};
+
 }  // namespace qwen3x_hip

@@ -5,8 +5,14 @@
 // router_test :109-131, expert_moe_test :62-107), tests/q8_cpu_test.cpp
 // (fixed 2x64 Q8_0 vector and embed, :271-318; plus the projection helper of
 // engine.cu:1607-1619 on the same matrix) and tests/q4_cpu_test.cpp
-// (q4_math_test :138-178, moe_test :217-276 -- the whole MoE layer).  Exit 0 = pass, 77 = no GPU (the reference CI's
-// skip code, .github/workflows/ci.yml:53-55), anything else = failure.
+// (q4_math_test :138-178, moe_test :217-276 -- the whole MoE layer), and the
+// loader tests on sparse full-size model.bin files (q8_cpu_test.cpp:222-264,
+// q4_cpu_test.cpp:85-136) against the device loader.  Exit 0 = pass, 77 = no
+// GPU (the reference CI's skip code, .github/workflows/ci.yml:53-55), anything
+// else = failure.
+#include <fcntl.h>
+#include <unistd.h>
+
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -378,6 +384,121 @@ void moe_layer_test() {
         HIP_OK(hipFree(p));
 }
 
+// ---- model.bin loader (q8_cpu_test.cpp:222-264, q4_cpu_test.cpp:85-136) ----
+
+// The 72-byte header of a model: magic, then the 16 fields (model_config.h:
+// 22-39, values :77-93).
+std::vector<uint8_t> model_header(const uint32_t (&fields)[16]) {
+    std::vector<uint8_t> header(72, 0);
+    std::memcpy(header.data(), "Q3XMODL\0", 8);
+    std::memcpy(header.data() + 8, fields, sizeof(fields));
+    return header;
+}
+
+void pwrite_exact(int fd, const void* data, size_t size, off_t offset) {
+    CHECK(pwrite(fd, data, size, offset) == static_cast<ssize_t>(size));
+}
+
+void check_loader(const char* path, bool expected, const char* expected_error) {
+    qwen3x_hip::Model model;
+    const char* error = nullptr;
+    CHECK(model.load(path, &error) == expected);
+    if (expected) {
+        CHECK(error == nullptr);
+    } else {
+        CHECK(error != nullptr && std::strstr(error, expected_error) != nullptr);
+        CHECK(model.handle == nullptr && model.layers == nullptr);
+    }
+}
+
+void loader_test_q8_9b() {
+    const uint32_t fields[16] = {9000, 248320, 4096, 12288, 32, 4, 16, 4, 256, 64, 16, 32, 128, 128, 4, 262144};
+    const auto header = model_header(fields);
+    const size_t expected_size = 9514418816ULL;  // q8_cpu_test.cpp:228
+    char path[] = "/tmp/q3x-hip-q8-loader-XXXXXX";
+    const int fd = mkstemp(path);
+    CHECK(fd >= 0);
+    auto restore = [&]() {
+        CHECK(ftruncate(fd, static_cast<off_t>(expected_size)) == 0);
+        pwrite_exact(fd, header.data(), header.size(), 0);
+    };
+    restore();
+    {
+        qwen3x_hip::Model model;
+        const char* error = nullptr;
+        CHECK(model.load(path, &error));
+        CHECK(model.config.id == 9000 && model.config.matrix_type == Q3X_HIP_MATRIX_Q8_0);
+        CHECK(model.lm_head.weight != model.embedding.weight && model.lm_head.rows == 248320);
+        CHECK(model.layers[0].gate.rows == 12288 && model.layers[0].gate.columns == 4096);
+        CHECK(model.layers[31].down.rows == 4096 && model.layers[31].down.columns == 12288);
+        CHECK(model.layers[3].attention.q.rows == 2 * 16 * 256 && model.layers[3].attention.qnorm);
+        CHECK(model.layers[2].delta.qkv.rows == 2 * 16 * 128 + 32 * 128 && model.layers[2].delta.alog);
+        // Every weight is 64-byte aligned inside the one device buffer.
+        CHECK(reinterpret_cast<uintptr_t>(model.layers[7].delta.norm) % 64 == 0);
+    }
+    CHECK(ftruncate(fd, static_cast<off_t>(expected_size - 1)) == 0);
+    check_loader(path, false, "truncated");
+    restore();
+    CHECK(ftruncate(fd, static_cast<off_t>(expected_size + 1)) == 0);
+    check_loader(path, false, "size does not match schema");
+    restore();
+    const uint8_t wrong_magic = 'X';
+    pwrite_exact(fd, &wrong_magic, 1, 0);
+    check_loader(path, false, "wrong model.bin magic");
+    restore();
+    const uint32_t unknown_id = 9001;
+    pwrite_exact(fd, &unknown_id, 4, 8);
+    check_loader(path, false, "unsupported Qwen model ID");
+    restore();
+    const uint32_t wrong_hidden = 4095;
+    pwrite_exact(fd, &wrong_hidden, 4, 8 + 2 * 4);
+    check_loader(path, false, "header mismatch");
+    close(fd);
+    CHECK(unlink(path) == 0);
+}
+
+void loader_test_q4_35b() {
+    const uint32_t fields[16] = {36035, 248320, 2048, 512, 40, 4, 16, 2, 256, 64, 16, 32, 128, 128, 4, 262144};
+    const auto header = model_header(fields);
+    const size_t expected_size = 19528534784ULL;  // q4_cpu_test.cpp:15
+    char path[] = "/tmp/q3x-hip-q4-loader-XXXXXX";
+    const int fd = mkstemp(path);
+    CHECK(fd >= 0);
+    auto restore = [&]() {
+        CHECK(ftruncate(fd, static_cast<off_t>(expected_size)) == 0);
+        pwrite_exact(fd, header.data(), header.size(), 0);
+    };
+    restore();
+    {
+        qwen3x_hip::Model model;
+        const char* error = nullptr;
+        CHECK(model.load(path, &error));
+        CHECK(error == nullptr);
+        CHECK(model.config.id == 36035);
+        CHECK(model.layers[39].moe.gate_up.experts == 256);
+        CHECK(model.layers[39].moe.gate_up.rows == 1024 && model.layers[39].moe.down.columns == 512);
+        CHECK(model.layers[0].moe.router.type == qwen3x_hip::MATRIX_BF16 && model.layers[0].moe.router.rows == 256);
+        CHECK(model.layers[0].moe.shared_scale.rows == 1 && model.layers[0].moe.shared_down.columns == 512);
+    }
+    auto reject_header = [&](off_t offset, uint32_t value, const char* expected) {
+        restore();
+        pwrite_exact(fd, &value, sizeof(value), offset);
+        check_loader(path, false, expected);
+    };
+    reject_header(0, 0, "magic");
+    reject_header(8, 12345, "model ID");
+    reject_header(8 + 4, 1, "header mismatch");
+    restore();
+    CHECK(ftruncate(fd, static_cast<off_t>(expected_size - 1)) == 0);
+    check_loader(path, false, "truncated");
+    restore();
+    CHECK(ftruncate(fd, static_cast<off_t>(expected_size + 1)) == 0);
+    check_loader(path, false, "size does not match schema");
+    check_loader("/nonexistent/model.bin", false, "cannot open model.bin");
+    close(fd);
+    CHECK(unlink(path) == 0);
+}
+
 }  // namespace
 
 int main() {
@@ -392,6 +513,8 @@ int main() {
     router_test();
     expert_moe_test();
     moe_layer_test();
+    loader_test_q8_9b();
+    loader_test_q4_35b();
     HIP_OK(hipDeviceSynchronize());
     std::puts("q3x-hip-host-test: ok");
     return 0;

@@ -6,7 +6,7 @@ import pytest
 
 import oracle
 import qwen3x_amd as q3x
-from tests.helpers import Q4_0, Q8_0, dequant_numpy, random_blocks
+from tests.helpers import BLOCK_BYTES, Q4_0, Q8_0, dequant_numpy, random_blocks
 from tests.test_gpu_parity import TOL, _torch, dev, host, moe_bound, say
 
 pytestmark = pytest.mark.gpu
@@ -116,9 +116,23 @@ def test_moe_layer_parity(type_, E, H, I, SI, k, tokens):
     wts = torch.zeros((tokens, k), dtype=torch.float32, device="cuda:0")
     say(f"moe_layer type={type_} E={E} H={H} I={I} SI={SI} k={k} tokens={tokens}")
     q3x.moe_layer(layer, dev(X), tokens, Y, ids, wts)
-    got, ids_g, wts_g = host(Y), host(ids), host(wts)
+    check_layer(w, type_, E, H, I, SI, k, X, host(Y), host(ids), host(wts), want, ids_o, wts_o)
+
+
+def check_layer(w, type_, E, H, I, SI, k, X, got, ids_g, wts_g, want, ids_o, wts_o):
+    """GPU layer output against the oracle's: the same experts (or a swap the
+    logits' own error allows), weights within the logit error, outputs
+    within layer_bound.  The bound only needs the selected experts, so their
+    blocks are gathered first (full pools can be large)."""
+    tokens = X.shape[0]
     assert np.all(np.isfinite(got))
-    bound = layer_bound(w, type_, E, H, I, SI, X, ids_o, wts_o)
+    sel = np.unique(ids_o)
+    bb = BLOCK_BYTES[type_]
+    gsz, dsz = 2 * I * H // 32 * bb, H * I // 32 * bb
+    ws = dict(w, gate_up=np.concatenate([w["gate_up"][e * gsz:(e + 1) * gsz] for e in sel]),
+              down=np.concatenate([w["down"][e * dsz:(e + 1) * dsz] for e in sel]))
+    remap = np.searchsorted(sel, ids_o)
+    bound = layer_bound(ws, type_, len(sel), H, I, SI, X, remap, wts_o)
     checked = 0
     for t in range(tokens):
         if not np.array_equal(ids_g[t], ids_o[t]):
