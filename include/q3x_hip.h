@@ -259,6 +259,16 @@ int q3x_hip_model_layout(const void* header, size_t header_bytes, uint64_t file_
                          q3x_hip_model_config* config, q3x_hip_tensor* tensors, size_t capacity,
                          size_t* count, const char** error);
 
+/* The same layout for any configuration `config` describes (the five of
+ * model.bin included): the tensors in file order with their offsets (from a
+ * 72-byte header, each at the next multiple of 64 bytes) and, in *bytes, the
+ * size of such a file.  For weights built in memory, e.g. small synthetic
+ * models.  Q3X_HIP_EINVAL for a configuration whose sizes are not positive,
+ * whose heads do not divide evenly, whose quantized rows are not whole
+ * 32-element blocks, or whose row counts overflow an int. */
+int q3x_hip_model_schema(const q3x_hip_model_config* config, q3x_hip_tensor* tensors, size_t capacity,
+                         size_t* count, uint64_t* bytes);
+
 typedef struct q3x_hip_model q3x_hip_model;
 
 /* Loads model.bin onto the current device (the CUDA loader, engine.cu:2032-
@@ -294,6 +304,53 @@ int q3x_hip_model_tensor(const q3x_hip_model* model, uint32_t role, int layer,
  * and its gate).  Q3X_HIP_EINVAL for a dense model or a layer out of range. */
 int q3x_hip_model_moe_layer(const q3x_hip_model* model, int layer,
                             q3x_hip_moe_layer_weights* weights);
+
+/* ------------------------------------------------------------------------
+ * Decode engine: tokens through every layer of a Q8_0 / Q4_0 model on the
+ * current device -- the reference's forward (engine.cpp:431-454; CUDA
+ * forward and state_forward, arch/cuda/engine.cu:1961-2005, 2237-2307) over
+ * this library's matmul entry points, for the backend interface
+ * q3x_backend::state_* (internal.h:11-34).  The engine owns its state on the
+ * device (work vectors, DeltaNet conv history and memory, KV cache, logits)
+ * and a stream; one decode step is captured into a hipGraph on first use and
+ * replayed for every token.  Not thread-safe: one caller per engine.
+ * ------------------------------------------------------------------------ */
+
+typedef struct q3x_hip_engine q3x_hip_engine;
+
+/* An engine over `weights`, a device buffer laid out as q3x_hip_model_schema
+ * gives for `config` (the buffer of q3x_hip_model_load qualifies), with room
+ * for `context` tokens (1 .. 262144).  Needs a Q8_0 or Q4_0 model with KD,
+ * VD <= 128, AD <= 256, RD <= min(64, AD) even, 2 <= CK <= 8, top_k <= 8
+ * (BF16 models: Q3X_HIP_ENOTSUP, as the matmul entry points).  The weights
+ * must outlive the engine.  *error names the cause of a failure. */
+int q3x_hip_engine_create(const q3x_hip_model_config* config, const void* weights, int context,
+                          q3x_hip_engine** engine, const char** error);
+void q3x_hip_engine_destroy(q3x_hip_engine* engine);
+
+/* Position 0 and a zero recurrent state (state_reset, engine.cpp:158-162). */
+int q3x_hip_engine_reset(q3x_hip_engine* engine);
+
+/* tokens[0 .. count) (host) through the model at the current position, one
+ * token at a time as the reference's state_forward (engine.cpp:586-589);
+ * the logits of the last token when compute_logits.  Returns when done.
+ * Q3X_HIP_EINVAL for a token outside [0, V) or more tokens than the context
+ * has left (nothing is run). */
+int q3x_hip_engine_forward(q3x_hip_engine* engine, const int* tokens, int count, int compute_logits);
+
+/* The last computed logits [V] into host memory (state_copy_logits). */
+int q3x_hip_engine_logits(const q3x_hip_engine* engine, float* logits);
+
+/* The index of the largest logit, lowest index among equals (state_argmax). */
+int q3x_hip_engine_argmax(const q3x_hip_engine* engine, int* token);
+
+/* Save / restore position, recurrent state and logits
+ * (state_checkpoint_save / _restore, engine.cpp:590-604). */
+int q3x_hip_engine_checkpoint_save(q3x_hip_engine* engine);
+int q3x_hip_engine_checkpoint_restore(q3x_hip_engine* engine);
+
+/* Tokens processed since the last reset (-1 for NULL). */
+int q3x_hip_engine_position(const q3x_hip_engine* engine);
 
 #ifdef __cplusplus
 }

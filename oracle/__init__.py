@@ -52,6 +52,7 @@ _REF_SIGS = {
     "q3xr_mv_bf16": (None, [_P, _I, _I, _P, _P]),
     "q3xr_moe_layer": (None, [_U, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "q3xr_model_load": (_I, [ctypes.c_char_p, _P, _P, _S, ctypes.POINTER(_S), ctypes.POINTER(ctypes.c_char_p)]),
+    "q3xr_forward": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _P]),
 }
 
 _lib = None
@@ -223,3 +224,21 @@ def ref_model_load(path: str, capacity: int = 4096):
         return error.value.decode(), None, None
     assert count.value <= capacity
     return None, offsets[:count.value].copy(), shapes[:count.value].copy()
+
+
+def ref_forward(config: dict, image: np.ndarray, table, tokens) -> np.ndarray:
+    """The reference's CPU forward (engine.cpp:431-454) token by token on
+    weights `image` (uint8, model.bin layout) whose tensors `table` lists as
+    (role, layer, offset); returns logits [len(tokens), V]."""
+    keys = ("id", "V", "H", "I", "N", "AI", "AH", "KVH", "AD", "RD", "KH", "VH", "KD", "VD", "CK", "experts",
+            "top_k", "shared_I", "matrix_type", "tied_embeddings")
+    cfg = np.array([int(config[k]) for k in keys], np.int32)
+    roles = np.array([t[0] for t in table], np.int32)
+    layers = np.array([t[1] for t in table], np.int32)
+    offsets = np.array([t[2] for t in table], np.uint64)
+    tokens = np.ascontiguousarray(tokens, np.int32)
+    out = np.empty((tokens.size, int(config["V"])), np.float32)
+    image = np.ascontiguousarray(image, np.uint8)
+    assert ref().q3xr_forward(_p(cfg), _p(image), _p(roles), _p(layers), _p(offsets), len(table), _p(tokens),
+                              tokens.size, _p(out))
+    return out

@@ -168,4 +168,73 @@ int q3xr_model_load(const char* path, uint64_t* offsets, int* shapes, size_t cap
     *count = n;
     return 1;
 }
+// engine.cpp:431-454 forward, token by token, on a model given in memory:
+// `cfg` holds the ModelConfig fields (id, V, H, I, N, AI, AH, KVH, AD, RD, KH,
+// VH, KD, VD, CK, experts, top_k, shared_I, matrix_type, tied_embeddings),
+// `image` the weights laid out as model.bin, and (role, layer, offset) each
+// tensor's place in it, roles numbered as the HIP library's tensor roles.
+// logits[t * V ..] receives the logits after token t.  Returns 0 when the
+// configuration cannot be built.
+int q3xr_forward(const int* cfg, const uint8_t* image, const int* roles, const int* layers,
+                 const uint64_t* offsets, int tensors, const int* tokens, int count, float* logits) {
+    const q3x_model::ModelConfig config {
+        static_cast<uint32_t>(cfg[0]), "synthetic", cfg[1], cfg[2], cfg[3], cfg[4],
+        cfg[5], cfg[6], cfg[7], cfg[8], cfg[9], cfg[10], cfg[11], cfg[12], cfg[13], cfg[14],
+        cfg[15], cfg[16], cfg[17], static_cast<q3x_model::MatrixType>(cfg[18]), cfg[19] != 0,
+    };
+    const auto& c = config;
+    const auto M = c.matrix_type;
+    const auto BF = q3x_model::MATRIX_BF16;
+    const int AS = c.AH * c.AD, KVW = c.KVH * c.AD, DO = c.VH * c.VD, DQKV = 2 * c.KH * c.KD + DO;
+    q3x_backend::Model model;
+    model.config = &config;
+    model.layer.reset(new q3x_backend::Layer[c.N]);
+    for (int i = 0; i < tensors; ++i) {
+        const void* p = image + offsets[i];
+        const auto* bf = static_cast<const q3x_backend::BF16*>(p);
+        const auto* f32 = static_cast<const float*>(p);
+        const int l = layers[i];
+        auto lin = [&](int rows, int cols, q3x_model::MatrixType t) { return q3x_backend::Linear{p, rows, cols, t}; };
+        switch (roles[i]) {
+        case 0: model.embedding = lin(c.V, c.H, M); break;
+        case 1: model.lm_head = lin(c.V, c.H, M); break;
+        case 2: model.final_norm = bf; break;
+        case 3: model.layer[l].input_norm = bf; break;
+        case 4: model.layer[l].post_norm = bf; break;
+        case 5: model.layer[l].delta.qkv = lin(DQKV, c.H, M); break;
+        case 6: model.layer[l].delta.z = lin(DO, c.H, M); break;
+        case 7: model.layer[l].delta.a = lin(c.VH, c.H, M); break;
+        case 8: model.layer[l].delta.b = lin(c.VH, c.H, M); break;
+        case 9: model.layer[l].delta.conv = bf; break;
+        case 10: model.layer[l].delta.alog = f32; break;
+        case 11: model.layer[l].delta.dt = bf; break;
+        case 12: model.layer[l].delta.norm = f32; break;
+        case 13: model.layer[l].delta.out = lin(c.H, DO, M); break;
+        case 14: model.layer[l].attention.q = lin(2 * AS, c.H, M); break;
+        case 15: model.layer[l].attention.k = lin(KVW, c.H, M); break;
+        case 16: model.layer[l].attention.v = lin(KVW, c.H, M); break;
+        case 17: model.layer[l].attention.qnorm = bf; break;
+        case 18: model.layer[l].attention.knorm = bf; break;
+        case 19: model.layer[l].attention.out = lin(c.H, AS, M); break;
+        case 20: model.layer[l].gate = lin(c.I, c.H, M); break;
+        case 21: model.layer[l].up = lin(c.I, c.H, M); break;
+        case 22: model.layer[l].down = lin(c.H, c.I, M); break;
+        case 23: model.layer[l].moe.router = lin(c.experts, c.H, BF); break;
+        case 24: model.layer[l].moe.gate_up = {p, c.experts, 2 * c.I, c.H, M}; break;
+        case 25: model.layer[l].moe.down = {p, c.experts, c.H, c.I, M}; break;
+        case 26: model.layer[l].moe.shared_gate = lin(c.shared_I, c.H, M); break;
+        case 27: model.layer[l].moe.shared_up = lin(c.shared_I, c.H, M); break;
+        case 28: model.layer[l].moe.shared_down = lin(c.H, c.shared_I, M); break;
+        case 29: model.layer[l].moe.shared_scale = lin(1, c.H, BF); break;
+        default: return 0;
+        }
+    }
+    if (c.tied_embeddings) model.lm_head = model.embedding;
+    q3x_backend::State state(config, count);
+    for (int t = 0; t < count; ++t) {
+        q3x_backend::forward(model, state, tokens[t], true);
+        std::memcpy(logits + static_cast<size_t>(t) * c.V, state.work.logits, sizeof(float) * c.V);
+    }
+    return 1;
+}
 }  // extern "C"

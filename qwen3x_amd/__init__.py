@@ -66,6 +66,16 @@ SIGNATURES = {
                                 ctypes.POINTER(ctypes.c_uint64)]),
     "q3x_hip_model_tensor": (_I, [_P, _U, _I, _P, ctypes.POINTER(_P)]),
     "q3x_hip_model_moe_layer": (_I, [_P, _I, _P]),
+    "q3x_hip_model_schema": (_I, [_P, _P, _S, ctypes.POINTER(_S), ctypes.POINTER(ctypes.c_uint64)]),
+    "q3x_hip_engine_create": (_I, [_P, _P, _I, ctypes.POINTER(_P), ctypes.POINTER(ctypes.c_char_p)]),
+    "q3x_hip_engine_destroy": (None, [_P]),
+    "q3x_hip_engine_reset": (_I, [_P]),
+    "q3x_hip_engine_forward": (_I, [_P, _P, _I, _I]),
+    "q3x_hip_engine_logits": (_I, [_P, _P]),
+    "q3x_hip_engine_argmax": (_I, [_P, ctypes.POINTER(_I)]),
+    "q3x_hip_engine_checkpoint_save": (_I, [_P]),
+    "q3x_hip_engine_checkpoint_restore": (_I, [_P]),
+    "q3x_hip_engine_position": (_I, [_P]),
 }
 
 
@@ -454,3 +464,100 @@ class Model:
                         DeviceRegion(self, w.down, E * qb(t, H, I)), DeviceRegion(self, w.shared_gate, qb(t, S, H)),
                         DeviceRegion(self, w.shared_up, qb(t, S, H)), DeviceRegion(self, w.shared_down, qb(t, H, S)),
                         DeviceRegion(self, w.shared_scale, H * 2), t, E, c.top_k, H, I, S)
+
+
+CONFIG_FIELDS = ("id", "V", "H", "I", "N", "AI", "AH", "KVH", "AD", "RD", "KH", "VH", "KD", "VD", "CK", "experts",
+                 "top_k", "shared_I", "matrix_type", "tied_embeddings")
+
+
+def make_config(name: str = "synthetic", **fields) -> ModelConfig:
+    """A ModelConfig from keyword fields (CONFIG_FIELDS); unnamed ones are 0."""
+    c = ModelConfig()
+    c.name = name.encode()
+    for k in CONFIG_FIELDS:
+        setattr(c, k, int(fields.get(k, 0)))
+    return c
+
+
+def config_dict(c: ModelConfig) -> dict:
+    return {k: getattr(c, k) for k in CONFIG_FIELDS}
+
+
+def model_schema(config: ModelConfig):
+    """([Tensor] in file order, file bytes) for any configuration."""
+    count = ctypes.c_size_t(0)
+    nbytes = ctypes.c_uint64(0)
+    _check("q3x_hip_model_schema", lib().q3x_hip_model_schema(ctypes.byref(config), None, 0, ctypes.byref(count),
+                                                              ctypes.byref(nbytes)))
+    table = (Tensor * count.value)()
+    _check("q3x_hip_model_schema", lib().q3x_hip_model_schema(ctypes.byref(config), table, count.value,
+                                                              ctypes.byref(count), ctypes.byref(nbytes)))
+    return list(table), nbytes.value
+
+
+class Engine:
+    """The decode engine (q3x_hip_engine_*): a model's weights (a device
+    buffer in model.bin layout) plus device-resident state for `context`
+    tokens.  Mirrors the reference backend's state_* operations
+    (internal.h:11-34)."""
+
+    def __init__(self, config: ModelConfig, weights, context: int):
+        self.config = config
+        self._weights = weights  # keeps the buffer alive
+        handle = ctypes.c_void_p()
+        error = ctypes.c_char_p()
+        ptr = weights if isinstance(weights, int) else _ptr(weights)
+        _check_model("q3x_hip_engine_create",
+                     lib().q3x_hip_engine_create(ctypes.byref(config), ptr, context, ctypes.byref(handle),
+                                                 ctypes.byref(error)), error)
+        self.handle = handle
+
+    @classmethod
+    def from_model(cls, model: "Model", context: int) -> "Engine":
+        return cls(model.config, DeviceRegion(model, model.base, model.nbytes), context)
+
+    def close(self):
+        if getattr(self, "handle", None) is not None:
+            lib().q3x_hip_engine_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def forward(self, tokens, logits: bool = True):
+        import numpy as np
+        t = np.ascontiguousarray(tokens, np.int32).reshape(-1)
+        _check("q3x_hip_engine_forward", lib().q3x_hip_engine_forward(self.handle, t.ctypes.data, t.size, int(logits)))
+
+    def logits(self):
+        import numpy as np
+        out = np.empty(self.config.V, np.float32)
+        _check("q3x_hip_engine_logits", lib().q3x_hip_engine_logits(self.handle, out.ctypes.data))
+        return out
+
+    def argmax(self) -> int:
+        out = ctypes.c_int(-1)
+        _check("q3x_hip_engine_argmax", lib().q3x_hip_engine_argmax(self.handle, ctypes.byref(out)))
+        return out.value
+
+    def reset(self):
+        _check("q3x_hip_engine_reset", lib().q3x_hip_engine_reset(self.handle))
+
+    def checkpoint_save(self):
+        _check("q3x_hip_engine_checkpoint_save", lib().q3x_hip_engine_checkpoint_save(self.handle))
+
+    def checkpoint_restore(self):
+        _check("q3x_hip_engine_checkpoint_restore", lib().q3x_hip_engine_checkpoint_restore(self.handle))
+
+    @property
+    def position(self) -> int:
+        return lib().q3x_hip_engine_position(self.handle)

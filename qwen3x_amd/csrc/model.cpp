@@ -15,6 +15,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <climits>
 #include <cerrno>
 #include <cstring>
 #include <mutex>
@@ -134,6 +135,42 @@ std::vector<q3x_hip_tensor> schema(const q3x_hip_model_config& c) {
     return list;
 }
 
+// Offsets in file order from the end of the header, each tensor at the next
+// multiple of 64 bytes (take(), engine.cpp:461-478); returns the end.
+uint64_t place(std::vector<q3x_hip_tensor>& list) {
+    uint64_t cursor = Q3X_HIP_MODEL_HEADER_BYTES;
+    for (auto& t : list) {
+        cursor = (cursor + kAlignment - 1) / kAlignment * kAlignment;
+        t.offset = cursor;
+        cursor += t.bytes;
+    }
+    return cursor;
+}
+
+// Shapes the schema walk accepts for a configuration given by the caller
+// (the five fixed ones pass): positive sizes, whole 32-element blocks in
+// every quantized row, heads that divide evenly, and sizes whose products
+// fit the int fields of the tensor table.
+bool config_ok(const q3x_hip_model_config& c) {
+    const long long dims[] = {c.V, c.H, c.I, c.N, c.AI, c.AH, c.KVH, c.AD, c.RD, c.KH, c.VH, c.KD, c.VD, c.CK};
+    for (long long d : dims)
+        if (d <= 0 || d > (1 << 24)) return false;
+    if (c.matrix_type > Q3X_HIP_MATRIX_Q4_0 || c.AH % c.KVH != 0 || c.VH % c.KH != 0) return false;
+    if (c.experts < 0 || c.top_k < 0 || c.shared_I < 0) return false;
+    if (c.experts && (c.top_k < 1 || c.top_k > c.experts || c.shared_I < 1)) return false;
+    const long long AS = 1ll * c.AH * c.AD, KVW = 1ll * c.KVH * c.AD, DO = 1ll * c.VH * c.VD;
+    const long long DQKV = 2ll * c.KH * c.KD + DO;
+    const long long rows[] = {2 * AS, KVW, DQKV, DO, 2ll * c.I * std::max(c.experts, 1), 1ll * c.H * std::max(c.experts, 1)};
+    for (long long r : rows)
+        if (r > INT32_MAX) return false;
+    if (c.matrix_type != Q3X_HIP_MATRIX_BF16) {
+        const long long cols[] = {c.H, AS, DO, c.I, c.experts ? c.shared_I : 32};
+        for (long long k : cols)
+            if (k % 32 != 0) return false;
+    }
+    return true;
+}
+
 // Header and size checks of Model::load (engine.cpp:485-496, 559) and the
 // schema walk of take() (engine.cpp:461-478): the cursor only grows, so a
 // tensor ends past the file exactly when the aligned schema end does.
@@ -158,12 +195,7 @@ int validate(const uint8_t* header, uint64_t file_size, const q3x_hip_model_conf
         }
     }
     std::vector<q3x_hip_tensor> list = schema(*found);
-    uint64_t cursor = Q3X_HIP_MODEL_HEADER_BYTES;
-    for (auto& t : list) {
-        cursor = (cursor + kAlignment - 1) / kAlignment * kAlignment;
-        t.offset = cursor;
-        cursor += t.bytes;
-    }
+    const uint64_t cursor = place(list);
     if (cursor > file_size) { *message = "truncated model.bin"; return Q3X_HIP_EMODEL; }
     if (cursor != file_size) { *message = "model.bin size does not match schema"; return Q3X_HIP_EMODEL; }
     *config = found;
@@ -275,6 +307,18 @@ extern "C" int q3x_hip_model_layout(const void* header, size_t header_bytes, uin
     if (tensors && capacity < list.size()) return Q3X_HIP_EINVAL;
     if (tensors) std::copy(list.begin(), list.end(), tensors);
     if (config) *config = *found;
+    return Q3X_HIP_OK;
+}
+
+extern "C" int q3x_hip_model_schema(const q3x_hip_model_config* config, q3x_hip_tensor* tensors, size_t capacity,
+                                    size_t* count, uint64_t* bytes) {
+    if (!config || !count || !config_ok(*config)) return Q3X_HIP_EINVAL;
+    std::vector<q3x_hip_tensor> list = schema(*config);
+    const uint64_t end = place(list);
+    *count = list.size();
+    if (bytes) *bytes = end;
+    if (tensors && capacity < list.size()) return Q3X_HIP_EINVAL;
+    if (tensors) std::copy(list.begin(), list.end(), tensors);
     return Q3X_HIP_OK;
 }
 

@@ -1,0 +1,97 @@
+"""GPU tests of the decode engine (q3x_hip_engine_*) against the reference's
+own CPU forward (engine.cpp:431-454, built from the reference sources into
+oracle/_ref) on small synthetic models with the real head sizes: logits after
+every token within 2e-4 + 2e-4 |reference|, the bound of the reference's own
+synthetic forward test (tests/metal_test.mm:121-124).  The reference forward
+runs here and on the GPU box from the built library; with it absent these
+tests skip."""
+import numpy as np
+import pytest
+
+import oracle
+import qwen3x_amd as q3x
+from tests.engine_models import CONFIGS, synthetic_model
+from tests.test_gpu_parity import _torch, dev, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _need_ref():
+    if oracle.ref() is None:
+        pytest.skip("reference build (oracle/_ref) absent")
+
+
+def _bound(want):
+    return 2e-4 + 2e-4 * np.abs(want)
+
+
+@pytest.mark.parametrize("name", sorted(CONFIGS))
+def test_engine_logits_match_the_reference_forward(name):
+    _need_ref()
+    _torch()
+    fields = CONFIGS[name]
+    config, image, table = synthetic_model(fields, seed=fields["id"])
+    rng = np.random.default_rng(100 + fields["id"])
+    tokens = rng.integers(0, fields["V"], 12).astype(np.int32)
+    want = oracle.ref_forward(fields, image, table, tokens)
+    weights = dev(image)
+    say(f"engine {name}: {len(tokens)} tokens")
+    with q3x.Engine(config, weights, context=len(tokens)) as engine:
+        for i, tok in enumerate(tokens):
+            engine.forward([tok])
+            got = engine.logits()
+            assert np.all(np.isfinite(got)), i
+            diff = np.abs(got - want[i])
+            assert np.all(diff <= _bound(want[i])), f"token {i}: worst {diff.max()} at {diff.argmax()}"
+        assert engine.position == len(tokens)
+
+
+@pytest.mark.parametrize("name", ["dense_q4", "moe_q4"])
+def test_prefill_then_decode_equals_token_by_token(name):
+    # A forward of several tokens (logits of the last) gives the same bits as
+    # the same tokens one call at a time: the same graph runs per token.
+    _torch()
+    fields = CONFIGS[name]
+    config, image, _ = synthetic_model(fields, seed=7)
+    tokens = np.random.default_rng(8).integers(0, fields["V"], 10).astype(np.int32)
+    weights = dev(image)
+    say(f"engine {name}: prefill vs token by token")
+    with q3x.Engine(config, weights, context=16) as a, q3x.Engine(config, weights, context=16) as b:
+        a.forward(tokens[:7])
+        a.forward(tokens[7:])
+        for tok in tokens:
+            b.forward([tok])
+        assert np.array_equal(a.logits().view(np.uint32), b.logits().view(np.uint32))
+        assert a.argmax() == b.argmax() == int(np.argmax(b.logits()))
+
+
+def test_checkpoint_reset_and_errors():
+    _torch()
+    fields = CONFIGS["moe_q4"]
+    config, image, _ = synthetic_model(fields, seed=9)
+    rng = np.random.default_rng(10)
+    prompt = rng.integers(0, fields["V"], 5).astype(np.int32)
+    cont = rng.integers(0, fields["V"], 3).astype(np.int32)
+    weights = dev(image)
+    say("engine checkpoint / reset")
+    with q3x.Engine(config, weights, context=8) as e:
+        e.forward(prompt)
+        first = e.logits()
+        e.checkpoint_save()
+        e.forward(cont)
+        after = e.logits()
+        e.checkpoint_restore()
+        assert e.position == 5
+        assert np.array_equal(e.logits().view(np.uint32), first.view(np.uint32))
+        e.forward(cont)
+        assert np.array_equal(e.logits().view(np.uint32), after.view(np.uint32))
+        e.reset()
+        assert e.position == 0
+        e.forward(prompt)
+        assert np.array_equal(e.logits().view(np.uint32), first.view(np.uint32))
+        # context exhausted / bad tokens: rejected, nothing run
+        with pytest.raises(q3x.Q3xHipError):
+            e.forward(np.zeros(4, np.int32))
+        with pytest.raises(q3x.Q3xHipError):
+            e.forward([fields["V"]])
+        assert e.position == 5

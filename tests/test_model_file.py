@@ -191,3 +191,52 @@ def test_quantize_bf16_arguments_are_rejected_without_device_work():
     assert lib.q3x_hip_quantize_bf16(2, ctypes.c_void_p(0x1002), 1, 32, P, None) == q3x.EINVAL
     assert lib.q3x_hip_quantize_bf16(1, P, 1, 48, P, None) == q3x.EINVAL
     assert lib.q3x_hip_quantize_bf16(7, P, 1, 32, P, None) == q3x.EINVAL
+
+
+def test_schema_for_any_configuration_and_its_rejections():
+    from tests.engine_models import CONFIGS
+    for model_id in IDS:   # the fixed configurations give the file layout
+        m = mf.MODELS[model_id]
+        cfg = q3x.make_config(id=model_id, V=m["vocab"], H=m["hidden"], I=m["intermediate"], N=m["layers"],
+                              AI=m["interval"], AH=m["heads"], KVH=m["kv_heads"], AD=m["head_dim"],
+                              RD=m["rotary_dim"], KH=m["key_heads"], VH=m["value_heads"], KD=m["key_dim"],
+                              VD=m["value_dim"], CK=m["conv"], experts=m["experts"], top_k=m["top_k"],
+                              shared_I=m["shared"], matrix_type=mf.MATRIX_TYPE[m["matrix"]],
+                              tied_embeddings=int(m["tied"]))
+        table, nbytes = q3x.model_schema(cfg)
+        rows, size = mf.layout(model_id)
+        assert nbytes == size
+        assert [(q3x.TENSOR_ROLES[t.role], t.layer, t.offset, t.bytes) for t in table] == \
+            [(r, l, o, b) for r, l, _, o, b in rows]
+    base = dict(CONFIGS["moe_q4"])
+    lib = q3x.lib()
+    count = ctypes.c_size_t(0)
+    for bad in (dict(H=0), dict(H=250), dict(AH=3, KVH=2), dict(VH=3, KH=2), dict(top_k=9), dict(shared_I=0), dict(I=40),
+                dict(matrix_type=5)):
+        cfg = q3x.make_config(**dict(base, **bad))
+        assert lib.q3x_hip_model_schema(ctypes.byref(cfg), None, 0, ctypes.byref(count), None) == q3x.EINVAL, bad
+
+
+def test_engine_rejects_before_device_work():
+    from tests.engine_models import CONFIGS
+    lib = q3x.lib()
+    handle = ctypes.c_void_p()
+    error = ctypes.c_char_p()
+    P = ctypes.c_void_p(0x1000)   # never dereferenced: validation fails first
+    bf16 = q3x.make_config(**dict(CONFIGS["dense_q8"], matrix_type=0))
+    assert lib.q3x_hip_engine_create(ctypes.byref(bf16), P, 8, ctypes.byref(handle), ctypes.byref(error)) == \
+        q3x.ENOTSUP
+    assert b"BF16" in error.value
+    for bad in (dict(KD=256), dict(VD=160), dict(RD=128), dict(CK=1), dict(H=250)):
+        cfg = q3x.make_config(**dict(CONFIGS["dense_q8"], **bad))
+        assert lib.q3x_hip_engine_create(ctypes.byref(cfg), P, 8, ctypes.byref(handle), ctypes.byref(error)) == \
+            q3x.EINVAL, bad
+    good = q3x.make_config(**CONFIGS["dense_q8"])
+    for context in (0, 262145):
+        assert lib.q3x_hip_engine_create(ctypes.byref(good), P, context, ctypes.byref(handle), None) == q3x.EINVAL
+    assert lib.q3x_hip_engine_create(ctypes.byref(good), None, 8, ctypes.byref(handle), None) == q3x.EINVAL
+    assert lib.q3x_hip_engine_forward(None, P, 1, 1) == q3x.EINVAL
+    assert lib.q3x_hip_engine_logits(None, P) == q3x.EINVAL
+    assert lib.q3x_hip_engine_reset(None) == q3x.EINVAL
+    assert lib.q3x_hip_engine_position(None) == -1
+    lib.q3x_hip_engine_destroy(None)
