@@ -11,12 +11,17 @@
 // kernels here are the small per-token operations between them.
 //
 // Every buffer lives on the device for the life of the engine: the work
-// vectors, the DeltaNet recurrent state (conv history and the KD x VD memory
-// of each head), the KV cache, the logits.  The token and the position are
+// rows, the DeltaNet recurrent state (conv history and the KD x VD memory of
+// each head), the KV cache, the logits.  The tokens and the position are
 // read from device memory, so one decode step is position-independent and
 // is captured once into a hipGraph (two: with and without logits) and
 // replayed for every token, as the reference captures its step
-// (arch/cuda/engine.cu:1995-2005).
+// (arch/cuda/engine.cu:1995-2005).  A forward of several tokens runs them
+// as chunks of up to kChunk rows: the matrices as prefill GEMMs
+// (q3x_hip_gemm, q3x_hip_moe_layer's grouped path), the conv and delta rule
+// token by token inside one launch with the state in registers, norms, RoPE
+// and attention over all rows at once -- the role of the reference's
+// prefill_chunk_* (arch/cuda/engine.cu:1881-1960).
 #include <math.h>
 
 #include <algorithm>
@@ -66,16 +71,19 @@ __device__ float block_max(float v, float* partial) {
 // engine.cpp:192
 __device__ __forceinline__ float softplus_ref(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 
-// Row `*token` of the embedding, dequantised bit for bit as the reference's
-// embed (engine.cpp:195-200 via arch/cpu.cpp:55-63, 81-90).
+// Rows of the embedding for tokens tokens[*step + r], r = blockIdx.y,
+// dequantised bit for bit as the reference's embed (engine.cpp:195-200 via
+// arch/cpu.cpp:55-63, 81-90).
 template <uint32_t QT>
 __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ w, int cols,
                                                     const int* __restrict__ tokens, const int* __restrict__ step,
                                                     float* __restrict__ out) {
     constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
-    const int token = tokens[*step];
+    const int r = blockIdx.y;
+    const int token = tokens[*step + r];
     const int bpr = cols / kBlock;
     const uint8_t* row = w + static_cast<size_t>(token) * bpr * BB;
+    float* o = out + static_cast<size_t>(r) * cols;
     for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += gridDim.x * blockDim.x) {
         const uint8_t* blk = row + (c / kBlock) * BB;
         const float scale = f16_exact(blk[0] | (blk[1] << 8));
@@ -87,111 +95,169 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ 
             const uint32_t packed = blk[2 + within % 16];
             q = static_cast<int>(within < 16 ? (packed & 15u) : (packed >> 4)) - 8;
         }
-        out[c] = scale * static_cast<float>(q);
+        o[c] = scale * static_cast<float>(q);
     }
 }
 
-// out = RMSNorm(hidden) * (1 + w) (engine.cpp:228-233); with `branch`,
-// hidden += branch first and is written back (the residual add of
-// engine.cpp:240-242 that precedes the norm).  One workgroup.
+// Row r = blockIdx.x: out = RMSNorm(hidden) * (1 + w) (engine.cpp:228-233);
+// with `branch`, hidden += branch first and is written back (the residual
+// add of engine.cpp:240-242 that precedes the norm).
 __global__ __launch_bounds__(kNormThreads) void rms_kernel(float* __restrict__ hidden, const float* __restrict__ branch,
                                                            const uint16_t* __restrict__ w, int n,
                                                            float* __restrict__ out) {
     __shared__ float partial[kNormThreads / kWave];
+    const size_t base = static_cast<size_t>(blockIdx.x) * n;
+    float* x = hidden + base;
     float square = 0.0f;
     for (int i = threadIdx.x; i < n; i += kNormThreads) {
-        float x = hidden[i];
+        float v = x[i];
         if (branch) {
-            x += branch[i];
-            hidden[i] = x;
+            v += branch[base + i];
+            x[i] = v;
         }
-        square = fmaf(x, x, square);
+        square = fmaf(v, v, square);
     }
     const float total = block_sum<kNormThreads>(square, partial);
     const float scale = 1.0f / sqrtf(total / static_cast<float>(n) + kEps);
-    for (int i = threadIdx.x; i < n; i += kNormThreads) out[i] = hidden[i] * scale * (1.0f + bf16_value(w[i]));
+    for (int i = threadIdx.x; i < n; i += kNormThreads) out[base + i] = x[i] * scale * (1.0f + bf16_value(w[i]));
 }
 
-// Causal depthwise convolution of one token over the DQKV channels with
-// CK - 1 remembered inputs, then SiLU (engine.cpp:251-261).
+// Causal depthwise convolution over the DQKV channels with CK - 1
+// remembered inputs, then SiLU (engine.cpp:251-261), for `count` tokens in
+// order (rows of qkv, in place); the history stays in registers.
+constexpr int kMaxConv = 8;
 __global__ __launch_bounds__(256) void delta_conv_kernel(float* __restrict__ qkv, const uint16_t* __restrict__ w,
-                                                         float* __restrict__ history, int channels, int CK) {
+                                                         float* __restrict__ history, int channels, int CK,
+                                                         int count) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= channels) return;
-    const float x = qkv[c];
     const uint16_t* wc = w + static_cast<size_t>(c) * CK;
-    float* past = history + static_cast<size_t>(c) * (CK - 1);
-    float sum = x * bf16_value(wc[CK - 1]);
-    for (int i = 0; i < CK - 1; ++i) sum = fmaf(past[i], bf16_value(wc[i]), sum);
-    for (int i = 0; i < CK - 2; ++i) past[i] = past[i + 1];
-    past[CK - 2] = x;
-    qkv[c] = silu_ref(sum);
+    float* hist = history + static_cast<size_t>(c) * (CK - 1);
+    float past[kMaxConv - 1], wt[kMaxConv];
+#pragma unroll
+    for (int i = 0; i < kMaxConv - 1; ++i) past[i] = i < CK - 1 ? hist[i] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxConv; ++i) wt[i] = i < CK ? bf16_value(wc[i]) : 0.0f;
+    for (int t = 0; t < count; ++t) {
+        float* xp = qkv + static_cast<size_t>(t) * channels + c;
+        const float x = *xp;
+        float last = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxConv; ++i)
+            if (i == CK - 1) last = wt[i];
+        float sum = x * last;
+#pragma unroll
+        for (int i = 0; i < kMaxConv - 1; ++i)
+            if (i < CK - 1) sum = fmaf(past[i], wt[i], sum);
+#pragma unroll
+        for (int i = 0; i < kMaxConv - 2; ++i)
+            if (i < CK - 2) past[i] = past[i + 1];
+#pragma unroll
+        for (int i = 0; i < kMaxConv - 1; ++i)
+            if (i == CK - 2) past[i] = x;
+        *xp = silu_ref(sum);
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxConv - 1; ++i)
+        if (i < CK - 1) hist[i] = past[i];
 }
 
-// One value head of the gated delta rule (engine.cpp:262-316): L2-normalised
-// q and k of its key head (q also divided by sqrt(KD)), beta = sigmoid(b),
-// decay = -exp(A_log) * softplus(a + dt_bias); the KD x VD memory S decays
-// by exp(decay), takes k (beta (v - k S)), and gives out = q S; then the
-// gated RMSNorm with the FP32 norm weight and SiLU(z) (engine.cpp:234-239).
-// 256 threads: thread t owns value column t % 128 and half of the keys, so
-// its S entries stay in registers between the three passes.
-// Requires KD <= 128, VD <= 128.
-__global__ __launch_bounds__(kHeadThreads) void delta_rule_kernel(
+// One value head of the gated delta rule (engine.cpp:262-316) for `count`
+// tokens in order: L2-normalised q and k of its key head (q also divided by
+// sqrt(KD)), beta = sigmoid(b), decay = -exp(A_log) * softplus(a + dt_bias);
+// the KD x VD memory S decays by exp(decay), takes k (beta (v - k S)), and
+// gives out = q S; then the gated RMSNorm with the FP32 norm weight and
+// SiLU(z) (engine.cpp:234-239).  1024 threads: thread t owns value column
+// t % 128 and keys 16 (t / 128) .. + 15, so its S entries stay in registers
+// across the tokens; sums over keys add the eight key groups' partials in a
+// fixed order.  Requires KD <= 128, VD <= 128.
+constexpr int kDeltaThreads = 1024;
+constexpr int kDeltaGroups = kDeltaThreads / 128;  // key groups
+constexpr int kDeltaKeys = 128 / kDeltaGroups;     // keys per thread
+
+__global__ __launch_bounds__(kDeltaThreads) void delta_rule_kernel(
     const float* __restrict__ qkv, const float* __restrict__ a, const float* __restrict__ b,
     const float* __restrict__ z, const float* __restrict__ alog, const uint16_t* __restrict__ dt,
     const float* __restrict__ norm, float* __restrict__ memory, float* __restrict__ out, int KH, int VH, int KD,
-    int VD) {
-    __shared__ float qs[128], ks[128], part[2][128], partial[kHeadThreads / kWave];
+    int VD, int count) {
+    __shared__ float qs[128], ks[128], part[kDeltaGroups][128], sum[128], partial[kDeltaThreads / kWave];
     const int head = blockIdx.x;
     const int t = threadIdx.x;
-    const int DQK = KH * KD;
+    const int DQK = KH * KD, DO = VH * VD, DQKV = 2 * DQK + DO;
     const int kh = head / (VH / KH);
-    const float qv = t < KD ? qkv[kh * KD + t] : 0.0f;
-    const float kv = t < KD ? qkv[DQK + kh * KD + t] : 0.0f;
-    const float qn = block_sum<kHeadThreads>(qv * qv, partial);
-    const float kn = block_sum<kHeadThreads>(kv * kv, partial);
-    if (t < KD) {
-        qs[t] = qv * (1.0f / sqrtf(qn + kEps)) / sqrtf(static_cast<float>(KD));
-        ks[t] = kv * (1.0f / sqrtf(kn + kEps));
-    }
-    __syncthreads();
-    const float beta = sigmoid_ref(b[head]);
-    const float decay = -expf(alog[head]) * softplus_ref(a[head] + bf16_value(dt[head]));
-    const float scale = expf(decay);
-    const int v = t & 127, half = t >> 7;
-    const int k0 = half * 64;
+    const int v = t & 127, group = t >> 7;
     const bool col = v < VD;
     float* S = memory + static_cast<size_t>(head) * KD * VD;
-    float s[64];
-    float pred = 0.0f;
+    float s[kDeltaKeys];
 #pragma unroll
-    for (int j = 0; j < 64; ++j) {
-        const int key = k0 + j;
-        s[j] = col && key < KD ? S[static_cast<size_t>(key) * VD + v] * scale : 0.0f;
-        if (key < KD) pred = fmaf(ks[key], s[j], pred);
+    for (int j = 0; j < kDeltaKeys; ++j) {
+        const int key = group * kDeltaKeys + j;
+        s[j] = col && key < KD ? S[static_cast<size_t>(key) * VD + v] : 0.0f;
     }
-    part[half][v] = pred;
-    __syncthreads();
-    const float vv = col ? qkv[2 * DQK + head * VD + v] : 0.0f;
-    const float delta = vv - (part[0][v] + part[1][v]);
-    float o = 0.0f;
+    const float A = expf(alog[head]);
+    const float bias = bf16_value(dt[head]);
+    const float nv = norm[t < VD ? t : 0];
+    for (int r = 0; r < count; ++r) {
+        const float* row = qkv + static_cast<size_t>(r) * DQKV;
+        const float qv = t < KD ? row[kh * KD + t] : 0.0f;
+        const float kv = t < KD ? row[DQK + kh * KD + t] : 0.0f;
+        const float vv = col ? row[2 * DQK + head * VD + v] : 0.0f;
+        const float qn = block_sum<kDeltaThreads>(qv * qv, partial);
+        const float kn = block_sum<kDeltaThreads>(kv * kv, partial);
+        if (t < KD) {
+            qs[t] = qv * (1.0f / sqrtf(qn + kEps)) / sqrtf(static_cast<float>(KD));
+            ks[t] = kv * (1.0f / sqrtf(kn + kEps));
+        }
+        __syncthreads();
+        const float beta = sigmoid_ref(b[static_cast<size_t>(r) * VH + head]);
+        const float decay = -A * softplus_ref(a[static_cast<size_t>(r) * VH + head] + bias);
+        const float scale = expf(decay);
+        float pred = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 64; ++j) {
-        const int key = k0 + j;
-        if (key < KD) {
-            s[j] = fmaf(ks[key] * beta, delta, s[j]);
-            o = fmaf(qs[key], s[j], o);
-            if (col) S[static_cast<size_t>(key) * VD + v] = s[j];
+        for (int j = 0; j < kDeltaKeys; ++j) {
+            const int key = group * kDeltaKeys + j;
+            s[j] *= scale;
+            if (key < KD) pred = fmaf(ks[key], s[j], pred);
+        }
+        part[group][v] = pred;
+        __syncthreads();
+        if (t < 128) {
+            float p = part[0][t];
+#pragma unroll
+            for (int g = 1; g < kDeltaGroups; ++g) p += part[g][t];
+            sum[t] = p;
+        }
+        __syncthreads();
+        const float delta = vv - sum[v];
+        float o = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kDeltaKeys; ++j) {
+            const int key = group * kDeltaKeys + j;
+            if (key < KD) {
+                s[j] = fmaf(ks[key] * beta, delta, s[j]);
+                o = fmaf(qs[key], s[j], o);
+            }
+        }
+        __syncthreads();  // every read of part / sum / qs / ks above is done
+        part[group][v] = o;
+        __syncthreads();
+        float result = 0.0f;
+        if (t < VD) {
+            result = part[0][t];
+#pragma unroll
+            for (int g = 1; g < kDeltaGroups; ++g) result += part[g][t];
+        }
+        const float sq = block_sum<kDeltaThreads>(result * result, partial);
+        if (t < VD) {
+            const float g = 1.0f / sqrtf(sq / static_cast<float>(VD) + kEps);
+            const size_t at = static_cast<size_t>(r) * DO + head * VD + t;
+            out[at] = result * (g * nv * silu_ref(z[at]));
         }
     }
-    __syncthreads();
-    part[half][v] = o;
-    __syncthreads();
-    const float result = col && half == 0 ? part[0][v] + part[1][v] : 0.0f;
-    const float sq = block_sum<kHeadThreads>(result * result, partial);
-    if (col && half == 0) {
-        const float g = 1.0f / sqrtf(sq / static_cast<float>(VD) + kEps);
-        out[head * VD + v] = result * (g * norm[v] * silu_ref(z[head * VD + v]));
+#pragma unroll
+    for (int j = 0; j < kDeltaKeys; ++j) {
+        const int key = group * kDeltaKeys + j;
+        if (col && key < KD) S[static_cast<size_t>(key) * VD + v] = s[j];
     }
 }
 
@@ -218,9 +284,9 @@ __device__ void norm_rope(float* x, const uint16_t* w, int AD, int RD, int posit
     __syncthreads();
 }
 
-// Query heads (blocks 0 .. AH-1): split the q|gate rows, norm and rotate q;
-// key/value heads (blocks AH ..): norm and rotate k and append k and v to
-// the cache at the current position (engine.cpp:318-343).  AD <= 256.
+// Row r = blockIdx.y at position *position + r.  Query heads (blockIdx.x <
+// AH): split the q|gate rows, norm and rotate q; key/value heads: norm and
+// rotate k and append k and v to the cache (engine.cpp:318-343).  AD <= 256.
 __global__ __launch_bounds__(kHeadThreads) void attention_prep_kernel(
     const float* __restrict__ query_and_gate, const float* __restrict__ key, const float* __restrict__ value,
     const uint16_t* __restrict__ qnorm, const uint16_t* __restrict__ knorm, const int* __restrict__ position,
@@ -228,73 +294,134 @@ __global__ __launch_bounds__(kHeadThreads) void attention_prep_kernel(
     float* __restrict__ value_cache, int AH, int KVH, int AD, int RD) {
     __shared__ float x[256], partial[kHeadThreads / kWave];
     const int t = threadIdx.x;
-    const int pos = *position;
+    const int r = blockIdx.y;
+    const int pos = *position + r;
+    const int AS = AH * AD, KVW = KVH * AD;
     if (blockIdx.x < AH) {
         const int head = blockIdx.x;
+        const float* qg = query_and_gate + static_cast<size_t>(r) * 2 * AS;
         if (t < AD) {
-            x[t] = query_and_gate[head * 2 * AD + t];
-            gate[head * AD + t] = query_and_gate[head * 2 * AD + AD + t];
+            x[t] = qg[head * 2 * AD + t];
+            gate[static_cast<size_t>(r) * AS + head * AD + t] = qg[head * 2 * AD + AD + t];
         }
         __syncthreads();
         norm_rope(x, qnorm, AD, RD, pos, partial);
-        if (t < AD) query[head * AD + t] = x[t];
+        if (t < AD) query[static_cast<size_t>(r) * AS + head * AD + t] = x[t];
     } else {
         const int head = blockIdx.x - AH;
-        if (t < AD) x[t] = key[head * AD + t];
+        if (t < AD) x[t] = key[static_cast<size_t>(r) * KVW + head * AD + t];
         __syncthreads();
         norm_rope(x, knorm, AD, RD, pos, partial);
         const size_t at = (static_cast<size_t>(pos) * KVH + head) * AD;
         if (t < AD) {
             key_cache[at + t] = x[t];
-            value_cache[at + t] = value[head * AD + t];
+            value_cache[at + t] = value[static_cast<size_t>(r) * KVW + head * AD + t];
         }
     }
 }
 
-// One query head over positions 0 .. position (engine.cpp:344-361): scores
-// q . k / sqrt(AD), max-subtracted softmax, sum of p / total * v in token
-// order, times sigmoid(gate).  Scores go to `scores` [AH, capacity].
+// Attention of query row r = blockIdx.y, head blockIdx.x / splits, over the
+// positions 0 .. *position + r (causal; engine.cpp:344-361: scores q . k /
+// sqrt(AD), softmax, sum of weights times v), with the softmax taken online
+// over blocks of 64 positions (a running maximum rescales the running sum
+// and accumulator), so no score buffer bounds the context.  With splits > 1
+// each workgroup takes one of `splits` position ranges and leaves its range's
+// maximum, sum and accumulator in `partial` for attention_combine_kernel;
+// with splits == 1 it writes the gated output.  AD <= 256.
+constexpr int kAttnSplits = 32;  // ranges per head for a decode step
+constexpr int kChunk = 512;      // rows of a prefill chunk
+constexpr int kAttnBlock = 64;
+
 __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
     const float* __restrict__ query, const float* __restrict__ gate, const float* __restrict__ key_cache,
-    const float* __restrict__ value_cache, const int* __restrict__ position, float* __restrict__ scores,
-    float* __restrict__ out, int AH, int KVH, int AD, int capacity) {
-    __shared__ float partial[kHeadThreads / kWave];
-    const int head = blockIdx.x;
+    const float* __restrict__ value_cache, const int* __restrict__ position, float* __restrict__ partial,
+    float* __restrict__ out, int AH, int KVH, int AD, int splits) {
+    __shared__ float sc[kAttnBlock], pw[kAttnBlock];
+    const int head = blockIdx.x / splits, split = blockIdx.x % splits;
+    const int r = blockIdx.y;
     const int kv = head / (AH / KVH);
-    const int n = *position + 1;
+    const int AS = AH * AD;
+    const int n = *position + r + 1;
+    const int per = (n + splits - 1) / splits;
+    const int t0 = min(n, split * per), t1 = min(n, t0 + per);
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const float* q = query + head * AD;
-    float* sc = scores + static_cast<size_t>(head) * capacity;
+    const int i = threadIdx.x;
+    const float* q = query + static_cast<size_t>(r) * AS + head * AD;
     const float divisor = sqrtf(static_cast<float>(AD));
     float qr[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) qr[j] = lane + 64 * j < AD ? q[lane + 64 * j] : 0.0f;
-    for (int tok = wave; tok < n; tok += kHeadThreads / kWave) {
-        const float* k = key_cache + (static_cast<size_t>(tok) * KVH + kv) * AD;
-        float d = 0.0f;
+    float m = -INFINITY, l = 0.0f, acc = 0.0f;
+    for (int b0 = t0; b0 < t1; b0 += kAttnBlock) {
+        const int nb = min(kAttnBlock, t1 - b0);
+        for (int j = wave; j < nb; j += kHeadThreads / kWave) {
+            const float* k = key_cache + (static_cast<size_t>(b0 + j) * KVH + kv) * AD;
+            float d = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (lane + 64 * j < AD) d = fmaf(qr[j], k[lane + 64 * j], d);
-        d = wave_sum_f32(d);
-        if (lane == 0) sc[tok] = d / divisor;
+            for (int u = 0; u < 4; ++u)
+                if (lane + 64 * u < AD) d = fmaf(qr[u], k[lane + 64 * u], d);
+            d = wave_sum_f32(d);
+            if (lane == 0) sc[j] = d / divisor;
+        }
+        __syncthreads();
+        float bm = sc[0];
+        for (int j = 1; j < nb; ++j) bm = fmaxf(bm, sc[j]);
+        const float mn = fmaxf(m, bm);
+        if (i < nb) pw[i] = expf(sc[i] - mn);
+        __syncthreads();
+        const float alpha = expf(m - mn);  // 0 for the first block (m = -inf)
+        float ps = 0.0f;
+        for (int j = 0; j < nb; ++j) ps += pw[j];
+        l = l * alpha + ps;
+        if (i < AD) {
+            float a = acc * alpha;
+            for (int j = 0; j < nb; ++j)
+                a = fmaf(pw[j], value_cache[(static_cast<size_t>(b0 + j) * KVH + kv) * AD + i], a);
+            acc = a;
+        }
+        m = mn;
+        __syncthreads();  // sc / pw are rewritten by the next block
     }
-    __syncthreads();
-    float m = -INFINITY;
-    for (int tok = threadIdx.x; tok < n; tok += kHeadThreads) m = fmaxf(m, sc[tok]);
-    m = block_max<kHeadThreads>(m, partial);
-    float sum = 0.0f;
-    for (int tok = threadIdx.x; tok < n; tok += kHeadThreads) {
-        const float e = expf(sc[tok] - m);
-        sc[tok] = e;
-        sum += e;
+    if (splits == 1) {
+        if (i < AD) {
+            const size_t at = static_cast<size_t>(r) * AS + head * AD + i;
+            out[at] = acc / l * sigmoid_ref(gate[at]);
+        }
+        return;
     }
-    const float total = block_sum<kHeadThreads>(sum, partial);  // also orders the sc writes before the reads
-    const int i = threadIdx.x;
-    if (i < AD) {
+    float* p = partial + ((static_cast<size_t>(r) * AH + head) * splits + split) * (AD + 2);
+    if (i < AD) p[i] = acc;
+    if (i == 0) {
+        p[AD] = m;
+        p[AD + 1] = l;
+    }
+}
+
+// out = (sum_s exp(m_s - M) acc_s) / (sum_s exp(m_s - M) l_s) * sigmoid(gate)
+// over the ranges s of one head of row r = blockIdx.y, M their largest
+// maximum (empty ranges have m = -inf and contribute nothing).
+__global__ __launch_bounds__(kHeadThreads) void attention_combine_kernel(const float* __restrict__ partial,
+                                                                         const float* __restrict__ gate,
+                                                                         float* __restrict__ out, int AH, int AD,
+                                                                         int splits) {
+    const int head = blockIdx.x, r = blockIdx.y;
+    const float* p = partial + (static_cast<size_t>(r) * AH + head) * splits * (AD + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < splits; ++s) M = fmaxf(M, p[s * (AD + 2) + AD]);
+    float L = 0.0f;
+    for (int s = 0; s < splits; ++s) {
+        const float m = p[s * (AD + 2) + AD];
+        if (m != -INFINITY) L += expf(m - M) * p[s * (AD + 2) + AD + 1];
+    }
+    const int AS = AH * AD;
+    for (int i = threadIdx.x; i < AD; i += kHeadThreads) {
         float acc = 0.0f;
-        for (int tok = 0; tok < n; ++tok)
-            acc = fmaf(sc[tok] / total, value_cache[(static_cast<size_t>(tok) * KVH + kv) * AD + i], acc);
-        out[head * AD + i] = acc * sigmoid_ref(gate[head * AD + i]);
+        for (int s = 0; s < splits; ++s) {
+            const float m = p[s * (AD + 2) + AD];
+            if (m != -INFINITY) acc = fmaf(expf(m - M), p[s * (AD + 2) + i], acc);
+        }
+        const size_t at = static_cast<size_t>(r) * AS + head * AD + i;
+        out[at] = acc / L * sigmoid_ref(gate[at]);
     }
 }
 
@@ -312,7 +439,6 @@ __global__ __launch_bounds__(kNormThreads) void argmax_kernel(const float* __res
     int index = n;
     for (int i = threadIdx.x; i < n; i += kNormThreads)
         if (x[i] > best || index == n) { best = x[i]; index = i; }
-    // Wave: the largest value, the lowest index among equals.
     for (int off = 32; off >= 1; off >>= 1) {
         const float ob = __shfl_xor(best, off);
         const int oi = __shfl_xor(index, off);
@@ -332,10 +458,10 @@ __global__ __launch_bounds__(kNormThreads) void argmax_kernel(const float* __res
     }
 }
 
-// Moves to the next token: step (index into the token list) and position.
-__global__ void advance_kernel(int* step, int* position) {
-    *step += 1;
-    *position += 1;
+// Moves past `count` tokens: step (index into the token list) and position.
+__global__ void advance_kernel(int* step, int* position, int count) {
+    *step += count;
+    *position += count;
 }
 __global__ void set_counters_kernel(int* step, int* position, int step_value, int position_value) {
     *step = step_value;
@@ -414,83 +540,115 @@ T* carve(uint8_t*& cursor, size_t count) {
     return p;
 }
 
-// Enqueues one decode step: token tokens[*d_step] at *d_position.
-int enqueue_step(q3x_hip_engine& e, bool logits) {
+// One matrix applied to `count` rows of x: the matvec for a decode step, the
+// prefill GEMM for a chunk.
+int apply(const Mat& m, uint32_t type, const float* x, int count, float* y, bool accumulate, hipStream_t s) {
+    if (count == 1) return q3x_hip_mv(m.w, type, m.rows, m.cols, x, y, accumulate ? 1 : 0, s);
+    return q3x_hip_gemm(m.w, type, m.rows, m.cols, x, count, y, accumulate ? 1 : 0, s);
+}
+
+// Several matrices of width `cols` applied to the same rows: one multi-matrix
+// launch for a decode step (the reference's projection helpers,
+// engine.cu:1599-1661), one GEMM each for a chunk.
+int apply_group(const Mat* m, float* const* y, int n, uint32_t type, int cols, const float* x, int count,
+                hipStream_t s) {
+    if (count == 1) {
+        q3x_hip_mv_item items[Q3X_HIP_MV_MULTI_MAX];
+        for (int i = 0; i < n; ++i) items[i] = q3x_hip_mv_item{m[i].w, m[i].rows, y[i], 0};
+        return q3x_hip_mv_multi(items, n, type, cols, x, s);
+    }
+    for (int i = 0; i < n; ++i) {
+        const int rc = q3x_hip_gemm(m[i].w, type, m[i].rows, cols, x, count, y[i], 0, s);
+        if (rc) return rc;
+    }
+    return Q3X_HIP_OK;
+}
+
+// Enqueues `count` tokens (tokens[*d_step ..] at *d_position ..) through
+// every layer; the logits of the last one when `logits`; then advances the
+// step and position by count.  count 1 is the decode step the graphs
+// capture; count > 1 (at most kChunk) a prefill chunk.
+int enqueue(q3x_hip_engine& e, int count, bool logits) {
     const q3x_hip_model_config& c = e.c;
     hipStream_t s = e.stream;
     const int DQKV = 2 * c.KH * c.KD + c.VH * c.VD;
     const uint32_t type = c.matrix_type;
-    const int eb = (c.H + 255) / 256;
+    const dim3 eg((c.H + 255) / 256, count);
     if (type == Q3X_HIP_MATRIX_Q8_0)
-        hipLaunchKernelGGL(embed_kernel<Q3X_HIP_MATRIX_Q8_0>, dim3(eb), dim3(256), 0, s,
+        hipLaunchKernelGGL(embed_kernel<Q3X_HIP_MATRIX_Q8_0>, eg, dim3(256), 0, s,
                            static_cast<const uint8_t*>(e.embedding.w), c.H, e.d_tokens, e.d_step, e.hidden);
     else
-        hipLaunchKernelGGL(embed_kernel<Q3X_HIP_MATRIX_Q4_0>, dim3(eb), dim3(256), 0, s,
+        hipLaunchKernelGGL(embed_kernel<Q3X_HIP_MATRIX_Q4_0>, eg, dim3(256), 0, s,
                            static_cast<const uint8_t*>(e.embedding.w), c.H, e.d_tokens, e.d_step, e.hidden);
     int rc = launch_status();
     bool pending = false;  // an MoE output in `branch` still to be added to hidden
     for (int i = 0; i < c.N && rc == Q3X_HIP_OK; ++i) {
         const LayerWeights& L = e.layers[i];
-        hipLaunchKernelGGL(rms_kernel, dim3(1), dim3(kNormThreads), 0, s, e.hidden, pending ? e.branch : nullptr,
-                           L.input_norm, c.H, e.normalized);
+        hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden,
+                           pending ? e.branch : nullptr, L.input_norm, c.H, e.normalized);
         if (!L.attention) {
-            const q3x_hip_mv_item items[4] = {{L.qkv.w, L.qkv.rows, e.qkv, 0},
-                                              {L.z.w, L.z.rows, e.z, 0},
-                                              {L.a.w, L.a.rows, e.a, 0},
-                                              {L.b.w, L.b.rows, e.b, 0}};
-            rc = q3x_hip_mv_multi(items, 4, type, c.H, e.normalized, s);
+            const Mat m[4] = {L.qkv, L.z, L.a, L.b};
+            float* const y[4] = {e.qkv, e.z, e.a, e.b};
+            rc = apply_group(m, y, 4, type, c.H, e.normalized, count, s);
             if (rc) break;
             hipLaunchKernelGGL(delta_conv_kernel, dim3((DQKV + 255) / 256), dim3(256), 0, s, e.qkv, L.conv,
-                               L.conv_state, DQKV, c.CK);
-            hipLaunchKernelGGL(delta_rule_kernel, dim3(c.VH), dim3(kHeadThreads), 0, s, e.qkv, e.a, e.b, e.z,
-                               L.alog, L.dt, L.norm, L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD);
-            rc = q3x_hip_mv(L.out.w, type, L.out.rows, L.out.cols, e.delta_out, e.hidden, 1, s);
+                               L.conv_state, DQKV, c.CK, count);
+            hipLaunchKernelGGL(delta_rule_kernel, dim3(c.VH), dim3(kDeltaThreads), 0, s, e.qkv, e.a, e.b, e.z,
+                               L.alog, L.dt, L.norm, L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD, count);
+            rc = apply(L.out, type, e.delta_out, count, e.hidden, true, s);
         } else {
-            const q3x_hip_mv_item items[3] = {{L.q.w, L.q.rows, e.query_and_gate, 0},
-                                              {L.k.w, L.k.rows, e.key, 0},
-                                              {L.v.w, L.v.rows, e.value, 0}};
-            rc = q3x_hip_mv_multi(items, 3, type, c.H, e.normalized, s);
+            const Mat m[3] = {L.q, L.k, L.v};
+            float* const y[3] = {e.query_and_gate, e.key, e.value};
+            rc = apply_group(m, y, 3, type, c.H, e.normalized, count, s);
             if (rc) break;
-            hipLaunchKernelGGL(attention_prep_kernel, dim3(c.AH + c.KVH), dim3(kHeadThreads), 0, s,
+            hipLaunchKernelGGL(attention_prep_kernel, dim3(c.AH + c.KVH, count), dim3(kHeadThreads), 0, s,
                                e.query_and_gate, e.key, e.value, L.qnorm, L.knorm, e.d_position, e.query, e.gate,
                                L.key_cache, L.value_cache, c.AH, c.KVH, c.AD, c.RD);
-            hipLaunchKernelGGL(attention_kernel, dim3(c.AH), dim3(kHeadThreads), 0, s, e.query, e.gate,
-                               L.key_cache, L.value_cache, e.d_position, e.scores, e.attn_out, c.AH, c.KVH, c.AD,
-                               e.capacity);
-            rc = q3x_hip_mv(L.o.w, type, L.o.rows, L.o.cols, e.attn_out, e.hidden, 1, s);
+            const int splits = count == 1 ? kAttnSplits : 1;
+            hipLaunchKernelGGL(attention_kernel, dim3(c.AH * splits, count), dim3(kHeadThreads), 0, s, e.query,
+                               e.gate, L.key_cache, L.value_cache, e.d_position, e.scores, e.attn_out, c.AH, c.KVH,
+                               c.AD, splits);
+            if (splits > 1)
+                hipLaunchKernelGGL(attention_combine_kernel, dim3(c.AH, count), dim3(kHeadThreads), 0, s, e.scores,
+                                   e.gate, e.attn_out, c.AH, c.AD, splits);
+            rc = apply(L.o, type, e.attn_out, count, e.hidden, true, s);
         }
         if (rc) break;
-        hipLaunchKernelGGL(rms_kernel, dim3(1), dim3(kNormThreads), 0, s, e.hidden, nullptr, L.post_norm, c.H,
+        hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden, nullptr, L.post_norm, c.H,
                            e.normalized);
         if (c.experts) {
-            rc = q3x_hip_moe_layer(&L.moe, e.normalized, 1, e.branch, nullptr, nullptr, e.moe_ws, e.moe_ws_bytes,
-                                   s);
+            rc = q3x_hip_moe_layer(&L.moe, e.normalized, count, e.branch, nullptr, nullptr, e.moe_ws,
+                                   e.moe_ws_bytes, s);
             pending = true;
         } else {
-            const q3x_hip_mv_item items[2] = {{L.gate.w, L.gate.rows, e.ffn_gate, 0}, {L.up.w, L.up.rows, e.ffn_up, 0}};
-            rc = q3x_hip_mv_multi(items, 2, type, c.H, e.normalized, s);
+            const Mat m[2] = {L.gate, L.up};
+            float* const y[2] = {e.ffn_gate, e.ffn_up};
+            rc = apply_group(m, y, 2, type, c.H, e.normalized, count, s);
             if (rc) break;
-            hipLaunchKernelGGL(swiglu_kernel, dim3((c.I + 255) / 256), dim3(256), 0, s, e.ffn_gate, e.ffn_up, c.I);
-            rc = q3x_hip_mv(L.down.w, type, L.down.rows, L.down.cols, e.ffn_gate, e.hidden, 1, s);
+            const int n = count * c.I;
+            hipLaunchKernelGGL(swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, s, e.ffn_gate, e.ffn_up, n);
+            rc = apply(L.down, type, e.ffn_gate, count, e.hidden, true, s);
             pending = false;
         }
         if (rc == Q3X_HIP_OK) rc = launch_status();
     }
     if (rc) return rc;
     if (logits) {
-        hipLaunchKernelGGL(rms_kernel, dim3(1), dim3(kNormThreads), 0, s, e.hidden, pending ? e.branch : nullptr,
-                           e.final_norm, c.H, e.normalized);
+        // The last row only: its residual, final norm and lm_head.
+        const size_t last = static_cast<size_t>(count - 1) * c.H;
+        hipLaunchKernelGGL(rms_kernel, dim3(1), dim3(kNormThreads), 0, s, e.hidden + last,
+                           pending ? e.branch + last : nullptr, e.final_norm, c.H, e.normalized);
         rc = q3x_hip_mv(e.lm_head.w, type, e.lm_head.rows, e.lm_head.cols, e.normalized, e.logits, 0, s);
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, e.d_step, e.d_position);
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, e.d_step, e.d_position, count);
     return launch_status();
 }
 
 int capture(q3x_hip_engine& e, bool logits) {
     hipGraph_t g = nullptr;
     if (hipStreamBeginCapture(e.stream, hipStreamCaptureModeThreadLocal) != hipSuccess) return Q3X_HIP_ERUNTIME;
-    const int rc = enqueue_step(e, logits);
+    const int rc = enqueue(e, 1, logits);
     const hipError_t end = hipStreamEndCapture(e.stream, &g);
     if (rc != Q3X_HIP_OK || end != hipSuccess) {
         if (g) (void)hipGraphDestroy(g);
@@ -599,24 +757,66 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
     const size_t conv = static_cast<size_t>(DQKV) * (c.CK - 1);
     const size_t memory = static_cast<size_t>(c.VH) * c.KD * c.VD;
     const size_t cache = static_cast<size_t>(context) * KVW;
-    const int delta_layers = c.N - c.N / c.AI, attention_layers = c.N / c.AI;
+    const int delta_layers = c.N - c.N / c.AI;
     e->recurrent_floats = static_cast<size_t>(delta_layers) * (conv + memory);
-    if (c.experts) e->moe_ws_bytes = q3x_hip_moe_layer_workspace_bytes(&e->layers[0].moe, 1);
-    e->token_capacity = std::max(context, 1);
-    // Arena: work vectors, recurrent state and its checkpoint, KV cache, logits.
-    auto bytes = [](size_t n, size_t size) { return (n * size + 255) / 256 * 256; };
-    size_t total = 0;
-    const size_t work_floats[] = {static_cast<size_t>(c.H), static_cast<size_t>(c.H), static_cast<size_t>(c.H),
-                                  static_cast<size_t>(c.V), static_cast<size_t>(DQKV), static_cast<size_t>(DO),
-                                  static_cast<size_t>(c.VH), static_cast<size_t>(c.VH), static_cast<size_t>(DO),
-                                  2 * static_cast<size_t>(AS), static_cast<size_t>(AS), static_cast<size_t>(AS),
-                                  static_cast<size_t>(KVW), static_cast<size_t>(KVW), static_cast<size_t>(AS),
-                                  static_cast<size_t>(c.AH) * context, static_cast<size_t>(c.I),
-                                  static_cast<size_t>(c.I), e->recurrent_floats, e->recurrent_floats,
-                                  static_cast<size_t>(c.V)};
-    for (size_t n : work_floats) total += bytes(n, 4);
-    total += static_cast<size_t>(attention_layers) * 2 * bytes(cache, 4);
-    total += bytes(e->token_capacity, 4) + 3 * 256 + bytes(e->moe_ws_bytes, 1);
+    const size_t R = static_cast<size_t>(std::min(context, kChunk));  // rows of a chunk
+    if (c.experts)
+        e->moe_ws_bytes = std::max(q3x_hip_moe_layer_workspace_bytes(&e->layers[0].moe, 1),
+                                   q3x_hip_moe_layer_workspace_bytes(&e->layers[0].moe, static_cast<int>(R)));
+    e->token_capacity = context;
+    // One arena: the work rows of a chunk, the recurrent state and its
+    // checkpoint, the KV caches, the logits, the token list and counters.
+    // plan(base) carves it; plan(nullptr) only measures it.
+    auto plan = [&](uint8_t* base) -> size_t {
+        size_t at = 0;
+        auto take = [&](size_t n, size_t size) {
+            uint8_t* p = base ? base + at : nullptr;
+            at += (n * size + 255) / 256 * 256;
+            return p;
+        };
+        auto f = [&](size_t n) { return reinterpret_cast<float*>(take(n, 4)); };
+        e->hidden = f(R * c.H);
+        e->normalized = f(R * c.H);
+        e->branch = f(R * c.H);
+        e->logits = f(c.V);
+        e->qkv = f(R * DQKV);
+        e->z = f(R * DO);
+        e->a = f(R * c.VH);
+        e->b = f(R * c.VH);
+        e->delta_out = f(R * DO);
+        e->query_and_gate = f(R * 2 * AS);
+        e->query = f(R * AS);
+        e->gate = f(R * AS);
+        e->key = f(R * KVW);
+        e->value = f(R * KVW);
+        e->attn_out = f(R * AS);
+        e->scores = f(static_cast<size_t>(c.AH) * kAttnSplits * (c.AD + 2));
+        e->ffn_gate = f(R * c.I);
+        e->ffn_up = f(R * c.I);
+        e->recurrent = f(e->recurrent_floats);
+        e->checkpoint_recurrent = f(e->recurrent_floats);
+        e->checkpoint_logits = f(c.V);
+        float* rec = e->recurrent;
+        for (int i = 0; i < c.N; ++i) {
+            LayerWeights& L = e->layers[i];
+            if (!L.attention) {
+                L.conv_state = rec;
+                if (rec) rec += conv;
+                L.memory = rec;
+                if (rec) rec += memory;
+            } else {
+                L.key_cache = f(cache);
+                L.value_cache = f(cache);
+            }
+        }
+        e->d_tokens = reinterpret_cast<int*>(take(e->token_capacity, 4));
+        e->d_step = reinterpret_cast<int*>(take(1, 4));
+        e->d_position = reinterpret_cast<int*>(take(1, 4));
+        e->d_argmax = reinterpret_cast<int*>(take(1, 4));
+        e->moe_ws = e->moe_ws_bytes ? take(e->moe_ws_bytes, 1) : nullptr;
+        return at;
+    };
+    const size_t total = plan(nullptr);
     int rc = Q3X_HIP_OK;
     const hipError_t status = hipMalloc(&e->arena, total);
     if (status != hipSuccess) {
@@ -626,46 +826,7 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
         rc = Q3X_HIP_ERUNTIME;
     }
     if (rc == Q3X_HIP_OK) {
-        uint8_t* cur = static_cast<uint8_t*>(e->arena);
-        e->hidden = carve<float>(cur, c.H);
-        e->normalized = carve<float>(cur, c.H);
-        e->branch = carve<float>(cur, c.H);
-        e->logits = carve<float>(cur, c.V);
-        e->qkv = carve<float>(cur, DQKV);
-        e->z = carve<float>(cur, DO);
-        e->a = carve<float>(cur, c.VH);
-        e->b = carve<float>(cur, c.VH);
-        e->delta_out = carve<float>(cur, DO);
-        e->query_and_gate = carve<float>(cur, 2 * static_cast<size_t>(AS));
-        e->query = carve<float>(cur, AS);
-        e->gate = carve<float>(cur, AS);
-        e->key = carve<float>(cur, KVW);
-        e->value = carve<float>(cur, KVW);
-        e->attn_out = carve<float>(cur, AS);
-        e->scores = carve<float>(cur, static_cast<size_t>(c.AH) * context);
-        e->ffn_gate = carve<float>(cur, c.I);
-        e->ffn_up = carve<float>(cur, c.I);
-        e->recurrent = carve<float>(cur, e->recurrent_floats);
-        e->checkpoint_recurrent = carve<float>(cur, e->recurrent_floats);
-        e->checkpoint_logits = carve<float>(cur, c.V);
-        float* rec = e->recurrent;
-        for (int i = 0; i < c.N; ++i) {
-            LayerWeights& L = e->layers[i];
-            if (!L.attention) {
-                L.conv_state = rec;
-                rec += conv;
-                L.memory = rec;
-                rec += memory;
-            } else {
-                L.key_cache = carve<float>(cur, cache);
-                L.value_cache = carve<float>(cur, cache);
-            }
-        }
-        e->d_tokens = carve<int>(cur, e->token_capacity);
-        e->d_step = carve<int>(cur, 1);
-        e->d_position = carve<int>(cur, 1);
-        e->d_argmax = carve<int>(cur, 1);
-        e->moe_ws = e->moe_ws_bytes ? carve<uint8_t>(cur, e->moe_ws_bytes) : nullptr;
+        plan(static_cast<uint8_t*>(e->arena));
         if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
             hipHostMalloc(reinterpret_cast<void**>(&e->h_tokens), sizeof(int) * e->token_capacity,
                           hipHostMallocDefault) != hipSuccess ||
@@ -680,7 +841,7 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
     // then happens outside a capture.
     if (rc == Q3X_HIP_OK) {
         hipLaunchKernelGGL(set_counters_kernel, dim3(1), dim3(1), 0, e->stream, e->d_step, e->d_position, 0, 0);
-        rc = enqueue_step(*e, true);
+        rc = enqueue(*e, 1, true);
         if (rc == Q3X_HIP_OK && hipStreamSynchronize(e->stream) != hipSuccess) rc = Q3X_HIP_ERUNTIME;
         if (rc == Q3X_HIP_OK) rc = q3x_hip_engine_reset(e);
         if (rc != Q3X_HIP_OK) set_error(error, "HIP engine warm-up step failed");
@@ -716,14 +877,20 @@ extern "C" int q3x_hip_engine_forward(q3x_hip_engine* e, const int* tokens, int 
     if (hipMemcpyAsync(e->d_tokens, e->h_tokens, sizeof(int) * count, hipMemcpyHostToDevice, e->stream) !=
         hipSuccess)
         return Q3X_HIP_ERUNTIME;
-    for (int i = 0; i < count; ++i) {
-        const bool logits = compute_logits && i + 1 == count;
-        hipGraphExec_t& g = e->graph[logits ? 1 : 0];
+    if (count == 1) {
+        hipGraphExec_t& g = e->graph[compute_logits ? 1 : 0];
         if (!g) {
-            const int rc = capture(*e, logits);
+            const int rc = capture(*e, compute_logits != 0);
             if (rc) return rc;
         }
         if (hipGraphLaunch(g, e->stream) != hipSuccess) return Q3X_HIP_ERUNTIME;
+    } else {
+        for (int done = 0; done < count;) {
+            const int n = std::min(kChunk, count - done);
+            const int rc = enqueue(*e, n, compute_logits && done + n == count);
+            if (rc) return rc;
+            done += n;
+        }
     }
     if (hipStreamSynchronize(e->stream) != hipSuccess) return Q3X_HIP_ERUNTIME;
     e->position += count;

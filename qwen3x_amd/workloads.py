@@ -140,3 +140,68 @@ def moe_layer_weights(index: int = 4, device="cuda") -> q3x.MoeLayer:
 
 def router_logits(index: int, tokens: int, experts: int, device="cuda"):
     return normal((tokens, experts), (SEED_BASE + index) * 1000 + 700 + tokens, 1.0, device)
+
+
+# ------------------------------------------------------------ whole models
+
+MODEL_HEADER = "Q3XMODL\0".encode()
+
+
+def model_header(model_id: int, fields) -> bytes:
+    """The 72-byte model.bin header of a fixed model: magic + 16 uint32
+    fields (id, V, H, I, N, AI, AH, KVH, AD, RD, KH, VH, KD, VD, CK, 262144)."""
+    import struct
+    return struct.pack("<8s16I", MODEL_HEADER, *fields)
+
+
+def synthetic_model_weights(model_id: int, seed: int, device="cuda"):
+    """(ModelConfig, uint8 device tensor) of a full-size model whose weights
+    are drawn on the GPU in model.bin layout: matrices N(0, 1/sqrt(cols))
+    (the embedding N(0, 1)) quantised by q3x_hip_quantize, BF16 norm and conv
+    vectors N(0, 0.1)/N(0, 0.5), FP32 A_log -1 + N(0, 0.2) and norm
+    1 + N(0, 0.2), router and shared-expert gate N(0, 1/sqrt(H)).  The
+    header is written too, so the buffer is a valid model.bin image."""
+    torch = _torch()
+    sizes = {
+        9000: (248320, 4096, 12288, 32, 4, 16, 4, 256, 64, 16, 32, 128, 128, 4),
+        36035: (248320, 2048, 512, 40, 4, 16, 2, 256, 64, 16, 32, 128, 128, 4),
+        38027: (248320, 5120, 17408, 64, 4, 24, 4, 256, 64, 16, 48, 128, 128, 4),
+    }[model_id]
+    header = model_header(model_id, (model_id,) + sizes + (262144,))
+    # The file size: the schema of the configuration the header names.
+    probe = q3x.make_config(id=model_id, V=sizes[0], H=sizes[1], I=sizes[2], N=sizes[3], AI=sizes[4],
+                            AH=sizes[5], KVH=sizes[6], AD=sizes[7], RD=sizes[8], KH=sizes[9], VH=sizes[10],
+                            KD=sizes[11], VD=sizes[12], CK=sizes[13], experts=256 if model_id == 36035 else 0,
+                            top_k=8 if model_id == 36035 else 0, shared_I=512 if model_id == 36035 else 0,
+                            matrix_type=q3x.MATRIX_Q8_0 if model_id == 9000 else q3x.MATRIX_Q4_0)
+    _, nbytes = q3x.model_schema(probe)
+    config, tensors = q3x.model_layout(header, nbytes)
+    buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    buf[:len(header)] = torch.frombuffer(bytearray(header), dtype=torch.uint8).to(device)
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    H = config.H
+    chunk = 1 << 26  # elements per generated piece
+    for t in tensors:
+        role = q3x.TENSOR_ROLES[t.role]
+        out = buf[t.offset:t.offset + t.bytes]
+        rows = max(t.experts, 1) * t.rows
+        if t.type in (q3x.MATRIX_Q8_0, q3x.MATRIX_Q4_0):
+            std = 1.0 if role in ("embedding", "lm_head") else 1.0 / t.cols ** 0.5
+            row_bytes = t.bytes // rows
+            step = max(1, chunk // t.cols)
+            for r0 in range(0, rows, step):
+                n = min(step, rows - r0)
+                src = torch.randn((n, t.cols), generator=g, device=device, dtype=torch.float32).mul_(std)
+                q3x.quantize(t.type, src, n, t.cols, out[r0 * row_bytes:(r0 + n) * row_bytes])
+        elif t.type == q3x.TENSOR_F32:
+            base = -1.0 if role == "delta_alog" else 1.0
+            vals = torch.randn(rows * t.cols, generator=g, device=device, dtype=torch.float32).mul_(0.2).add_(base)
+            out.copy_(vals.view(torch.uint8))
+        else:
+            std = {"moe_router": H ** -0.5, "moe_shared_scale": H ** -0.5, "delta_conv": 0.5,
+                   "delta_dt": 0.5}.get(role, 0.1)
+            vals = torch.randn(rows * t.cols, generator=g, device=device, dtype=torch.float32).mul_(std)
+            out.copy_((vals.view(torch.int32) >> 16).to(torch.int16).view(torch.uint8))
+    torch.cuda.synchronize()
+    return config, buf
