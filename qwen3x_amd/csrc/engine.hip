@@ -261,6 +261,135 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_rule_kernel(
     }
 }
 
+// Prefill form of the delta rule, in three launches so that only the
+// recurrence itself runs token by token:
+//   delta_prep_kernel (row r, key head kh; parallel): q, k of the head
+//     L2-normalised in place (q also divided by sqrt(KD)); for the value
+//     heads of kh, b <- beta = sigmoid(b) and a <- exp(decay) in place;
+//   delta_scan_kernel (value head; sequential over the rows): the memory
+//     update of delta_rule_kernel, writing q S unnormalised;
+//   delta_norm_kernel (row, value head; parallel): the gated RMSNorm.
+// The arithmetic of each step is delta_rule_kernel's.
+constexpr int kScanTile = 32;  // rows of q / k staged in LDS at a time
+
+__global__ __launch_bounds__(128) void delta_prep_kernel(float* __restrict__ qkv, float* __restrict__ a,
+                                                         float* __restrict__ b, const float* __restrict__ alog,
+                                                         const uint16_t* __restrict__ dt, int KH, int VH, int KD,
+                                                         int VD) {
+    __shared__ float partial[128 / kWave];
+    const int kh = blockIdx.x, r = blockIdx.y;
+    const int t = threadIdx.x;
+    const int DQK = KH * KD, DQKV = 2 * DQK + VH * VD;
+    float* row = qkv + static_cast<size_t>(r) * DQKV;
+    const float qv = t < KD ? row[kh * KD + t] : 0.0f;
+    const float kv = t < KD ? row[DQK + kh * KD + t] : 0.0f;
+    const float qn = block_sum<128>(qv * qv, partial);
+    const float kn = block_sum<128>(kv * kv, partial);
+    if (t < KD) {
+        row[kh * KD + t] = qv * (1.0f / sqrtf(qn + kEps)) / sqrtf(static_cast<float>(KD));
+        row[DQK + kh * KD + t] = kv * (1.0f / sqrtf(kn + kEps));
+    }
+    const int per = VH / KH;
+    for (int u = t; u < per; u += 128) {
+        const int head = kh * per + u;
+        const size_t at = static_cast<size_t>(r) * VH + head;
+        b[at] = sigmoid_ref(b[at]);
+        a[at] = expf(-expf(alog[head]) * softplus_ref(a[at] + bf16_value(dt[head])));
+    }
+}
+
+__global__ __launch_bounds__(kDeltaThreads) void delta_scan_kernel(const float* __restrict__ qkv,
+                                                                   const float* __restrict__ scale,
+                                                                   const float* __restrict__ beta,
+                                                                   float* __restrict__ memory, float* __restrict__ out,
+                                                                   int KH, int VH, int KD, int VD, int count) {
+    __shared__ float qt[kScanTile][128], kt[kScanTile][128], st[kScanTile], bt[kScanTile];
+    __shared__ float pp[kDeltaGroups][128], po[kDeltaGroups][128];
+    const int head = blockIdx.x;
+    const int t = threadIdx.x;
+    const int DQK = KH * KD, DO = VH * VD, DQKV = 2 * DQK + DO;
+    const int kh = head / (VH / KH);
+    const int v = t & 127, group = t >> 7;
+    const bool col = v < VD;
+    float* S = memory + static_cast<size_t>(head) * KD * VD;
+    float s[kDeltaKeys];
+#pragma unroll
+    for (int j = 0; j < kDeltaKeys; ++j) {
+        const int key = group * kDeltaKeys + j;
+        s[j] = col && key < KD ? S[static_cast<size_t>(key) * VD + v] : 0.0f;
+    }
+    for (int r0 = 0; r0 < count; r0 += kScanTile) {
+        const int nt = min(kScanTile, count - r0);
+        __syncthreads();  // the previous tile is consumed
+        for (int e = t; e < nt * 128; e += kDeltaThreads) {
+            const int rr = e / 128, k = e % 128;
+            const float* row = qkv + static_cast<size_t>(r0 + rr) * DQKV;
+            qt[rr][k] = k < KD ? row[kh * KD + k] : 0.0f;
+            kt[rr][k] = k < KD ? row[DQK + kh * KD + k] : 0.0f;
+        }
+        if (t < nt) {
+            st[t] = scale[static_cast<size_t>(r0 + t) * VH + head];
+            bt[t] = beta[static_cast<size_t>(r0 + t) * VH + head];
+        }
+        __syncthreads();
+        float vnext = col ? qkv[static_cast<size_t>(r0) * DQKV + 2 * DQK + head * VD + v] : 0.0f;
+        for (int rr = 0; rr < nt; ++rr) {
+            const float vv = vnext;
+            if (rr + 1 < nt && col) vnext = qkv[static_cast<size_t>(r0 + rr + 1) * DQKV + 2 * DQK + head * VD + v];
+            const float sc = st[rr], bb = bt[rr];
+            float pred = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kDeltaKeys; ++j) {
+                const int key = group * kDeltaKeys + j;
+                s[j] *= sc;
+                if (key < KD) pred = fmaf(kt[rr][key], s[j], pred);
+            }
+            pp[group][v] = pred;
+            __syncthreads();
+            float sum = pp[0][v];
+#pragma unroll
+            for (int g = 1; g < kDeltaGroups; ++g) sum += pp[g][v];
+            const float delta = vv - sum;
+            float o = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kDeltaKeys; ++j) {
+                const int key = group * kDeltaKeys + j;
+                if (key < KD) {
+                    s[j] = fmaf(kt[rr][key] * bb, delta, s[j]);
+                    o = fmaf(qt[rr][key], s[j], o);
+                }
+            }
+            po[group][v] = o;
+            __syncthreads();
+            if (t < VD) {
+                float result = po[0][t];
+#pragma unroll
+                for (int g = 1; g < kDeltaGroups; ++g) result += po[g][t];
+                out[static_cast<size_t>(r0 + rr) * DO + head * VD + t] = result;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kDeltaKeys; ++j) {
+        const int key = group * kDeltaKeys + j;
+        if (col && key < KD) S[static_cast<size_t>(key) * VD + v] = s[j];
+    }
+}
+
+__global__ __launch_bounds__(128) void delta_norm_kernel(float* __restrict__ out, const float* __restrict__ z,
+                                                         const float* __restrict__ norm, int VH, int VD) {
+    __shared__ float partial[128 / kWave];
+    const int head = blockIdx.x, r = blockIdx.y;
+    const int t = threadIdx.x;
+    const size_t at = static_cast<size_t>(r) * VH * VD + head * VD + t;
+    const float x = t < VD ? out[at] : 0.0f;
+    const float sq = block_sum<128>(x * x, partial);
+    if (t < VD) {
+        const float g = 1.0f / sqrtf(sq / static_cast<float>(VD) + kEps);
+        out[at] = x * (g * norm[t] * silu_ref(z[at]));
+    }
+}
+
 // RMSNorm (1 + w) and rotary embedding of one AD-wide head at `position`
 // (engine.cpp:228-233, 243-250), in place in `x` (shared memory).
 __device__ void norm_rope(float* x, const uint16_t* w, int AD, int RD, int position, float* partial) {
@@ -320,108 +449,176 @@ __global__ __launch_bounds__(kHeadThreads) void attention_prep_kernel(
     }
 }
 
-// Attention of query row r = blockIdx.y, head blockIdx.x / splits, over the
-// positions 0 .. *position + r (causal; engine.cpp:344-361: scores q . k /
-// sqrt(AD), softmax, sum of weights times v), with the softmax taken online
-// over blocks of 64 positions (a running maximum rescales the running sum
-// and accumulator), so no score buffer bounds the context.  With splits > 1
-// each workgroup takes one of `splits` position ranges and leaves its range's
-// maximum, sum and accumulator in `partial` for attention_combine_kernel;
-// with splits == 1 it writes the gated output.  AD <= 256.
-constexpr int kAttnSplits = 32;  // ranges per head for a decode step
-constexpr int kChunk = 512;      // rows of a prefill chunk
+// Attention of query row r = blockIdx.y for the G = AH / KVH query heads
+// that share KV head blockIdx.x / splits (engine.cpp:344-361: scores q . k /
+// sqrt(AD), softmax, sum of weights times v), over positions 0 .. *position
+// + r (causal).  Each K and V row is loaded once for all G heads.  The
+// softmax is taken online over blocks of 64 positions (a running maximum
+// rescales the running sum and accumulator), so no score buffer bounds the
+// context.  With splits > 1 each workgroup takes one of `splits` position
+// ranges and leaves each head's range maximum, sum and accumulator in
+// `partial` for attention_combine_kernel; with splits == 1 it writes the
+// gated output.  AD <= 256, G <= kMaxGroup.
+constexpr int kAttnSplits = 32;  // ranges per KV head for a decode step
 constexpr int kAttnBlock = 64;
+constexpr int kMaxGroup = 8;
+constexpr int kChunk = 512;      // rows of a prefill chunk
 
 __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
     const float* __restrict__ query, const float* __restrict__ gate, const float* __restrict__ key_cache,
     const float* __restrict__ value_cache, const int* __restrict__ position, float* __restrict__ partial,
     float* __restrict__ out, int AH, int KVH, int AD, int splits) {
-    __shared__ float sc[kAttnBlock], pw[kAttnBlock];
-    const int head = blockIdx.x / splits, split = blockIdx.x % splits;
+    __shared__ float sc[kMaxGroup][kAttnBlock], pw[kMaxGroup][kAttnBlock];
+    const int kv = blockIdx.x / splits, split = blockIdx.x % splits;
     const int r = blockIdx.y;
-    const int kv = head / (AH / KVH);
+    const int G = AH / KVH;
     const int AS = AH * AD;
     const int n = *position + r + 1;
     const int per = (n + splits - 1) / splits;
     const int t0 = min(n, split * per), t1 = min(n, t0 + per);
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int i = threadIdx.x;
-    const float* q = query + static_cast<size_t>(r) * AS + head * AD;
+    const size_t KVW = static_cast<size_t>(KVH) * AD;
+    const float* kbase = key_cache + static_cast<size_t>(kv) * AD;
+    const float* vbase = value_cache + static_cast<size_t>(kv) * AD;
     const float divisor = sqrtf(static_cast<float>(AD));
-    float qr[4];
+    float qr[kMaxGroup][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qr[j] = lane + 64 * j < AD ? q[lane + 64 * j] : 0.0f;
-    float m = -INFINITY, l = 0.0f, acc = 0.0f;
+    for (int g = 0; g < kMaxGroup; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            qr[g][e] = g < G && lane + 64 * e < AD
+                           ? query[static_cast<size_t>(r) * AS + (kv * G + g) * AD + lane + 64 * e]
+                           : 0.0f;
+    float m[kMaxGroup], l[kMaxGroup], acc[kMaxGroup], alpha[kMaxGroup];
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+        acc[g] = 0.0f;
+    }
     for (int b0 = t0; b0 < t1; b0 += kAttnBlock) {
         const int nb = min(kAttnBlock, t1 - b0);
-        for (int j = wave; j < nb; j += kHeadThreads / kWave) {
-            const float* k = key_cache + (static_cast<size_t>(b0 + j) * KVH + kv) * AD;
-            float d = 0.0f;
+        // Scores: each wave takes positions wave, wave + 4, ..., two at a
+        // time, the K rows requested together, every head's dot from them.
+        for (int j0 = 2 * wave; j0 < nb; j0 += 2 * (kHeadThreads / kWave)) {
+            float kr[2][4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (lane + 64 * u < AD) d = fmaf(qr[u], k[lane + 64 * u], d);
-            d = wave_sum_f32(d);
-            if (lane == 0) sc[j] = d / divisor;
+            for (int u = 0; u < 2; ++u) {
+                const float* k = kbase + static_cast<size_t>(b0 + min(j0 + u, nb - 1)) * KVW;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) kr[u][e] = lane + 64 * e < AD ? k[lane + 64 * e] : 0.0f;
+            }
+#pragma unroll
+            for (int g = 0; g < kMaxGroup; ++g) {
+                if (g < G) {
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        float x = 0.0f;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) x = fmaf(qr[g][e], kr[u][e], x);
+                        x = wave_sum_f32(x);
+                        if (lane == 0 && j0 + u < nb) sc[g][j0 + u] = x / divisor;
+                    }
+                }
+            }
         }
         __syncthreads();
-        float bm = sc[0];
-        for (int j = 1; j < nb; ++j) bm = fmaxf(bm, sc[j]);
-        const float mn = fmaxf(m, bm);
-        if (i < nb) pw[i] = expf(sc[i] - mn);
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) {
+            if (g < G) {
+                float bm = sc[g][0];
+                for (int j = 1; j < nb; ++j) bm = fmaxf(bm, sc[g][j]);
+                const float mn = fmaxf(m[g], bm);
+                if (i < nb) pw[g][i] = expf(sc[g][i] - mn);
+                alpha[g] = expf(m[g] - mn);  // 0 for the first block (m = -inf)
+                m[g] = mn;
+            }
+        }
         __syncthreads();
-        const float alpha = expf(m - mn);  // 0 for the first block (m = -inf)
-        float ps = 0.0f;
-        for (int j = 0; j < nb; ++j) ps += pw[j];
-        l = l * alpha + ps;
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) {
+            if (g < G) {
+                float ps = 0.0f;
+                for (int j = 0; j < nb; ++j) ps += pw[g][j];
+                l[g] = l[g] * alpha[g] + ps;
+                acc[g] *= alpha[g];
+            }
+        }
         if (i < AD) {
-            float a = acc * alpha;
-            for (int j = 0; j < nb; ++j)
-                a = fmaf(pw[j], value_cache[(static_cast<size_t>(b0 + j) * KVH + kv) * AD + i], a);
-            acc = a;
+            // Eight positions' values requested together, then accumulated
+            // in position order for every head.
+            const float* vp = vbase + static_cast<size_t>(b0) * KVW + i;
+            int j = 0;
+            for (; j + 8 <= nb; j += 8) {
+                float vv[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) vv[u] = vp[static_cast<size_t>(j + u) * KVW];
+#pragma unroll
+                for (int g = 0; g < kMaxGroup; ++g)
+                    if (g < G)
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) acc[g] = fmaf(pw[g][j + u], vv[u], acc[g]);
+            }
+            for (; j < nb; ++j) {
+                const float vv = vp[static_cast<size_t>(j) * KVW];
+#pragma unroll
+                for (int g = 0; g < kMaxGroup; ++g)
+                    if (g < G) acc[g] = fmaf(pw[g][j], vv, acc[g]);
+            }
         }
-        m = mn;
         __syncthreads();  // sc / pw are rewritten by the next block
     }
-    if (splits == 1) {
-        if (i < AD) {
-            const size_t at = static_cast<size_t>(r) * AS + head * AD + i;
-            out[at] = acc / l * sigmoid_ref(gate[at]);
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+        if (g >= G) continue;
+        const int head = kv * G + g;
+        if (splits == 1) {
+            if (i < AD) {
+                const size_t at = static_cast<size_t>(r) * AS + head * AD + i;
+                out[at] = acc[g] / l[g] * sigmoid_ref(gate[at]);
+            }
+        } else {
+            float* p = partial + ((static_cast<size_t>(r) * AH + head) * splits + split) * (AD + 2);
+            if (i < AD) p[i] = acc[g];
+            if (i == 0) {
+                p[AD] = m[g];
+                p[AD + 1] = l[g];
+            }
         }
-        return;
-    }
-    float* p = partial + ((static_cast<size_t>(r) * AH + head) * splits + split) * (AD + 2);
-    if (i < AD) p[i] = acc;
-    if (i == 0) {
-        p[AD] = m;
-        p[AD + 1] = l;
     }
 }
 
 // out = (sum_s exp(m_s - M) acc_s) / (sum_s exp(m_s - M) l_s) * sigmoid(gate)
-// over the ranges s of one head of row r = blockIdx.y, M their largest
-// maximum (empty ranges have m = -inf and contribute nothing).
+// over the kAttnSplits ranges s of head blockIdx.x of row r = blockIdx.y, M
+// their largest maximum (empty ranges have m = -inf and weight 0).
 __global__ __launch_bounds__(kHeadThreads) void attention_combine_kernel(const float* __restrict__ partial,
                                                                          const float* __restrict__ gate,
-                                                                         float* __restrict__ out, int AH, int AD,
-                                                                         int splits) {
+                                                                         float* __restrict__ out, int AH, int AD) {
+    __shared__ float w[kAttnSplits];
+    __shared__ float total;
     const int head = blockIdx.x, r = blockIdx.y;
-    const float* p = partial + (static_cast<size_t>(r) * AH + head) * splits * (AD + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < splits; ++s) M = fmaxf(M, p[s * (AD + 2) + AD]);
-    float L = 0.0f;
-    for (int s = 0; s < splits; ++s) {
-        const float m = p[s * (AD + 2) + AD];
-        if (m != -INFINITY) L += expf(m - M) * p[s * (AD + 2) + AD + 1];
+    const float* p = partial + (static_cast<size_t>(r) * AH + head) * kAttnSplits * (AD + 2);
+    if (threadIdx.x < kWave) {  // wave 0, every lane active
+        const int s = threadIdx.x;
+        const float m = s < kAttnSplits ? p[s * (AD + 2) + AD] : -INFINITY;
+        const float M = wave_max_f32(m);
+        const float ws = m != -INFINITY ? expf(m - M) : 0.0f;
+        if (s < kAttnSplits) w[s] = ws;
+        const float L = wave_sum_f32(s < kAttnSplits ? ws * p[s * (AD + 2) + AD + 1] : 0.0f);
+        if (s == 0) total = L;
     }
+    __syncthreads();
     const int AS = AH * AD;
     for (int i = threadIdx.x; i < AD; i += kHeadThreads) {
+        float v[kAttnSplits];
+#pragma unroll
+        for (int s = 0; s < kAttnSplits; ++s) v[s] = p[s * (AD + 2) + i];
         float acc = 0.0f;
-        for (int s = 0; s < splits; ++s) {
-            const float m = p[s * (AD + 2) + AD];
-            if (m != -INFINITY) acc = fmaf(expf(m - M), p[s * (AD + 2) + i], acc);
-        }
+#pragma unroll
+        for (int s = 0; s < kAttnSplits; ++s) acc = fmaf(w[s], v[s], acc);
         const size_t at = static_cast<size_t>(r) * AS + head * AD + i;
-        out[at] = acc / L * sigmoid_ref(gate[at]);
+        out[at] = acc / total * sigmoid_ref(gate[at]);
     }
 }
 
@@ -501,6 +698,7 @@ struct LayerWeights {
 bool engine_config_ok(const q3x_hip_model_config& c, int context) {
     return (c.matrix_type == Q3X_HIP_MATRIX_Q8_0 || c.matrix_type == Q3X_HIP_MATRIX_Q4_0) && c.KD <= 128 &&
            c.VD <= 128 && c.AD <= 256 && c.RD <= 64 && c.RD % 2 == 0 && c.RD <= c.AD && c.CK >= 2 && c.CK <= 8 &&
+           c.AH / c.KVH <= kMaxGroup &&
            c.top_k <= 8 && context >= 1 && context <= 262144;
 }
 
@@ -593,8 +791,17 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
             if (rc) break;
             hipLaunchKernelGGL(delta_conv_kernel, dim3((DQKV + 255) / 256), dim3(256), 0, s, e.qkv, L.conv,
                                L.conv_state, DQKV, c.CK, count);
-            hipLaunchKernelGGL(delta_rule_kernel, dim3(c.VH), dim3(kDeltaThreads), 0, s, e.qkv, e.a, e.b, e.z,
-                               L.alog, L.dt, L.norm, L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD, count);
+            if (count == 1) {
+                hipLaunchKernelGGL(delta_rule_kernel, dim3(c.VH), dim3(kDeltaThreads), 0, s, e.qkv, e.a, e.b, e.z,
+                                   L.alog, L.dt, L.norm, L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD, 1);
+            } else {
+                hipLaunchKernelGGL(delta_prep_kernel, dim3(c.KH, count), dim3(128), 0, s, e.qkv, e.a, e.b, L.alog,
+                                   L.dt, c.KH, c.VH, c.KD, c.VD);
+                hipLaunchKernelGGL(delta_scan_kernel, dim3(c.VH), dim3(kDeltaThreads), 0, s, e.qkv, e.a, e.b,
+                                   L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD, count);
+                hipLaunchKernelGGL(delta_norm_kernel, dim3(c.VH, count), dim3(128), 0, s, e.delta_out, e.z, L.norm,
+                                   c.VH, c.VD);
+            }
             rc = apply(L.out, type, e.delta_out, count, e.hidden, true, s);
         } else {
             const Mat m[3] = {L.q, L.k, L.v};
@@ -605,12 +812,12 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                                e.query_and_gate, e.key, e.value, L.qnorm, L.knorm, e.d_position, e.query, e.gate,
                                L.key_cache, L.value_cache, c.AH, c.KVH, c.AD, c.RD);
             const int splits = count == 1 ? kAttnSplits : 1;
-            hipLaunchKernelGGL(attention_kernel, dim3(c.AH * splits, count), dim3(kHeadThreads), 0, s, e.query,
+            hipLaunchKernelGGL(attention_kernel, dim3(c.KVH * splits, count), dim3(kHeadThreads), 0, s, e.query,
                                e.gate, L.key_cache, L.value_cache, e.d_position, e.scores, e.attn_out, c.AH, c.KVH,
                                c.AD, splits);
             if (splits > 1)
                 hipLaunchKernelGGL(attention_combine_kernel, dim3(c.AH, count), dim3(kHeadThreads), 0, s, e.scores,
-                                   e.gate, e.attn_out, c.AH, c.AD, splits);
+                                   e.gate, e.attn_out, c.AH, c.AD);
             rc = apply(L.o, type, e.attn_out, count, e.hidden, true, s);
         }
         if (rc) break;

@@ -22,6 +22,8 @@ CONFIGS = {
     "moe_q4": dict(BASE, id=3, matrix_type=Q4_0, I=64, experts=8, top_k=2, shared_I=64),
     # tied embeddings, Q8_0 MoE, a shared expert narrower than the routed ones
     "moe_q8_tied": dict(BASE, id=4, matrix_type=Q8_0, I=128, experts=8, top_k=3, shared_I=64, tied_embeddings=1),
+    # eight query heads per KV head (the 35B-A3B's grouping) and four value heads per key head
+    "gqa8_q8": dict(BASE, id=5, matrix_type=Q8_0, AH=8, KVH=1, KH=1, VH=4),
 }
 
 

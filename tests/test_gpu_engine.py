@@ -47,7 +47,7 @@ def test_engine_logits_match_the_reference_forward(name):
 
 
 @pytest.mark.parametrize("name,prompt", [("dense_q8", 40), ("dense_q4", 530), ("moe_q4", 300),
-                                         ("moe_q8_tied", 64)])
+                                         ("moe_q8_tied", 64), ("gqa8_q8", 100)])
 def test_prefill_then_decode_match_the_reference_forward(name, prompt):
     # A forward of many tokens runs them as prefill chunks of up to 512 rows
     # (GEMMs, the recurrences token by token inside one launch); its logits,
