@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the lm_head kernel (--steps launches) and a same-size copy, for counter runs")
     ap.add_argument("--only", default="",
-                    help="comma list of configs (cfg0,cfg2,cfg3,cfg4) to run alone, for counter runs")
+                    help="comma list of configs (cfg0,cfg2,cfg3,cfg4,engine) to run alone, for counter runs")
     return ap.parse_args()
 
 
@@ -382,6 +382,41 @@ def extra_configs(torch, q3x, wl, only=None):
                     "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
             del X, Y, wsl
         del layer
+    if want("engine"):
+        out.update(engine_runs(torch, q3x, wl))
+    return out
+
+
+def engine_runs(torch, q3x, wl, prompt=4096, decode=32):
+    """The decode engine on full-size models with synthetic weights, in the
+    shape of the reference's own benchmark (`--bench 4096 32`: prefill a
+    4096-token prompt, then decode 32 tokens one call each, as in
+    eval/q8-9b.md:80).  Weights are drawn and quantised on the GPU; the
+    tokens are random ids."""
+    import numpy as np
+    out = {}
+    for model_id, name in ((9000, "9b_q8_0"), (36035, "35b_a3b_q4_0"), (38027, "27b_q4_0")):
+        config, buf = wl.synthetic_model_weights(model_id, wl.SEED_BASE + model_id)
+        engine = q3x.Engine(config, buf, context=prompt + decode + 8)
+        tokens = np.random.default_rng(model_id).integers(0, config.V, prompt + decode).astype(np.int32)
+        engine.forward(tokens[:8])
+        engine.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        engine.forward(tokens[:prompt])
+        t_prefill = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for i in range(prompt, prompt + decode):
+            engine.forward(tokens[i:i + 1])
+        t_decode = time.perf_counter() - t0
+        out[f"engine_{name}_prefill{prompt}_decode{decode}"] = {
+            "prefill_tok_s": prompt / t_prefill, "decode_tok_s": decode / t_decode,
+            "decode_ms_per_token": t_decode / decode * 1e3, "model_bytes": buf.numel(),
+            "note": "whole-model forward (engine), synthetic full-size weights; decode at 4K context, "
+                    "logits every token; host wall clock around each forward call"}
+        engine.close()
+        del buf, engine
+        torch.cuda.empty_cache()
     return out
 
 

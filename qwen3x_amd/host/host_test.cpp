@@ -21,6 +21,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include "backend.h"
 #include "hip_ops.h"
 
 namespace {
@@ -499,6 +500,44 @@ void loader_test_q4_35b() {
     CHECK(unlink(path) == 0);
 }
 
+// The backend operations (internal.h:11-34) on a sparse full-size 9B file:
+// all-zero weights give all-zero logits, so argmax is 0; the life cycle,
+// checkpoints and constants follow the reference's backends.
+void backend_test() {
+    const uint32_t fields[16] = {9000, 248320, 4096, 12288, 32, 4, 16, 4, 256, 64, 16, 32, 128, 128, 4, 262144};
+    const auto header = model_header(fields);
+    char path[] = "/tmp/q3x-hip-backend-XXXXXX";
+    const int fd = mkstemp(path);
+    CHECK(fd >= 0);
+    CHECK(ftruncate(fd, static_cast<off_t>(9514418816ULL)) == 0);
+    pwrite_exact(fd, header.data(), header.size(), 0);
+    char err[128] = "x";
+    CHECK(q3x_backend::model_create("/nonexistent/model.bin", err, sizeof(err)) == nullptr);
+    CHECK(std::strstr(err, "cannot open model.bin") != nullptr);
+    q3x_backend::Model* model = q3x_backend::model_create(path, err, sizeof(err));
+    CHECK(model != nullptr && err[0] == '\0');
+    CHECK(q3x_backend::model_id(model) == 9000);
+    q3x_backend::State* state = q3x_backend::state_create(model, 16);
+    const int tokens[3] = {1, 248043, 7};
+    q3x_backend::state_forward(model, state, tokens, 3, true);
+    std::vector<float> logits(248320, 1.0f);
+    q3x_backend::state_copy_logits(state, logits.data());
+    for (float v : logits) CHECK(v == 0.0f);
+    CHECK(q3x_backend::state_argmax(state) == 0);
+    q3x_backend::state_checkpoint_save(state);
+    q3x_backend::state_forward(model, state, tokens, 1, true);
+    q3x_backend::state_checkpoint_restore(state);
+    q3x_backend::state_reset(state);
+    q3x_backend::state_forward(model, state, tokens + 2, 1, false);
+    CHECK(q3x_backend::vocab_size() == 248320 && q3x_backend::max_context() == 262144);
+    CHECK(q3x_backend::token_is_stop(248044) && q3x_backend::token_is_stop(248046) &&
+          !q3x_backend::token_is_stop(248045));
+    q3x_backend::state_destroy(state);
+    q3x_backend::model_destroy(model);
+    close(fd);
+    CHECK(unlink(path) == 0);
+}
+
 }  // namespace
 
 int main() {
@@ -515,6 +554,7 @@ int main() {
     moe_layer_test();
     loader_test_q8_9b();
     loader_test_q4_35b();
+    backend_test();
     HIP_OK(hipDeviceSynchronize());
     std::puts("q3x-hip-host-test: ok");
     return 0;
