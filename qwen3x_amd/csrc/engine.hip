@@ -138,9 +138,19 @@ __global__ __launch_bounds__(256) void delta_conv_kernel(float* __restrict__ qkv
     for (int i = 0; i < kMaxConv - 1; ++i) past[i] = i < CK - 1 ? hist[i] : 0.0f;
 #pragma unroll
     for (int i = 0; i < kMaxConv; ++i) wt[i] = i < CK ? bf16_value(wc[i]) : 0.0f;
+    constexpr int kAhead = 8;  // tokens whose inputs are requested together
+    float xs[kAhead];
     for (int t = 0; t < count; ++t) {
         float* xp = qkv + static_cast<size_t>(t) * channels + c;
-        const float x = *xp;
+        if (t % kAhead == 0) {
+#pragma unroll
+            for (int u = 0; u < kAhead; ++u)
+                xs[u] = t + u < count ? qkv[static_cast<size_t>(t + u) * channels + c] : 0.0f;
+        }
+        float x = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u)
+            if (u == t % kAhead) x = xs[u];
         float last = 0.0f;
 #pragma unroll
         for (int i = 0; i < kMaxConv; ++i)
@@ -459,7 +469,7 @@ __global__ __launch_bounds__(kHeadThreads) void attention_prep_kernel(
 // ranges and leaves each head's range maximum, sum and accumulator in
 // `partial` for attention_combine_kernel; with splits == 1 it writes the
 // gated output.  AD <= 256, G <= kMaxGroup.
-constexpr int kAttnSplits = 32;  // ranges per KV head for a decode step
+constexpr int kAttnSplits = 128;  // ranges per KV head for a decode step
 constexpr int kAttnBlock = 64;
 constexpr int kMaxGroup = 8;
 constexpr int kChunk = 512;      // rows of a prefill chunk
@@ -595,28 +605,30 @@ __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
 __global__ __launch_bounds__(kHeadThreads) void attention_combine_kernel(const float* __restrict__ partial,
                                                                          const float* __restrict__ gate,
                                                                          float* __restrict__ out, int AH, int AD) {
-    __shared__ float w[kAttnSplits];
+    static_assert(kAttnSplits % kWave == 0, "ranges in whole waves");
+    __shared__ float w[kAttnSplits], red[kHeadThreads / kWave];
     __shared__ float total;
     const int head = blockIdx.x, r = blockIdx.y;
     const float* p = partial + (static_cast<size_t>(r) * AH + head) * kAttnSplits * (AD + 2);
-    if (threadIdx.x < kWave) {  // wave 0, every lane active
-        const int s = threadIdx.x;
-        const float m = s < kAttnSplits ? p[s * (AD + 2) + AD] : -INFINITY;
-        const float M = wave_max_f32(m);
-        const float ws = m != -INFINITY ? expf(m - M) : 0.0f;
-        if (s < kAttnSplits) w[s] = ws;
-        const float L = wave_sum_f32(s < kAttnSplits ? ws * p[s * (AD + 2) + AD + 1] : 0.0f);
-        if (s == 0) total = L;
-    }
+    const int t = threadIdx.x;
+    // Range weights: the maximum over all ranges, then exp(m_s - M).
+    const float m = t < kAttnSplits ? p[t * (AD + 2) + AD] : -INFINITY;
+    const float M = block_max<kHeadThreads>(m, red);
+    const float ws = t < kAttnSplits && m != -INFINITY ? expf(m - M) : 0.0f;
+    if (t < kAttnSplits) w[t] = ws;
+    const float L = block_sum<kHeadThreads>(t < kAttnSplits ? ws * p[t * (AD + 2) + AD + 1] : 0.0f, red);
+    if (t == 0) total = L;
     __syncthreads();
     const int AS = AH * AD;
-    for (int i = threadIdx.x; i < AD; i += kHeadThreads) {
-        float v[kAttnSplits];
-#pragma unroll
-        for (int s = 0; s < kAttnSplits; ++s) v[s] = p[s * (AD + 2) + i];
+    for (int i = t; i < AD; i += kHeadThreads) {
         float acc = 0.0f;
+        for (int s0 = 0; s0 < kAttnSplits; s0 += 32) {
+            float v[32];
 #pragma unroll
-        for (int s = 0; s < kAttnSplits; ++s) acc = fmaf(w[s], v[s], acc);
+            for (int s = 0; s < 32; ++s) v[s] = p[(s0 + s) * (AD + 2) + i];
+#pragma unroll
+            for (int s = 0; s < 32; ++s) acc = fmaf(w[s0 + s], v[s], acc);
+        }
         const size_t at = static_cast<size_t>(r) * AS + head * AD + i;
         out[at] = acc / total * sigmoid_ref(gate[at]);
     }
