@@ -320,11 +320,14 @@ typedef struct q3x_hip_engine q3x_hip_engine;
 
 /* An engine over `weights`, a device buffer laid out as q3x_hip_model_schema
  * gives for `config` (the buffer of q3x_hip_model_load qualifies), with room
- * for `context` tokens (1 .. 262144).  Needs a Q8_0 or Q4_0 model with KD,
- * VD <= 128, AD <= 256, RD <= min(64, AD) even, 2 <= CK <= 8, top_k <= 8, AH / KVH <= 8
- * (BF16 models: Q3X_HIP_ENOTSUP, as the matmul entry points).  The weights
- * must outlive the engine.  *error names the cause of a failure. */
-int q3x_hip_engine_create(const q3x_hip_model_config* config, const void* weights, int context,
+ * for `context` tokens (1 .. 262144).  A forward of several tokens runs as
+ * prefill chunks of `chunk` rows (0: 2048; at most `context`), whose work
+ * buffers the engine holds.  Needs a Q8_0 or Q4_0 model with KD, VD <= 128,
+ * AD <= 256 a multiple of 32, RD <= min(64, AD) even, 2 <= CK <= 8,
+ * top_k <= 8, AH / KVH <= 8 (BF16 models: Q3X_HIP_ENOTSUP, as the matmul
+ * entry points).  The weights must outlive the engine.  *error names the
+ * cause of a failure. */
+int q3x_hip_engine_create(const q3x_hip_model_config* config, const void* weights, int context, int chunk,
                           q3x_hip_engine** engine, const char** error);
 void q3x_hip_engine_destroy(q3x_hip_engine* engine);
 

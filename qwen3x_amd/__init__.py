@@ -67,7 +67,7 @@ SIGNATURES = {
     "q3x_hip_model_tensor": (_I, [_P, _U, _I, _P, ctypes.POINTER(_P)]),
     "q3x_hip_model_moe_layer": (_I, [_P, _I, _P]),
     "q3x_hip_model_schema": (_I, [_P, _P, _S, ctypes.POINTER(_S), ctypes.POINTER(ctypes.c_uint64)]),
-    "q3x_hip_engine_create": (_I, [_P, _P, _I, ctypes.POINTER(_P), ctypes.POINTER(ctypes.c_char_p)]),
+    "q3x_hip_engine_create": (_I, [_P, _P, _I, _I, ctypes.POINTER(_P), ctypes.POINTER(ctypes.c_char_p)]),
     "q3x_hip_engine_destroy": (None, [_P]),
     "q3x_hip_engine_reset": (_I, [_P]),
     "q3x_hip_engine_forward": (_I, [_P, _P, _I, _I]),
@@ -501,20 +501,20 @@ class Engine:
     tokens.  Mirrors the reference backend's state_* operations
     (internal.h:11-34)."""
 
-    def __init__(self, config: ModelConfig, weights, context: int):
+    def __init__(self, config: ModelConfig, weights, context: int, chunk: int = 0):
         self.config = config
         self._weights = weights  # keeps the buffer alive
         handle = ctypes.c_void_p()
         error = ctypes.c_char_p()
         ptr = weights if isinstance(weights, int) else _ptr(weights)
         _check_model("q3x_hip_engine_create",
-                     lib().q3x_hip_engine_create(ctypes.byref(config), ptr, context, ctypes.byref(handle),
+                     lib().q3x_hip_engine_create(ctypes.byref(config), ptr, context, chunk, ctypes.byref(handle),
                                                  ctypes.byref(error)), error)
         self.handle = handle
 
     @classmethod
-    def from_model(cls, model: "Model", context: int) -> "Engine":
-        return cls(model.config, DeviceRegion(model, model.base, model.nbytes), context)
+    def from_model(cls, model: "Model", context: int, chunk: int = 0) -> "Engine":
+        return cls(model.config, DeviceRegion(model, model.base, model.nbytes), context, chunk)
 
     def close(self):
         if getattr(self, "handle", None) is not None:

@@ -472,7 +472,7 @@ __global__ __launch_bounds__(kHeadThreads) void attention_prep_kernel(
 constexpr int kAttnSplits = 128;  // ranges per KV head for a decode step
 constexpr int kAttnBlock = 64;
 constexpr int kMaxGroup = 8;
-constexpr int kChunk = 512;      // rows of a prefill chunk
+constexpr int kChunk = 2048;     // default rows of a prefill chunk
 
 __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
     const float* __restrict__ query, const float* __restrict__ gate, const float* __restrict__ key_cache,
@@ -599,6 +599,144 @@ __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
     }
 }
 
+// Prefill attention on the matrix cores: one wave per (query head
+// blockIdx.x, tile of 32 query rows blockIdx.y), causal over positions
+// 0 .. *position + row, FP32 MFMA (v_mfma_f32_32x32x2_f32, exact products,
+// FP32 sums).  Per block of 32 positions the wave forms S^T = K Q^T (rows
+// positions, columns queries), so lane l holds 16 of query l % 32's scores
+// and lane l ^ 32 the other 16: the online-softmax maximum and sum of a query
+// are a 16-register reduction and one swap between the wave's halves.  In
+// the same registers exp(S^T - m) is the A operand of P V (the pair index of
+// the MFMA k step is the half of the wave in both), so P is never moved; the
+// per-query rescale factors reach the output rows through a 32-float LDS
+// transpose.  Q stays in registers for the whole position loop.  Scores are
+// q . k / sqrt(AD) as engine.cpp:344-361; AD a multiple of 32, at most 256.
+constexpr int kFlashQ = 32;
+
+__global__ __launch_bounds__(kWave, 1) void attention_prefill_kernel(
+    const float* __restrict__ query, const float* __restrict__ gate, const float* __restrict__ key_cache,
+    const float* __restrict__ value_cache, const int* __restrict__ position, float* __restrict__ out, int AH,
+    int KVH, int AD, int count) {
+    __shared__ float row_scale[kFlashQ];
+    const int head = blockIdx.x, q0 = blockIdx.y * kFlashQ;
+    const int G = AH / KVH, kv = head / G;
+    const int AS = AH * AD, NB = AD / 32;
+    const size_t KVW = static_cast<size_t>(KVH) * AD;
+    const int lane = threadIdx.x, li = lane & 31, kh = lane >> 5;
+    const int p0 = *position;
+    const int rows = min(kFlashQ, count - q0);
+    const int last = p0 + q0 + rows - 1;  // the tile's last query position
+    const int my_pos = p0 + q0 + li;      // this lane's query (S^T column)
+    const bool my_valid = li < rows;
+    const float divisor = sqrtf(static_cast<float>(AD));
+    // Q row li, dims 32 b + 16 kh + (0 .. 15) of each 32-dim block b.
+    f32x4 qf[8][4];
+    {
+        const float* qr = query + static_cast<size_t>(q0 + min(li, rows - 1)) * AS + head * AD;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                qf[b][j] = b < NB ? *reinterpret_cast<const f32x4*>(qr + 32 * b + 16 * kh + 4 * j) : f32x4{0, 0, 0, 0};
+    }
+    f32x16 o[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
+    float m = -INFINITY, l = 0.0f;  // of query li (the same in lanes li and li + 32)
+    const float* kbase = key_cache + static_cast<size_t>(kv) * AD;
+    const float* vbase = value_cache + static_cast<size_t>(kv) * AD;
+    for (int b0 = 0; b0 <= last; b0 += 32) {
+        // S^T[p][q] for positions b0 + p: two accumulators over alternate
+        // 32-dim blocks, so consecutive MFMAs do not wait on each other.
+        f32x16 s0, s1;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.0f;
+        const float* kr = kbase + static_cast<size_t>(min(b0 + li, last)) * KVW;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            if (b < NB) {
+                f32x4 kf[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) kf[j] = *reinterpret_cast<const f32x4*>(kr + 32 * b + 16 * kh + 4 * j);
+#pragma unroll
+                for (int st = 0; st < 16; ++st) {
+                    if (b & 1)
+                        s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[st >> 2][st & 3], qf[b][st >> 2][st & 3], s1, 0, 0, 0);
+                    else
+                        s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[st >> 2][st & 3], qf[b][st >> 2][st & 3], s0, 0, 0, 0);
+                }
+            }
+        }
+        // Scores, causal mask, block maximum of query li.
+        float sc[16];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int p = b0 + 8 * (r >> 2) + 4 * kh + (r & 3);
+            const float v = (s0[r] + s1[r]) / divisor;
+            sc[r] = p <= my_pos && p <= last ? v : -INFINITY;
+            bm = fmaxf(bm, sc[r]);
+        }
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        const float mn = my_valid ? fmaxf(m, bm) : 0.0f;
+        float ps = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            sc[r] = my_valid ? expf(sc[r] - mn) : 0.0f;  // masked: exp(-inf) = 0
+            ps += sc[r];
+        }
+        ps += __shfl_xor(ps, 32);
+        const float alpha = my_valid ? expf(m - mn) : 0.0f;  // 0 on the first block
+        l = l * alpha + ps;
+        m = mn;
+        // Rescale the output rows: row q of register r is query
+        // 8 (r / 4) + 4 kh + r % 4; its factor comes from lane q.
+        if (kh == 0) row_scale[li] = alpha;
+        wave_lds_sync();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float a = row_scale[8 * (r >> 2) + 4 * kh + (r & 3)];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) o[t][r] *= a;
+        }
+        wave_lds_sync();
+        // O += P V: k step u pairs position 8 (u / 4) + 4 kh + u % 4 with
+        // register u of P, lane column li with output dim 32 t + li.
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            if (t < NB) {
+                float vb[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const int p = min(b0 + 8 * (u >> 2) + 4 * kh + (u & 3), last);
+                    vb[u] = vbase[static_cast<size_t>(p) * KVW + 32 * t + li];
+                }
+#pragma unroll
+                for (int u = 0; u < 16; ++u) o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(sc[u], vb[u], o[t], 0, 0, 0);
+            }
+        }
+    }
+    // out = O / l * sigmoid(gate) for the tile's valid rows.
+    if (kh == 0) row_scale[li] = my_valid ? 1.0f / l : 0.0f;
+    wave_lds_sync();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int q = 8 * (r >> 2) + 4 * kh + (r & 3);
+        if (q < rows) {
+            const float inv = row_scale[q];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                if (t < NB) {
+                    const size_t at = static_cast<size_t>(q0 + q) * AS + head * AD + 32 * t + li;
+                    out[at] = o[t][r] * inv * sigmoid_ref(gate[at]);
+                }
+            }
+        }
+    }
+}
+
 // out = (sum_s exp(m_s - M) acc_s) / (sum_s exp(m_s - M) l_s) * sigmoid(gate)
 // over the kAttnSplits ranges s of head blockIdx.x of row r = blockIdx.y, M
 // their largest maximum (empty ranges have m = -inf and weight 0).
@@ -710,7 +848,7 @@ struct LayerWeights {
 bool engine_config_ok(const q3x_hip_model_config& c, int context) {
     return (c.matrix_type == Q3X_HIP_MATRIX_Q8_0 || c.matrix_type == Q3X_HIP_MATRIX_Q4_0) && c.KD <= 128 &&
            c.VD <= 128 && c.AD <= 256 && c.RD <= 64 && c.RD % 2 == 0 && c.RD <= c.AD && c.CK >= 2 && c.CK <= 8 &&
-           c.AH / c.KVH <= kMaxGroup &&
+           c.AH / c.KVH <= kMaxGroup && c.AD % 32 == 0 &&
            c.top_k <= 8 && context >= 1 && context <= 262144;
 }
 
@@ -719,6 +857,7 @@ bool engine_config_ok(const q3x_hip_model_config& c, int context) {
 struct q3x_hip_engine {
     q3x_hip_model_config c{};
     int capacity = 0;
+    int chunk = 0;                // rows of a prefill chunk
     int position = 0;             // host mirror of *d_position
     int checkpoint_position = 0;
     Mat embedding, lm_head;
@@ -823,13 +962,17 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
             hipLaunchKernelGGL(attention_prep_kernel, dim3(c.AH + c.KVH, count), dim3(kHeadThreads), 0, s,
                                e.query_and_gate, e.key, e.value, L.qnorm, L.knorm, e.d_position, e.query, e.gate,
                                L.key_cache, L.value_cache, c.AH, c.KVH, c.AD, c.RD);
-            const int splits = count == 1 ? kAttnSplits : 1;
-            hipLaunchKernelGGL(attention_kernel, dim3(c.KVH * splits, count), dim3(kHeadThreads), 0, s, e.query,
-                               e.gate, L.key_cache, L.value_cache, e.d_position, e.scores, e.attn_out, c.AH, c.KVH,
-                               c.AD, splits);
-            if (splits > 1)
-                hipLaunchKernelGGL(attention_combine_kernel, dim3(c.AH, count), dim3(kHeadThreads), 0, s, e.scores,
+            if (count == 1) {
+                hipLaunchKernelGGL(attention_kernel, dim3(c.KVH * kAttnSplits, 1), dim3(kHeadThreads), 0, s,
+                                   e.query, e.gate, L.key_cache, L.value_cache, e.d_position, e.scores, e.attn_out,
+                                   c.AH, c.KVH, c.AD, kAttnSplits);
+                hipLaunchKernelGGL(attention_combine_kernel, dim3(c.AH, 1), dim3(kHeadThreads), 0, s, e.scores,
                                    e.gate, e.attn_out, c.AH, c.AD);
+            } else {
+                hipLaunchKernelGGL(attention_prefill_kernel, dim3(c.AH, (count + kFlashQ - 1) / kFlashQ), dim3(kWave),
+                                   0, s, e.query, e.gate, L.key_cache, L.value_cache, e.d_position, e.attn_out, c.AH,
+                                   c.KVH, c.AD, count);
+            }
             rc = apply(L.o, type, e.attn_out, count, e.hidden, true, s);
         }
         if (rc) break;
@@ -901,8 +1044,8 @@ extern "C" void q3x_hip_engine_destroy(q3x_hip_engine* e) {
 }
 
 extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const void* weights, int context,
-                                     q3x_hip_engine** engine, const char** error) {
-    if (!config || !weights || !engine) return Q3X_HIP_EINVAL;
+                                     int chunk, q3x_hip_engine** engine, const char** error) {
+    if (!config || !weights || !engine || chunk < 0) return Q3X_HIP_EINVAL;
     *engine = nullptr;
     const q3x_hip_model_config& c = *config;
     size_t count = 0;
@@ -978,7 +1121,8 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
     const size_t cache = static_cast<size_t>(context) * KVW;
     const int delta_layers = c.N - c.N / c.AI;
     e->recurrent_floats = static_cast<size_t>(delta_layers) * (conv + memory);
-    const size_t R = static_cast<size_t>(std::min(context, kChunk));  // rows of a chunk
+    e->chunk = std::min(context, chunk > 0 ? chunk : kChunk);
+    const size_t R = static_cast<size_t>(e->chunk);  // rows of a chunk
     if (c.experts)
         e->moe_ws_bytes = std::max(q3x_hip_moe_layer_workspace_bytes(&e->layers[0].moe, 1),
                                    q3x_hip_moe_layer_workspace_bytes(&e->layers[0].moe, static_cast<int>(R)));
@@ -1105,7 +1249,7 @@ extern "C" int q3x_hip_engine_forward(q3x_hip_engine* e, const int* tokens, int 
         if (hipGraphLaunch(g, e->stream) != hipSuccess) return Q3X_HIP_ERUNTIME;
     } else {
         for (int done = 0; done < count;) {
-            const int n = std::min(kChunk, count - done);
+            const int n = std::min(e->chunk, count - done);
             const int rc = enqueue(*e, n, compute_logits && done + n == count);
             if (rc) return rc;
             done += n;

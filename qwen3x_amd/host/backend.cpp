@@ -69,7 +69,8 @@ State* state_create(Model* model, int context_size) {
     State* state = new (std::nothrow) State();
     BACKEND_ASSERT(state);
     const char* message = nullptr;
-    const int code = q3x_hip_engine_create(&model->config, model->weights, context_size, &state->engine, &message);
+    const int code =
+        q3x_hip_engine_create(&model->config, model->weights, context_size, 0, &state->engine, &message);
     if (code != Q3X_HIP_OK) {
         std::fprintf(stderr, "state_create: %s\n", message ? message : q3x_hip_strerror(code));
         fail("q3x_hip_engine_create", __FILE__, __LINE__, code);

@@ -46,13 +46,15 @@ def test_engine_logits_match_the_reference_forward(name):
         assert engine.position == len(tokens)
 
 
-@pytest.mark.parametrize("name,prompt", [("dense_q8", 40), ("dense_q4", 530), ("moe_q4", 300),
-                                         ("moe_q8_tied", 64), ("gqa8_q8", 100)])
-def test_prefill_then_decode_match_the_reference_forward(name, prompt):
-    # A forward of many tokens runs them as prefill chunks of up to 512 rows
-    # (GEMMs, the recurrences token by token inside one launch); its logits,
-    # and those of the decode steps that follow, against the reference's
-    # token-by-token forward.  530 tokens cross a chunk boundary.
+@pytest.mark.parametrize("name,prompt,chunk", [("dense_q8", 40, 0), ("dense_q4", 530, 256), ("moe_q4", 300, 0),
+                                               ("moe_q8_tied", 64, 48), ("gqa8_q8", 100, 0), ("dense_q8", 333, 100)])
+def test_prefill_then_decode_match_the_reference_forward(name, prompt, chunk):
+    # A forward of many tokens runs them as prefill chunks (GEMMs, the
+    # recurrences token by token inside one launch, attention on the matrix
+    # cores); its logits, and those of the decode steps that follow, against
+    # the reference's token-by-token forward.  Chunks of 256, 48 and 100 rows
+    # put chunk boundaries inside the prompts, and tiles of 32 query rows
+    # end partly filled.
     _need_ref()
     _torch()
     fields = CONFIGS[name]
@@ -61,8 +63,8 @@ def test_prefill_then_decode_match_the_reference_forward(name, prompt):
     tokens = rng.integers(0, fields["V"], prompt + 4).astype(np.int32)
     want = oracle.ref_forward(fields, image, table, tokens)
     weights = dev(image)
-    say(f"engine {name}: prefill {prompt} + decode 4")
-    with q3x.Engine(config, weights, context=len(tokens)) as engine:
+    say(f"engine {name}: prefill {prompt} (chunk {chunk}) + decode 4")
+    with q3x.Engine(config, weights, context=len(tokens), chunk=chunk) as engine:
         engine.forward(tokens[:prompt])
         got = engine.logits()
         diff = np.abs(got - want[prompt - 1])

@@ -224,17 +224,18 @@ def test_engine_rejects_before_device_work():
     error = ctypes.c_char_p()
     P = ctypes.c_void_p(0x1000)   # never dereferenced: validation fails first
     bf16 = q3x.make_config(**dict(CONFIGS["dense_q8"], matrix_type=0))
-    assert lib.q3x_hip_engine_create(ctypes.byref(bf16), P, 8, ctypes.byref(handle), ctypes.byref(error)) == \
+    assert lib.q3x_hip_engine_create(ctypes.byref(bf16), P, 8, 0, ctypes.byref(handle), ctypes.byref(error)) == \
         q3x.ENOTSUP
     assert b"BF16" in error.value
-    for bad in (dict(KD=256), dict(VD=160), dict(RD=128), dict(CK=1), dict(H=250)):
+    for bad in (dict(KD=256), dict(VD=160), dict(RD=128), dict(CK=1), dict(H=250), dict(AD=80, RD=16)):
         cfg = q3x.make_config(**dict(CONFIGS["dense_q8"], **bad))
-        assert lib.q3x_hip_engine_create(ctypes.byref(cfg), P, 8, ctypes.byref(handle), ctypes.byref(error)) == \
+        assert lib.q3x_hip_engine_create(ctypes.byref(cfg), P, 8, 0, ctypes.byref(handle), ctypes.byref(error)) == \
             q3x.EINVAL, bad
     good = q3x.make_config(**CONFIGS["dense_q8"])
     for context in (0, 262145):
-        assert lib.q3x_hip_engine_create(ctypes.byref(good), P, context, ctypes.byref(handle), None) == q3x.EINVAL
-    assert lib.q3x_hip_engine_create(ctypes.byref(good), None, 8, ctypes.byref(handle), None) == q3x.EINVAL
+        assert lib.q3x_hip_engine_create(ctypes.byref(good), P, context, 0, ctypes.byref(handle), None) == q3x.EINVAL
+    assert lib.q3x_hip_engine_create(ctypes.byref(good), None, 8, 0, ctypes.byref(handle), None) == q3x.EINVAL
+    assert lib.q3x_hip_engine_create(ctypes.byref(good), P, 8, -1, ctypes.byref(handle), None) == q3x.EINVAL
     assert lib.q3x_hip_engine_forward(None, P, 1, 1) == q3x.EINVAL
     assert lib.q3x_hip_engine_logits(None, P) == q3x.EINVAL
     assert lib.q3x_hip_engine_reset(None) == q3x.EINVAL
