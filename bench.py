@@ -168,7 +168,9 @@ def launch_breakdown(torch, q3x, step, layer_sets):
     }
     out = {}
     for name, (fn, nbytes) in kinds.items():
-        ms = events_ms(torch, fn, 4 * n)
+        # Median of five windows of 4n calls: one slow window (a clock or
+        # power transition) does not stand for the launch.
+        ms = statistics.median(events_ms(torch, fn, 4 * n) for _ in range(5))
         out[name] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
     step.reset()
     return out
