@@ -29,6 +29,8 @@
 #include <vector>
 
 #include "common.h"
+#include "matvec.h"
+#include "moe.h"
 #include "rows.h"
 
 struct q3x_hip_engine;
@@ -778,6 +780,96 @@ __global__ __launch_bounds__(256) void swiglu_kernel(float* __restrict__ gate, c
     if (i < n) gate[i] = silu_ref(gate[i]) * up[i];
 }
 
+// Element i of x in the matvec kernels' padded LDS copy.
+__device__ __forceinline__ float* lds_x(uint8_t* xl, int i) {
+    return reinterpret_cast<float*>(xl + x_block_offset(i / kBlock) + 4 * (i % kBlock));
+}
+
+// Input staging for a decode step's projections (mv_pipe_kernel's `In`):
+// x = RMSNorm(h) * (1 + w) of the raw residual h (engine.cpp:228-233),
+// formed by every workgroup of the matvec launch on its way into LDS.  Each
+// thread loads its 16-byte chunks of h together with their four norm
+// weights (one round trip; the first kHeld chunks stay in registers) and
+// copies h to LDS; after one barrier every wave sums the squares of all of
+// h from LDS in the same fixed order (lane l takes chunks l, l + 64, ...
+// with FMAs, then the wave's DPP tree), so every wave of every workgroup --
+// whatever the launch shape -- holds the same scale; then each thread
+// scales its own chunks.  Requires w 8-byte aligned.
+struct NormInput {
+    static constexpr int kHeld = 4;
+    const uint16_t* w;
+    __device__ void stage(const float* x, uint8_t* xl, int bpr, float* /*work*/) const {
+        const int chunks = bpr * 8;
+        const int B = blockDim.x;
+        const f32x4* xs = reinterpret_cast<const f32x4*>(x);
+        const uint2* ws = reinterpret_cast<const uint2*>(w);
+        auto at = [&](int c) { return reinterpret_cast<f32x4*>(xl + x_block_offset(c >> 3) + 16 * (c & 7)); };
+        f32x4 xr[kHeld];
+        uint2 wr[kHeld];
+#pragma unroll
+        for (int k = 0; k < kHeld; ++k) {
+            const int c = threadIdx.x + k * B;
+            if (c < chunks) {
+                xr[k] = xs[c];
+                wr[k] = ws[c];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kHeld; ++k) {
+            const int c = threadIdx.x + k * B;
+            if (c < chunks) *at(c) = xr[k];
+        }
+        for (int c = threadIdx.x + kHeld * B; c < chunks; c += B) *at(c) = xs[c];
+        __syncthreads();
+        float square = 0.0f;
+        for (int c = threadIdx.x % kWave; c < chunks; c += kWave) {
+            const f32x4 v = *at(c);
+            square = fmaf(v.x, v.x, square);
+            square = fmaf(v.y, v.y, square);
+            square = fmaf(v.z, v.z, square);
+            square = fmaf(v.w, v.w, square);
+        }
+        const float total = wave_sum_f32(square);
+        const float scale = 1.0f / sqrtf(total / static_cast<float>(bpr * kBlock) + kEps);
+        __syncthreads();  // every wave's reads of h precede the scaled writes
+        auto put = [&](int c, f32x4 v, uint2 q) {
+            v.x = v.x * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.x)));
+            v.y = v.y * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.x >> 16)));
+            v.z = v.z * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.y)));
+            v.w = v.w * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.y >> 16)));
+            *at(c) = v;
+        };
+#pragma unroll
+        for (int k = 0; k < kHeld; ++k) {
+            const int c = threadIdx.x + k * B;
+            if (c < chunks) put(c, xr[k], wr[k]);
+        }
+        for (int c = threadIdx.x + kHeld * B; c < chunks; c += B) put(c, *at(c), ws[c]);
+        __syncthreads();
+    }
+};
+
+// Input staging for a decode step's down projection: x = silu(gate) * up
+// (engine.cpp:371-376; swiglu_kernel's arithmetic) formed on the way into
+// LDS from the gate|up matvec's two outputs.
+struct SwiGLUInput {
+    const float* up;
+    __device__ void stage(const float* gate, uint8_t* xl, int bpr, float* /*work*/) const {
+        const f32x4* g = reinterpret_cast<const f32x4*>(gate);
+        const f32x4* u = reinterpret_cast<const f32x4*>(up);
+        for (int c = threadIdx.x; c < bpr * 8; c += blockDim.x) {
+            const f32x4 a = g[c], b = u[c];
+            f32x4 h;
+            h.x = silu_ref(a.x) * b.x;
+            h.y = silu_ref(a.y) * b.y;
+            h.z = silu_ref(a.z) * b.z;
+            h.w = silu_ref(a.w) * b.w;
+            *reinterpret_cast<f32x4*>(xl + x_block_offset(c >> 3) + 16 * (c & 7)) = h;
+        }
+        __syncthreads();
+    }
+};
+
 // The first index of the largest logit (std::max_element, engine.cpp:606-610).
 __global__ __launch_bounds__(kNormThreads) void argmax_kernel(const float* __restrict__ x, int n, int* __restrict__ out) {
     __shared__ float bv[kNormThreads / kWave];
@@ -913,6 +1005,40 @@ int apply_group(const Mat* m, float* const* y, int n, uint32_t type, int cols, c
     return Q3X_HIP_OK;
 }
 
+// A decode step's matvec of the matrices m[0..n) (same width `cols`) over
+// x, with `in` staging x into LDS (a norm or SwiGLU applied on the way in):
+// one launch of the pipelined kernel; add[i]: y[i] += W x.  Returns
+// Q3X_HIP_ENOTSUP before launching anything where that kernel does not take
+// the shape (x too long for LDS, unaligned rows); the caller then runs the
+// separate kernels.
+template <class In>
+int mv_staged(const Mat* m, float* const* y, const bool* add, int n, uint32_t type, int cols, const float* x,
+              const In& in, hipStream_t s) {
+    const int bpr = cols / kBlock;
+    const size_t row_bytes = static_cast<size_t>(bpr) * block_bytes(type);
+    if (row_bytes % 16 != 0 || !aligned(x, 16) || n < 1 || n > MultiRows::kMax) return Q3X_HIP_ENOTSUP;
+    MultiRows map{};
+    map.count = n;
+    map.row_bytes = row_bytes;
+    map.x = x;
+    int total = 0;
+    for (int i = 0; i < n; ++i) {
+        if (!aligned(m[i].w, 16) || m[i].cols != cols) return Q3X_HIP_ENOTSUP;
+        total += m[i].rows;
+        map.w[i] = static_cast<const uint8_t*>(m[i].w);
+        map.y[i] = y[i];
+        map.end[i] = total;
+        if (add[i]) map.accumulate_mask |= 1u << i;
+    }
+    for (int i = n; i < MultiRows::kMax; ++i) {
+        map.w[i] = map.w[0];
+        map.y[i] = map.y[0];
+        map.end[i] = total;
+    }
+    return type == Q3X_HIP_MATRIX_Q8_0 ? launch_pipe_for<Q3X_HIP_MATRIX_Q8_0>(map, total, bpr, s, in)
+                                       : launch_pipe_for<Q3X_HIP_MATRIX_Q4_0>(map, total, bpr, s, in);
+}
+
 // Enqueues `count` tokens (tokens[*d_step ..] at *d_position ..) through
 // every layer; the logits of the last one when `logits`; then advances the
 // step and position by count.  count 1 is the decode step the graphs
@@ -930,16 +1056,28 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
         hipLaunchKernelGGL(embed_kernel<Q3X_HIP_MATRIX_Q4_0>, eg, dim3(256), 0, s,
                            static_cast<const uint8_t*>(e.embedding.w), c.H, e.d_tokens, e.d_step, e.hidden);
     int rc = launch_status();
+    // A decode step forms each norm and SwiGLU inside the matvec that reads
+    // it, and adds an MoE layer's output to hidden directly; a chunk (or a
+    // shape those launches do not take) runs them as kernels of their own.
+    const bool step = count == 1;
+    const bool no_add[4] = {false, false, false, false};
     bool pending = false;  // an MoE output in `branch` still to be added to hidden
     for (int i = 0; i < c.N && rc == Q3X_HIP_OK; ++i) {
         const LayerWeights& L = e.layers[i];
-        hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden,
-                           pending ? e.branch : nullptr, L.input_norm, c.H, e.normalized);
+        const int nproj = L.attention ? 3 : 4;
+        const Mat proj[4] = {L.attention ? L.q : L.qkv, L.attention ? L.k : L.z, L.attention ? L.v : L.a, L.b};
+        float* const proj_out[4] = {L.attention ? e.query_and_gate : e.qkv, L.attention ? e.key : e.z,
+                                    L.attention ? e.value : e.a, e.b};
+        rc = Q3X_HIP_ENOTSUP;
+        if (step && !pending && aligned(L.input_norm, 8))
+            rc = mv_staged(proj, proj_out, no_add, nproj, type, c.H, e.hidden, NormInput{L.input_norm}, s);
+        if (rc == Q3X_HIP_ENOTSUP) {
+            hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden,
+                               pending ? e.branch : nullptr, L.input_norm, c.H, e.normalized);
+            rc = apply_group(proj, proj_out, nproj, type, c.H, e.normalized, count, s);
+        }
+        if (rc) break;
         if (!L.attention) {
-            const Mat m[4] = {L.qkv, L.z, L.a, L.b};
-            float* const y[4] = {e.qkv, e.z, e.a, e.b};
-            rc = apply_group(m, y, 4, type, c.H, e.normalized, count, s);
-            if (rc) break;
             hipLaunchKernelGGL(delta_conv_kernel, dim3((DQKV + 255) / 256), dim3(256), 0, s, e.qkv, L.conv,
                                L.conv_state, DQKV, c.CK, count);
             if (count == 1) {
@@ -955,10 +1093,6 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
             }
             rc = apply(L.out, type, e.delta_out, count, e.hidden, true, s);
         } else {
-            const Mat m[3] = {L.q, L.k, L.v};
-            float* const y[3] = {e.query_and_gate, e.key, e.value};
-            rc = apply_group(m, y, 3, type, c.H, e.normalized, count, s);
-            if (rc) break;
             hipLaunchKernelGGL(attention_prep_kernel, dim3(c.AH + c.KVH, count), dim3(kHeadThreads), 0, s,
                                e.query_and_gate, e.key, e.value, L.qnorm, L.knorm, e.d_position, e.query, e.gate,
                                L.key_cache, L.value_cache, c.AH, c.KVH, c.AD, c.RD);
@@ -976,20 +1110,36 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
             rc = apply(L.o, type, e.attn_out, count, e.hidden, true, s);
         }
         if (rc) break;
-        hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden, nullptr, L.post_norm, c.H,
-                           e.normalized);
         if (c.experts) {
-            rc = q3x_hip_moe_layer(&L.moe, e.normalized, count, e.branch, nullptr, nullptr, e.moe_ws,
-                                   e.moe_ws_bytes, s);
-            pending = true;
+            hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden, nullptr, L.post_norm,
+                               c.H, e.normalized);
+            rc = step ? moe_layer_decode_add(L.moe, e.normalized, e.hidden, e.moe_ws, e.moe_ws_bytes, s)
+                      : Q3X_HIP_ENOTSUP;
+            pending = rc == Q3X_HIP_ENOTSUP;
+            if (pending)
+                rc = q3x_hip_moe_layer(&L.moe, e.normalized, count, e.branch, nullptr, nullptr, e.moe_ws,
+                                       e.moe_ws_bytes, s);
         } else {
-            const Mat m[2] = {L.gate, L.up};
-            float* const y[2] = {e.ffn_gate, e.ffn_up};
-            rc = apply_group(m, y, 2, type, c.H, e.normalized, count, s);
+            const Mat gate_up[2] = {L.gate, L.up};
+            float* const ffn[2] = {e.ffn_gate, e.ffn_up};
+            rc = step && aligned(L.post_norm, 8)
+                     ? mv_staged(gate_up, ffn, no_add, 2, type, c.H, e.hidden, NormInput{L.post_norm}, s)
+                     : Q3X_HIP_ENOTSUP;
+            if (rc == Q3X_HIP_ENOTSUP) {
+                hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden, nullptr,
+                                   L.post_norm, c.H, e.normalized);
+                rc = apply_group(gate_up, ffn, 2, type, c.H, e.normalized, count, s);
+            }
             if (rc) break;
-            const int n = count * c.I;
-            hipLaunchKernelGGL(swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, s, e.ffn_gate, e.ffn_up, n);
-            rc = apply(L.down, type, e.ffn_gate, count, e.hidden, true, s);
+            const bool add = true;
+            float* const residual = e.hidden;
+            rc = step ? mv_staged(&L.down, &residual, &add, 1, type, c.I, e.ffn_gate, SwiGLUInput{e.ffn_up}, s)
+                      : Q3X_HIP_ENOTSUP;
+            if (rc == Q3X_HIP_ENOTSUP) {
+                const int n = count * c.I;
+                hipLaunchKernelGGL(swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, s, e.ffn_gate, e.ffn_up, n);
+                rc = apply(L.down, type, e.ffn_gate, count, e.hidden, true, s);
+            }
             pending = false;
         }
         if (rc == Q3X_HIP_OK) rc = launch_status();
@@ -998,9 +1148,14 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
     if (logits) {
         // The last row only: its residual, final norm and lm_head.
         const size_t last = static_cast<size_t>(count - 1) * c.H;
-        hipLaunchKernelGGL(rms_kernel, dim3(1), dim3(kNormThreads), 0, s, e.hidden + last,
-                           pending ? e.branch + last : nullptr, e.final_norm, c.H, e.normalized);
-        rc = q3x_hip_mv(e.lm_head.w, type, e.lm_head.rows, e.lm_head.cols, e.normalized, e.logits, 0, s);
+        rc = Q3X_HIP_ENOTSUP;
+        if (step && !pending && aligned(e.final_norm, 8))
+            rc = mv_staged(&e.lm_head, &e.logits, no_add, 1, type, c.H, e.hidden, NormInput{e.final_norm}, s);
+        if (rc == Q3X_HIP_ENOTSUP) {
+            hipLaunchKernelGGL(rms_kernel, dim3(1), dim3(kNormThreads), 0, s, e.hidden + last,
+                               pending ? e.branch + last : nullptr, e.final_norm, c.H, e.normalized);
+            rc = q3x_hip_mv(e.lm_head.w, type, e.lm_head.rows, e.lm_head.cols, e.normalized, e.logits, 0, s);
+        }
         if (rc) return rc;
     }
     hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, e.d_step, e.d_position, count);

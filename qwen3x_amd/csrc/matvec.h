@@ -299,8 +299,22 @@ __host__ __device__ constexpr uint32_t pipe_x_bytes(uint32_t qt, int bpr) {
            (qt == Q3X_HIP_MATRIX_Q4_0 ? ((4u * bpr + 15u) & ~15u) : 0u);
 }
 
-template <uint32_t QT, int LPR, int R, int D, class Rows, int WPE>
-__global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int nrows, int bpr) {
+// Input staging of mv_pipe_kernel: the launch's x (bpr blocks of 32 FP32
+// values) into the workgroup's padded LDS copy, once per workgroup, with
+// every thread of the workgroup taking part.  Other stagings (a norm or an
+// activation applied on the way in) supply the same stage() member; `work`
+// is 1 KB of LDS that is free until the staging's last barrier.
+struct PlainInput {
+    __device__ void stage(const float* x, uint8_t* xl, int bpr, float* /*work*/) const {
+        const f32x4* xs = reinterpret_cast<const f32x4*>(x);
+        for (int c = threadIdx.x; c < bpr * 8; c += blockDim.x)
+            *reinterpret_cast<f32x4*>(xl + x_block_offset(c >> 3) + 16 * (c & 7)) = xs[c];
+        __syncthreads();
+    }
+};
+
+template <uint32_t QT, int LPR, int R, int D, class Rows, int WPE, class In = PlainInput>
+__global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int nrows, int bpr, In in) {
     using S = PipeShape<QT, LPR>;
     constexpr int BB = S::BB, G = S::G, J = S::J, RS = G * R;
     constexpr bool Q4 = QT == Q3X_HIP_MATRIX_Q4_0;
@@ -349,10 +363,7 @@ __global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int n
     // x into LDS once per workgroup (overlaps the first weight loads), then
     // the per-block references for Q4_0.
     {
-        const f32x4* xs = reinterpret_cast<const f32x4*>(rows.input(0));
-        for (int c = threadIdx.x; c < bpr * 8; c += blockDim.x)
-            *reinterpret_cast<f32x4*>(xl + x_block_offset(c >> 3) + 16 * (c & 7)) = xs[c];
-        __syncthreads();
+        in.stage(rows.input(0), xl, bpr, reinterpret_cast<float*>(lds_dyn + pipe_x_bytes(QT, bpr)));
         if (Q4) {
             for (int b = threadIdx.x; b < bpr; b += blockDim.x)
                 sxl[b] = q4_mix_reference(reinterpret_cast<const float*>(xl + x_block_offset(b)));
@@ -535,10 +546,11 @@ inline int launch_staged(const Rows& rows, int nrows, int bpr, hipStream_t strea
 // fewest that the resident waves allow, and the grid then shrinks so that
 // every wave gets B full batches (balanced), spreading the waves over all
 // CUs (fewer per workgroup) when there are fewer than 256 workgroups' worth.
-template <uint32_t QT, int LPR, int R, class Rows, int D = 1, int WPE = 4>
-inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_t stream, int per_cu = 1) {
+template <uint32_t QT, int LPR, int R, class Rows, int D = 1, int WPE = 4, class In = PlainInput>
+inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_t stream, int per_cu = 1,
+                       const In& in = In{}) {
     using S = PipeShape<QT, LPR>;
-    auto kernel = mv_pipe_kernel<QT, LPR, R, D, Rows, WPE>;
+    auto kernel = mv_pipe_kernel<QT, LPR, R, D, Rows, WPE, In>;
     static const bool lds_ready =
         hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(kLdsPerCU)) == hipSuccess;
@@ -560,7 +572,7 @@ inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_
     lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb_used) * S::WAVE_LDS;
     Rows planned = rows;
     planned.plan_waves(grid * wpb_used);
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWave * wpb_used), lds, stream, planned, nrows, bpr);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWave * wpb_used), lds, stream, planned, nrows, bpr, in);
     return launch_status();
 }
 
@@ -571,28 +583,28 @@ inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_
 // drains evenly).  Prefetching two or three steps ahead measured slower at
 // every size (the registers cost more occupancy than the extra bytes in
 // flight gain), so the launches use one.
-template <uint32_t QT, class Rows>
-inline int launch_pipe_for(const Rows& rows, int nrows, int bpr, hipStream_t stream) {
-    if (bpr <= 16) return launch_pipe<QT, 16, 1>(rows, nrows, bpr, 16, stream);
-    if (bpr <= 32) return launch_pipe<QT, 32, 1>(rows, nrows, bpr, 16, stream);
+template <uint32_t QT, class Rows, class In = PlainInput>
+inline int launch_pipe_for(const Rows& rows, int nrows, int bpr, hipStream_t stream, const In& in = In{}) {
+    if (bpr <= 16) return launch_pipe<QT, 16, 1, Rows, 1, 4, In>(rows, nrows, bpr, 16, stream, 1, in);
+    if (bpr <= 32) return launch_pipe<QT, 32, 1, Rows, 1, 4, In>(rows, nrows, bpr, 16, stream, 1, in);
     if (QT == Q3X_HIP_MATRIX_Q8_0) {
         // 16K-64K rows (e.g. a gate|up pair): a 64-VGPR build, so that two
         // 16-wave workgroups are resident per CU (the default build needs 68
         // VGPRs, 7 waves per SIMD); taller matrices stream better without.
         if (nrows >= 16384 && nrows <= 65536)
-            return launch_pipe<QT, 64, 1, Rows, 1, 8>(rows, nrows, bpr, 16, stream, 2);
-        return launch_pipe<QT, 64, 1>(rows, nrows, bpr, 16, stream, nrows >= 8192 ? 2 : 1);
+            return launch_pipe<QT, 64, 1, Rows, 1, 8, In>(rows, nrows, bpr, 16, stream, 2, in);
+        return launch_pipe<QT, 64, 1, Rows, 1, 4, In>(rows, nrows, bpr, 16, stream, nrows >= 8192 ? 2 : 1, in);
     }
     // Short Q4_0 rows that 64-block passes would leave partly idle (e.g. 160
     // blocks = 2.5 passes) take 32 lanes per row (two rows per pass).  The
     // lanes per row depend on the row length only, so the per-row reduction
     // order (and the result) is the same whatever the launch's row count.
     if (bpr <= 256 && bpr % 64 != 0 && bpr % 32 == 0) {
-        if (nrows <= 4096) return launch_pipe<QT, 32, 1>(rows, nrows, bpr, 16, stream);
-        return launch_pipe<QT, 32, 2>(rows, nrows, bpr, 16, stream, 2);
+        if (nrows <= 4096) return launch_pipe<QT, 32, 1, Rows, 1, 4, In>(rows, nrows, bpr, 16, stream, 1, in);
+        return launch_pipe<QT, 32, 2, Rows, 1, 4, In>(rows, nrows, bpr, 16, stream, 2, in);
     }
-    if (nrows <= 4096) return launch_pipe<QT, 64, 1>(rows, nrows, bpr, 16, stream);
-    return launch_pipe<QT, 64, 2>(rows, nrows, bpr, 16, stream, 2);
+    if (nrows <= 4096) return launch_pipe<QT, 64, 1, Rows, 1, 4, In>(rows, nrows, bpr, 16, stream, 1, in);
+    return launch_pipe<QT, 64, 2, Rows, 1, 4, In>(rows, nrows, bpr, 16, stream, 2, in);
 }
 
 template <uint32_t QT, class Rows>

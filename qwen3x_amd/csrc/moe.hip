@@ -19,6 +19,8 @@
 //     runs gate_up for every tile of every expert, then SwiGLU, then one for
 //     down; a combine sums the slots of each token in slot order from zero.
 // No atomics touch any accumulated value, so results are deterministic.
+#include "moe.h"
+
 #include "gemm.h"
 #include "matvec.h"
 
@@ -879,9 +881,12 @@ inline MoeLayerLayout moe_layer_layout(int tokens, int experts, int top_k, int H
     return L;
 }
 
+// accumulate (one token only): Y += the layer output, or Q3X_HIP_ENOTSUP
+// before Y is touched where the decode path does not take the shape.
 template <uint32_t QT>
 int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens, float* Y, int* ids,
-                  float* weights, uint8_t* ws, const MoeLayerLayout& L, hipStream_t stream) {
+                  float* weights, uint8_t* ws, const MoeLayerLayout& L, hipStream_t stream,
+                  bool accumulate = false) {
     constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
     const int E = w.experts, H = w.H, I = w.I, SI = w.shared_I, K = w.top_k;
     float* logits = reinterpret_cast<float*>(ws + L.logits);
@@ -917,8 +922,9 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
     // Decode: routed and shared experts in two launches.
     if (tokens == 1) {
         const SharedExpert shared{sg, su, sd, SI, gate};
-        status = moe_decode<QT>(gate_up, down, E, H, I, X, sel, wts, K, Y, 0, rws, L.R, shared, stream);
-        if (status != Q3X_HIP_ENOTSUP) return status;
+        status = moe_decode<QT>(gate_up, down, E, H, I, X, sel, wts, K, Y, accumulate ? 1 : 0, rws, L.R, shared,
+                                stream);
+        if (status != Q3X_HIP_ENOTSUP || accumulate) return status;
     }
     // Prefill (or an unaligned decode): the grouped routed experts write Y,
     // then the shared expert's GEMMs add to it.
@@ -1031,9 +1037,9 @@ extern "C" size_t q3x_hip_moe_layer_workspace_bytes(const q3x_hip_moe_layer_weig
     return moe_layer_layout(tokens, layer->experts, layer->top_k, layer->H, layer->I, layer->shared_I).total;
 }
 
-extern "C" int q3x_hip_moe_layer(const q3x_hip_moe_layer_weights* layer, const float* X, int tokens, float* Y,
-                                 int* ids, float* weights, void* workspace, size_t workspace_bytes,
-                                 hipStream_t stream) {
+static int moe_layer_checked(const q3x_hip_moe_layer_weights* layer, const float* X, int tokens, float* Y,
+                             int* ids, float* weights, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream, bool accumulate) {
     if (layer && layer->type == Q3X_HIP_MATRIX_BF16) return Q3X_HIP_ENOTSUP;
     if (!X || !Y || !workspace || !moe_layer_ok(layer, tokens)) return Q3X_HIP_EINVAL;
     const q3x_hip_moe_layer_weights& w = *layer;
@@ -1045,6 +1051,17 @@ extern "C" int q3x_hip_moe_layer(const q3x_hip_moe_layer_weights* layer, const f
         return Q3X_HIP_EINVAL;
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     return w.type == Q3X_HIP_MATRIX_Q8_0
-               ? moe_layer_run<Q3X_HIP_MATRIX_Q8_0>(w, X, tokens, Y, ids, weights, ws, L, stream)
-               : moe_layer_run<Q3X_HIP_MATRIX_Q4_0>(w, X, tokens, Y, ids, weights, ws, L, stream);
+               ? moe_layer_run<Q3X_HIP_MATRIX_Q8_0>(w, X, tokens, Y, ids, weights, ws, L, stream, accumulate)
+               : moe_layer_run<Q3X_HIP_MATRIX_Q4_0>(w, X, tokens, Y, ids, weights, ws, L, stream, accumulate);
+}
+
+extern "C" int q3x_hip_moe_layer(const q3x_hip_moe_layer_weights* layer, const float* X, int tokens, float* Y,
+                                 int* ids, float* weights, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream) {
+    return moe_layer_checked(layer, X, tokens, Y, ids, weights, workspace, workspace_bytes, stream, false);
+}
+
+int q3x::moe_layer_decode_add(const q3x_hip_moe_layer_weights& layer, const float* X, float* Y, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream) {
+    return moe_layer_checked(&layer, X, 1, Y, nullptr, nullptr, workspace, workspace_bytes, stream, true);
 }
