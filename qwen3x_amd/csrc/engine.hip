@@ -461,142 +461,128 @@ __global__ __launch_bounds__(kHeadThreads) void attention_prep_kernel(
     }
 }
 
-// Attention of query row r = blockIdx.y for the G = AH / KVH query heads
-// that share KV head blockIdx.x / splits (engine.cpp:344-361: scores q . k /
-// sqrt(AD), softmax, sum of weights times v), over positions 0 .. *position
-// + r (causal).  Each K and V row is loaded once for all G heads.  The
-// softmax is taken online over blocks of 64 positions (a running maximum
-// rescales the running sum and accumulator), so no score buffer bounds the
-// context.  With splits > 1 each workgroup takes one of `splits` position
-// ranges and leaves each head's range maximum, sum and accumulator in
-// `partial` for attention_combine_kernel; with splits == 1 it writes the
-// gated output.  AD <= 256, G <= kMaxGroup.
+// Decode attention of the query row at *position for the G = AH / KVH query
+// heads that share KV head blockIdx.x / splits (engine.cpp:344-361: scores
+// q . k / sqrt(AD), softmax, sum of weights times v), over position range
+// blockIdx.x % splits of 0 .. *position.  A range is taken in blocks of 64
+// positions, every K and V load of a block requested at once (wave w holds
+// the key rows of positions w, w + 4, ... of the block, lane l elements 4l ..
+// 4l + 3; thread i holds value element i of every position), each K and V row
+// loaded once for all G heads.  Scores leave each wave's DPP sum for LDS;
+// wave w then runs the online softmax of heads w, w + 4 with wave reductions
+// (a running maximum rescales the running sum and accumulators), so no score
+// buffer bounds the context.  Each head's range maximum, sum and accumulator
+// go to `partial` for attention_combine_kernel (empty ranges leave m = -inf,
+// l = 0).  AD <= 256 and a multiple of 4, G <= kMaxGroup.
 constexpr int kAttnSplits = 128;  // ranges per KV head for a decode step
 constexpr int kAttnBlock = 64;
 constexpr int kMaxGroup = 8;
 constexpr int kChunk = 2048;     // default rows of a prefill chunk
 
 __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
-    const float* __restrict__ query, const float* __restrict__ gate, const float* __restrict__ key_cache,
-    const float* __restrict__ value_cache, const int* __restrict__ position, float* __restrict__ partial,
-    float* __restrict__ out, int AH, int KVH, int AD, int splits) {
-    __shared__ float sc[kMaxGroup][kAttnBlock], pw[kMaxGroup][kAttnBlock];
+    const float* __restrict__ query, const float* __restrict__ key_cache, const float* __restrict__ value_cache,
+    const int* __restrict__ position, float* __restrict__ partial, int AH, int KVH, int AD, int splits) {
+    constexpr int kWaves = kHeadThreads / kWave;
+    constexpr int kRows = kAttnBlock / kWaves;  // key rows per wave per block
+    __shared__ __attribute__((aligned(16))) float sc[kMaxGroup][kAttnBlock];  // scores, then weights
+    __shared__ float head_m[kMaxGroup], head_l[kMaxGroup], head_alpha[kMaxGroup];
     const int kv = blockIdx.x / splits, split = blockIdx.x % splits;
-    const int r = blockIdx.y;
     const int G = AH / KVH;
-    const int AS = AH * AD;
-    const int n = *position + r + 1;
+    const int n = *position + 1;
     const int per = (n + splits - 1) / splits;
     const int t0 = min(n, split * per), t1 = min(n, t0 + per);
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int i = threadIdx.x;
     const size_t KVW = static_cast<size_t>(KVH) * AD;
     const float* kbase = key_cache + static_cast<size_t>(kv) * AD;
     const float* vbase = value_cache + static_cast<size_t>(kv) * AD;
     const float divisor = sqrtf(static_cast<float>(AD));
-    float qr[kMaxGroup][4];
+    const bool kl = 4 * lane < AD;
+    f32x4 q[kMaxGroup];
 #pragma unroll
     for (int g = 0; g < kMaxGroup; ++g)
+        q[g] = g < G && kl ? *reinterpret_cast<const f32x4*>(query + (kv * G + g) * AD + 4 * lane) : f32x4{0, 0, 0, 0};
+    float acc[kMaxGroup];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            qr[g][e] = g < G && lane + 64 * e < AD
-                           ? query[static_cast<size_t>(r) * AS + (kv * G + g) * AD + lane + 64 * e]
-                           : 0.0f;
-    float m[kMaxGroup], l[kMaxGroup], acc[kMaxGroup], alpha[kMaxGroup];
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) {
-        m[g] = -INFINITY;
-        l[g] = 0.0f;
-        acc[g] = 0.0f;
+    for (int g = 0; g < kMaxGroup; ++g) acc[g] = 0.0f;
+    if (i < kMaxGroup) {
+        head_m[i] = -INFINITY;
+        head_l[i] = 0.0f;
     }
+    __syncthreads();
     for (int b0 = t0; b0 < t1; b0 += kAttnBlock) {
         const int nb = min(kAttnBlock, t1 - b0);
-        // Scores: each wave takes positions wave, wave + 4, ..., two at a
-        // time, the K rows requested together, every head's dot from them.
-        for (int j0 = 2 * wave; j0 < nb; j0 += 2 * (kHeadThreads / kWave)) {
-            float kr[2][4];
+        float vr[kAttnBlock];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const float* k = kbase + static_cast<size_t>(b0 + min(j0 + u, nb - 1)) * KVW;
+        for (int j = 0; j < kAttnBlock; ++j)
+            vr[j] = j < nb && i < AD ? vbase[static_cast<size_t>(b0 + j) * KVW + i] : 0.0f;
+        f32x4 kr[kRows];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) kr[u][e] = lane + 64 * e < AD ? k[lane + 64 * e] : 0.0f;
-            }
+        for (int u = 0; u < kRows; ++u) {
+            const int j = u * kWaves + wave;
+            kr[u] = j < nb && kl ? *reinterpret_cast<const f32x4*>(kbase + static_cast<size_t>(b0 + j) * KVW + 4 * lane)
+                                 : f32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < kRows; ++u) {
+            const int j = u * kWaves + wave;
+            if (j >= nb) break;
 #pragma unroll
             for (int g = 0; g < kMaxGroup; ++g) {
                 if (g < G) {
-#pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        float x = 0.0f;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) x = fmaf(qr[g][e], kr[u][e], x);
-                        x = wave_sum_f32(x);
-                        if (lane == 0 && j0 + u < nb) sc[g][j0 + u] = x / divisor;
-                    }
+                    float x = q[g].x * kr[u].x;
+                    x = fmaf(q[g].y, kr[u].y, x);
+                    x = fmaf(q[g].z, kr[u].z, x);
+                    x = fmaf(q[g].w, kr[u].w, x);
+                    x = wave_sum_f32(x);
+                    if (lane == 0) sc[g][j] = x / divisor;
                 }
             }
         }
         __syncthreads();
-#pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g) {
-            if (g < G) {
-                float bm = sc[g][0];
-                for (int j = 1; j < nb; ++j) bm = fmaxf(bm, sc[g][j]);
-                const float mn = fmaxf(m[g], bm);
-                if (i < nb) pw[g][i] = expf(sc[g][i] - mn);
-                alpha[g] = expf(m[g] - mn);  // 0 for the first block (m = -inf)
-                m[g] = mn;
+        for (int g = wave; g < G; g += kWaves) {
+            const float sj = lane < nb ? sc[g][lane] : -INFINITY;
+            const float mo = head_m[g];
+            const float mn = fmaxf(mo, wave_max_f32(sj));
+            const float pj = lane < nb ? expf(sj - mn) : 0.0f;
+            const float ps = wave_sum_f32(pj);
+            sc[g][lane] = pj;
+            if (lane == 0) {
+                const float alpha = expf(mo - mn);  // 0 for the first block (mo = -inf)
+                head_alpha[g] = alpha;
+                head_m[g] = mn;
+                head_l[g] = head_l[g] * alpha + ps;
             }
         }
         __syncthreads();
-#pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g) {
-            if (g < G) {
-                float ps = 0.0f;
-                for (int j = 0; j < nb; ++j) ps += pw[g][j];
-                l[g] = l[g] * alpha[g] + ps;
-                acc[g] *= alpha[g];
-            }
-        }
         if (i < AD) {
-            // Eight positions' values requested together, then accumulated
-            // in position order for every head.
-            const float* vp = vbase + static_cast<size_t>(b0) * KVW + i;
-            int j = 0;
-            for (; j + 8 <= nb; j += 8) {
-                float vv[8];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) vv[u] = vp[static_cast<size_t>(j + u) * KVW];
+            for (int g = 0; g < kMaxGroup; ++g) {
+                if (g < G) {
+                    float a = acc[g] * head_alpha[g];
 #pragma unroll
-                for (int g = 0; g < kMaxGroup; ++g)
-                    if (g < G)
-#pragma unroll
-                        for (int u = 0; u < 8; ++u) acc[g] = fmaf(pw[g][j + u], vv[u], acc[g]);
-            }
-            for (; j < nb; ++j) {
-                const float vv = vp[static_cast<size_t>(j) * KVW];
-#pragma unroll
-                for (int g = 0; g < kMaxGroup; ++g)
-                    if (g < G) acc[g] = fmaf(pw[g][j], vv, acc[g]);
+                    for (int j = 0; j < kAttnBlock; j += 4) {
+                        const f32x4 w = *reinterpret_cast<const f32x4*>(&sc[g][j]);
+                        a = fmaf(w.x, vr[j + 0], a);
+                        a = fmaf(w.y, vr[j + 1], a);
+                        a = fmaf(w.z, vr[j + 2], a);
+                        a = fmaf(w.w, vr[j + 3], a);
+                    }
+                    acc[g] = a;
+                }
             }
         }
-        __syncthreads();  // sc / pw are rewritten by the next block
+        __syncthreads();  // sc and the head state are rewritten by the next block
     }
 #pragma unroll
     for (int g = 0; g < kMaxGroup; ++g) {
         if (g >= G) continue;
-        const int head = kv * G + g;
-        if (splits == 1) {
-            if (i < AD) {
-                const size_t at = static_cast<size_t>(r) * AS + head * AD + i;
-                out[at] = acc[g] / l[g] * sigmoid_ref(gate[at]);
-            }
-        } else {
-            float* p = partial + ((static_cast<size_t>(r) * AH + head) * splits + split) * (AD + 2);
-            if (i < AD) p[i] = acc[g];
-            if (i == 0) {
-                p[AD] = m[g];
-                p[AD + 1] = l[g];
-            }
+        float* p = partial + (static_cast<size_t>(kv * G + g) * splits + split) * (AD + 2);
+        if (i < AD) p[i] = acc[g];
+        if (i == 0) {
+            p[AD] = head_m[g];
+            p[AD + 1] = head_l[g];
         }
     }
 }
@@ -761,14 +747,13 @@ __global__ __launch_bounds__(kHeadThreads) void attention_combine_kernel(const f
     __syncthreads();
     const int AS = AH * AD;
     for (int i = t; i < AD; i += kHeadThreads) {
+        // Every range's accumulator requested at once, then summed in order.
+        float v[kAttnSplits];
+#pragma unroll
+        for (int s = 0; s < kAttnSplits; ++s) v[s] = p[s * (AD + 2) + i];
         float acc = 0.0f;
-        for (int s0 = 0; s0 < kAttnSplits; s0 += 32) {
-            float v[32];
 #pragma unroll
-            for (int s = 0; s < 32; ++s) v[s] = p[(s0 + s) * (AD + 2) + i];
-#pragma unroll
-            for (int s = 0; s < 32; ++s) acc = fmaf(w[s0 + s], v[s], acc);
-        }
+        for (int s = 0; s < kAttnSplits; ++s) acc = fmaf(w[s], v[s], acc);
         const size_t at = static_cast<size_t>(r) * AS + head * AD + i;
         out[at] = acc / total * sigmoid_ref(gate[at]);
     }
@@ -966,7 +951,7 @@ struct q3x_hip_engine {
     int *d_tokens = nullptr, *d_step = nullptr, *d_position = nullptr, *d_argmax = nullptr;
     void* moe_ws = nullptr;
     size_t moe_ws_bytes = 0;
-    int* h_tokens = nullptr;  // pinned staging of a forward's tokens
+    int* h_tokens = nullptr;  // pinned staging of a forward's counters and tokens
     int token_capacity = 0;
     hipStream_t stream = nullptr;
     hipGraphExec_t graph[2] = {nullptr, nullptr};
@@ -1097,9 +1082,9 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                                e.query_and_gate, e.key, e.value, L.qnorm, L.knorm, e.d_position, e.query, e.gate,
                                L.key_cache, L.value_cache, c.AH, c.KVH, c.AD, c.RD);
             if (count == 1) {
-                hipLaunchKernelGGL(attention_kernel, dim3(c.KVH * kAttnSplits, 1), dim3(kHeadThreads), 0, s,
-                                   e.query, e.gate, L.key_cache, L.value_cache, e.d_position, e.scores, e.attn_out,
-                                   c.AH, c.KVH, c.AD, kAttnSplits);
+                hipLaunchKernelGGL(attention_kernel, dim3(c.KVH * kAttnSplits), dim3(kHeadThreads), 0, s, e.query,
+                                   L.key_cache, L.value_cache, e.d_position, e.scores, c.AH, c.KVH, c.AD,
+                                   kAttnSplits);
                 hipLaunchKernelGGL(attention_combine_kernel, dim3(c.AH, 1), dim3(kHeadThreads), 0, s, e.scores,
                                    e.gate, e.attn_out, c.AH, c.AD);
             } else {
@@ -1327,9 +1312,11 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
                 L.value_cache = f(cache);
             }
         }
-        e->d_tokens = reinterpret_cast<int*>(take(e->token_capacity, 4));
-        e->d_step = reinterpret_cast<int*>(take(1, 4));
-        e->d_position = reinterpret_cast<int*>(take(1, 4));
+        // [step, position, tokens...]: one copy from the pinned staging
+        // sets a forward's counters and tokens.
+        e->d_step = reinterpret_cast<int*>(take(2 + static_cast<size_t>(e->token_capacity), 4));
+        e->d_position = e->d_step + 1;
+        e->d_tokens = e->d_step + 2;
         e->d_argmax = reinterpret_cast<int*>(take(1, 4));
         e->moe_ws = e->moe_ws_bytes ? take(e->moe_ws_bytes, 1) : nullptr;
         return at;
@@ -1346,7 +1333,7 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
     if (rc == Q3X_HIP_OK) {
         plan(static_cast<uint8_t*>(e->arena));
         if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
-            hipHostMalloc(reinterpret_cast<void**>(&e->h_tokens), sizeof(int) * e->token_capacity,
+            hipHostMalloc(reinterpret_cast<void**>(&e->h_tokens), sizeof(int) * (2 + e->token_capacity),
                           hipHostMallocDefault) != hipSuccess ||
             hipMemsetAsync(e->arena, 0, total, e->stream) != hipSuccess ||
             hipStreamSynchronize(e->stream) != hipSuccess) {
@@ -1389,10 +1376,10 @@ extern "C" int q3x_hip_engine_forward(q3x_hip_engine* e, const int* tokens, int 
     if (count > e->capacity - e->position) return Q3X_HIP_EINVAL;
     for (int i = 0; i < count; ++i)
         if (tokens[i] < 0 || tokens[i] >= e->c.V) return Q3X_HIP_EINVAL;
-    for (int i = 0; i < count; ++i) e->h_tokens[i] = tokens[i];
-    hipLaunchKernelGGL(set_counters_kernel, dim3(1), dim3(1), 0, e->stream, e->d_step, e->d_position, 0,
-                       e->position);
-    if (hipMemcpyAsync(e->d_tokens, e->h_tokens, sizeof(int) * count, hipMemcpyHostToDevice, e->stream) !=
+    e->h_tokens[0] = 0;  // step: index of the next token in the list
+    e->h_tokens[1] = e->position;
+    for (int i = 0; i < count; ++i) e->h_tokens[2 + i] = tokens[i];
+    if (hipMemcpyAsync(e->d_step, e->h_tokens, sizeof(int) * (2 + count), hipMemcpyHostToDevice, e->stream) !=
         hipSuccess)
         return Q3X_HIP_ERUNTIME;
     if (count == 1) {
@@ -1410,7 +1397,16 @@ extern "C" int q3x_hip_engine_forward(q3x_hip_engine* e, const int* tokens, int 
             done += n;
         }
     }
-    if (hipStreamSynchronize(e->stream) != hipSuccess) return Q3X_HIP_ERUNTIME;
+    if (count == 1) {
+        // A decode step lasts milliseconds: poll for its end rather than
+        // sleep in the runtime's wait, which wakes tens of microseconds late.
+        hipError_t q;
+        while ((q = hipStreamQuery(e->stream)) == hipErrorNotReady) {
+        }
+        if (q != hipSuccess) return Q3X_HIP_ERUNTIME;
+    } else if (hipStreamSynchronize(e->stream) != hipSuccess) {
+        return Q3X_HIP_ERUNTIME;
+    }
     e->position += count;
     return Q3X_HIP_OK;
 }
