@@ -310,82 +310,110 @@ __global__ __launch_bounds__(128) void delta_prep_kernel(float* __restrict__ qkv
     }
 }
 
-__global__ __launch_bounds__(kDeltaThreads) void delta_scan_kernel(const float* __restrict__ qkv,
-                                                                   const float* __restrict__ scale,
-                                                                   const float* __restrict__ beta,
-                                                                   float* __restrict__ memory, float* __restrict__ out,
-                                                                   int KH, int VH, int KD, int VD, int count) {
-    __shared__ float qt[kScanTile][128], kt[kScanTile][128], st[kScanTile], bt[kScanTile];
-    __shared__ float pp[kDeltaGroups][128], po[kDeltaGroups][128];
+// delta_scan_kernel: one workgroup of 8 waves per value head; lane l of
+// wave w owns value column 16 w + l / 4 and keys 32 (l % 4) .. + 31, its
+// S entries in registers across the tokens.  A column's four key groups sit
+// in one quad of lanes, so the sums over keys (k S before the update, q S
+// after it) are two DPP adds: the tokens run with no barrier between them.
+// q, k and v of kScanTile tokens are staged in LDS at a time, the next
+// tile's loads in flight while the current one is processed.
+constexpr int kScanThreads = 512;
+constexpr int kScanKeys = 32;  // keys per thread
+constexpr int kScanLoads = 3 * kScanTile * 128 / kScanThreads;  // staged values per thread per tile
+
+__global__ __launch_bounds__(kScanThreads) void delta_scan_kernel(const float* __restrict__ qkv,
+                                                                  const float* __restrict__ scale,
+                                                                  const float* __restrict__ beta,
+                                                                  float* __restrict__ memory, float* __restrict__ out,
+                                                                  int KH, int VH, int KD, int VD, int count) {
+    // [q | k | v] of the tile's tokens, 128 slots each (zeros past KD / VD).
+    __shared__ __attribute__((aligned(16))) float tile[3][kScanTile][128];
+    __shared__ float st[kScanTile], bt[kScanTile];
     const int head = blockIdx.x;
     const int t = threadIdx.x;
+    const int lane = t & (kWave - 1), wave = t / kWave;
     const int DQK = KH * KD, DO = VH * VD, DQKV = 2 * DQK + DO;
     const int kh = head / (VH / KH);
-    const int v = t & 127, group = t >> 7;
-    const bool col = v < VD;
+    const int c = wave * 16 + lane / 4, k0 = (lane & 3) * kScanKeys;
+    const bool col = c < VD;
     float* S = memory + static_cast<size_t>(head) * KD * VD;
-    float s[kDeltaKeys];
+    float s[kScanKeys];
 #pragma unroll
-    for (int j = 0; j < kDeltaKeys; ++j) {
-        const int key = group * kDeltaKeys + j;
-        s[j] = col && key < KD ? S[static_cast<size_t>(key) * VD + v] : 0.0f;
-    }
+    for (int j = 0; j < kScanKeys; ++j) s[j] = col && k0 + j < KD ? S[static_cast<size_t>(k0 + j) * VD + c] : 0.0f;
+    // Value e = t + i * kScanThreads of a tile: array e / (kScanTile * 128),
+    // token (e / 128) % kScanTile, slot e % 128.
+    float pre[kScanLoads], pst = 0.0f, pbt = 0.0f;
+    auto load_tile = [&](int r0) {
+        const int nt = min(kScanTile, count - r0);
+#pragma unroll
+        for (int i = 0; i < kScanLoads; ++i) {
+            const int e = t + i * kScanThreads;
+            const int arr = e / (kScanTile * 128), rr = (e / 128) % kScanTile, k = e % 128;
+            const float* row = qkv + static_cast<size_t>(r0 + rr) * DQKV;
+            const int off = arr == 0 ? kh * KD + k : arr == 1 ? DQK + kh * KD + k : 2 * DQK + head * VD + k;
+            pre[i] = rr < nt && k < (arr == 2 ? VD : KD) ? row[off] : 0.0f;
+        }
+        if (t < nt) {
+            pst = scale[static_cast<size_t>(r0 + t) * VH + head];
+            pbt = beta[static_cast<size_t>(r0 + t) * VH + head];
+        }
+    };
+    load_tile(0);
     for (int r0 = 0; r0 < count; r0 += kScanTile) {
         const int nt = min(kScanTile, count - r0);
         __syncthreads();  // the previous tile is consumed
-        for (int e = t; e < nt * 128; e += kDeltaThreads) {
-            const int rr = e / 128, k = e % 128;
-            const float* row = qkv + static_cast<size_t>(r0 + rr) * DQKV;
-            qt[rr][k] = k < KD ? row[kh * KD + k] : 0.0f;
-            kt[rr][k] = k < KD ? row[DQK + kh * KD + k] : 0.0f;
-        }
-        if (t < nt) {
-            st[t] = scale[static_cast<size_t>(r0 + t) * VH + head];
-            bt[t] = beta[static_cast<size_t>(r0 + t) * VH + head];
+#pragma unroll
+        for (int i = 0; i < kScanLoads; ++i) (&tile[0][0][0])[t + i * kScanThreads] = pre[i];
+        if (t < kScanTile) {
+            st[t] = pst;
+            bt[t] = pbt;
         }
         __syncthreads();
-        float vnext = col ? qkv[static_cast<size_t>(r0) * DQKV + 2 * DQK + head * VD + v] : 0.0f;
+        if (r0 + kScanTile < count) load_tile(r0 + kScanTile);
         for (int rr = 0; rr < nt; ++rr) {
-            const float vv = vnext;
-            if (rr + 1 < nt && col) vnext = qkv[static_cast<size_t>(r0 + rr + 1) * DQKV + 2 * DQK + head * VD + v];
+            const f32x4* kp = reinterpret_cast<const f32x4*>(&tile[1][rr][k0]);
+            const f32x4* qp = reinterpret_cast<const f32x4*>(&tile[0][rr][k0]);
             const float sc = st[rr], bb = bt[rr];
-            float pred = 0.0f;
+            const float vv = tile[2][rr][c < 128 ? c : 0];
+            float p0 = 0.0f, p1 = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kDeltaKeys; ++j) {
-                const int key = group * kDeltaKeys + j;
-                s[j] *= sc;
-                if (key < KD) pred = fmaf(kt[rr][key], s[j], pred);
+            for (int j4 = 0; j4 < kScanKeys / 4; ++j4) {
+                const f32x4 kk = kp[j4];
+                s[4 * j4 + 0] *= sc;
+                s[4 * j4 + 1] *= sc;
+                s[4 * j4 + 2] *= sc;
+                s[4 * j4 + 3] *= sc;
+                p0 = fmaf(kk.x, s[4 * j4 + 0], p0);
+                p1 = fmaf(kk.y, s[4 * j4 + 1], p1);
+                p0 = fmaf(kk.z, s[4 * j4 + 2], p0);
+                p1 = fmaf(kk.w, s[4 * j4 + 3], p1);
             }
-            pp[group][v] = pred;
-            __syncthreads();
-            float sum = pp[0][v];
+            float pred = p0 + p1;
+            pred += dpp_f32<0xB1>(pred);  // the quad's four key groups
+            pred += dpp_f32<0x4E>(pred);
+            const float delta = vv - pred;
+            float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
-            for (int g = 1; g < kDeltaGroups; ++g) sum += pp[g][v];
-            const float delta = vv - sum;
-            float o = 0.0f;
-#pragma unroll
-            for (int j = 0; j < kDeltaKeys; ++j) {
-                const int key = group * kDeltaKeys + j;
-                if (key < KD) {
-                    s[j] = fmaf(kt[rr][key] * bb, delta, s[j]);
-                    o = fmaf(qt[rr][key], s[j], o);
-                }
+            for (int j4 = 0; j4 < kScanKeys / 4; ++j4) {
+                const f32x4 kk = kp[j4], qq = qp[j4];
+                s[4 * j4 + 0] = fmaf(kk.x * bb, delta, s[4 * j4 + 0]);
+                s[4 * j4 + 1] = fmaf(kk.y * bb, delta, s[4 * j4 + 1]);
+                s[4 * j4 + 2] = fmaf(kk.z * bb, delta, s[4 * j4 + 2]);
+                s[4 * j4 + 3] = fmaf(kk.w * bb, delta, s[4 * j4 + 3]);
+                o0 = fmaf(qq.x, s[4 * j4 + 0], o0);
+                o1 = fmaf(qq.y, s[4 * j4 + 1], o1);
+                o0 = fmaf(qq.z, s[4 * j4 + 2], o0);
+                o1 = fmaf(qq.w, s[4 * j4 + 3], o1);
             }
-            po[group][v] = o;
-            __syncthreads();
-            if (t < VD) {
-                float result = po[0][t];
-#pragma unroll
-                for (int g = 1; g < kDeltaGroups; ++g) result += po[g][t];
-                out[static_cast<size_t>(r0 + rr) * DO + head * VD + t] = result;
-            }
+            float o = o0 + o1;
+            o += dpp_f32<0xB1>(o);
+            o += dpp_f32<0x4E>(o);
+            if ((lane & 3) == 0 && col) out[static_cast<size_t>(r0 + rr) * DO + head * VD + c] = o;
         }
     }
 #pragma unroll
-    for (int j = 0; j < kDeltaKeys; ++j) {
-        const int key = group * kDeltaKeys + j;
-        if (col && key < KD) S[static_cast<size_t>(key) * VD + v] = s[j];
-    }
+    for (int j = 0; j < kScanKeys; ++j)
+        if (col && k0 + j < KD) S[static_cast<size_t>(k0 + j) * VD + c] = s[j];
 }
 
 __global__ __launch_bounds__(128) void delta_norm_kernel(float* __restrict__ out, const float* __restrict__ z,
@@ -1071,7 +1099,7 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
             } else {
                 hipLaunchKernelGGL(delta_prep_kernel, dim3(c.KH, count), dim3(128), 0, s, e.qkv, e.a, e.b, L.alog,
                                    L.dt, c.KH, c.VH, c.KD, c.VD);
-                hipLaunchKernelGGL(delta_scan_kernel, dim3(c.VH), dim3(kDeltaThreads), 0, s, e.qkv, e.a, e.b,
+                hipLaunchKernelGGL(delta_scan_kernel, dim3(c.VH), dim3(kScanThreads), 0, s, e.qkv, e.a, e.b,
                                    L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD, count);
                 hipLaunchKernelGGL(delta_norm_kernel, dim3(c.VH, count), dim3(128), 0, s, e.delta_out, e.z, L.norm,
                                    c.VH, c.VD);
