@@ -174,6 +174,34 @@ __global__ __launch_bounds__(256) void delta_conv_kernel(float* __restrict__ qkv
         if (i < CK - 1) hist[i] = past[i];
 }
 
+// The DeltaNet memory S of a value head is stored column by column,
+// S[c * KD + k] (value column c, key k), so a thread's run of consecutive
+// keys of one column is contiguous: 16-byte accesses when KD % 4 == 0.
+template <int N>
+__device__ __forceinline__ void load_keys(const float* col, int k0, int KD, bool ok, float* s) {
+    if (ok && KD % 4 == 0 && k0 + N <= KD) {
+#pragma unroll
+        for (int j = 0; j < N; j += 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(col + k0 + j);
+            s[j] = v.x; s[j + 1] = v.y; s[j + 2] = v.z; s[j + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < N; ++j) s[j] = ok && k0 + j < KD ? col[k0 + j] : 0.0f;
+    }
+}
+template <int N>
+__device__ __forceinline__ void store_keys(float* col, int k0, int KD, bool ok, const float* s) {
+    if (ok && KD % 4 == 0 && k0 + N <= KD) {
+#pragma unroll
+        for (int j = 0; j < N; j += 4) *reinterpret_cast<f32x4*>(col + k0 + j) = f32x4{s[j], s[j + 1], s[j + 2], s[j + 3]};
+    } else if (ok) {
+#pragma unroll
+        for (int j = 0; j < N; ++j)
+            if (k0 + j < KD) col[k0 + j] = s[j];
+    }
+}
+
 // One value head of the gated delta rule (engine.cpp:262-316) for `count`
 // tokens in order: L2-normalised q and k of its key head (q also divided by
 // sqrt(KD)), beta = sigmoid(b), decay = -exp(A_log) * softplus(a + dt_bias);
@@ -199,13 +227,9 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_rule_kernel(
     const int kh = head / (VH / KH);
     const int v = t & 127, group = t >> 7;
     const bool col = v < VD;
-    float* S = memory + static_cast<size_t>(head) * KD * VD;
+    float* S = memory + (static_cast<size_t>(head) * VD + (col ? v : 0)) * KD;  // column v
     float s[kDeltaKeys];
-#pragma unroll
-    for (int j = 0; j < kDeltaKeys; ++j) {
-        const int key = group * kDeltaKeys + j;
-        s[j] = col && key < KD ? S[static_cast<size_t>(key) * VD + v] : 0.0f;
-    }
+    load_keys<kDeltaKeys>(S, group * kDeltaKeys, KD, col, s);
     const float A = expf(alog[head]);
     const float bias = bf16_value(dt[head]);
     const float nv = norm[t < VD ? t : 0];
@@ -266,11 +290,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_rule_kernel(
             out[at] = result * (g * nv * silu_ref(z[at]));
         }
     }
-#pragma unroll
-    for (int j = 0; j < kDeltaKeys; ++j) {
-        const int key = group * kDeltaKeys + j;
-        if (col && key < KD) S[static_cast<size_t>(key) * VD + v] = s[j];
-    }
+    store_keys<kDeltaKeys>(S, group * kDeltaKeys, KD, col, s);
 }
 
 // Prefill form of the delta rule, in three launches so that only the
@@ -336,10 +356,9 @@ __global__ __launch_bounds__(kScanThreads) void delta_scan_kernel(const float* _
     const int kh = head / (VH / KH);
     const int c = wave * 16 + lane / 4, k0 = (lane & 3) * kScanKeys;
     const bool col = c < VD;
-    float* S = memory + static_cast<size_t>(head) * KD * VD;
+    float* S = memory + (static_cast<size_t>(head) * VD + (col ? c : 0)) * KD;  // column c
     float s[kScanKeys];
-#pragma unroll
-    for (int j = 0; j < kScanKeys; ++j) s[j] = col && k0 + j < KD ? S[static_cast<size_t>(k0 + j) * VD + c] : 0.0f;
+    load_keys<kScanKeys>(S, k0, KD, col, s);
     // Value e = t + i * kScanThreads of a tile: array e / (kScanTile * 128),
     // token (e / 128) % kScanTile, slot e % 128.
     float pre[kScanLoads], pst = 0.0f, pbt = 0.0f;
@@ -411,9 +430,7 @@ __global__ __launch_bounds__(kScanThreads) void delta_scan_kernel(const float* _
             if ((lane & 3) == 0 && col) out[static_cast<size_t>(r0 + rr) * DO + head * VD + c] = o;
         }
     }
-#pragma unroll
-    for (int j = 0; j < kScanKeys; ++j)
-        if (col && k0 + j < KD) S[static_cast<size_t>(k0 + j) * VD + c] = s[j];
+    store_keys<kScanKeys>(S, k0, KD, col, s);
 }
 
 __global__ __launch_bounds__(128) void delta_norm_kernel(float* __restrict__ out, const float* __restrict__ z,
@@ -945,7 +962,7 @@ struct LayerWeights {
     Mat gate, up, down;  // dense FFN
     q3x_hip_moe_layer_weights moe{};
     float* conv_state = nullptr;  // DeltaNet: [DQKV, CK - 1]
-    float* memory = nullptr;      //           [VH, KD, VD]
+    float* memory = nullptr;      //           [VH, VD, KD] (column by column)
     float* key_cache = nullptr;   // attention: [capacity, KVH, AD]
     float* value_cache = nullptr;
 };
