@@ -43,11 +43,15 @@ struct DenseGemm {
     __device__ void store_pair(const GemmTile&, int, int, float, float) const {}
 };
 
-// Tile shapes (WM x WN waves, each TM x TN tiles of 32x32), measured on
-// MI355X over the prefill shapes: 128 x 128 tiles on 8 waves while the grid
-// has >= 4 such tiles per CU (e.g. N = 4096); below that 64 tokens x 128
-// weight rows on 8 waves for Q8_0 and 64 x 64 on 4 waves for Q4_0, whose
-// heavier dequantisation favours more, smaller workgroups.
+// Tile shapes (WM x WN waves, each TM x TN tiles of 32x32): 128 x 128 on 8
+// waves, 64 tokens x 128 weight rows on 8 waves, 64 x 64 on 4 waves.  A
+// launch's time goes as (its tile shape's rate) x (the CU balance: tiles per
+// CU on average over the most any CU takes, ceil(tiles / 256)) -- a tile
+// left over runs alone on its CU.  Rates measured on MI355X (TFLOP/s at
+// full balance, FP32 MFMA): Q8_0 130 / 120 / 118, Q4_0 128 / 126 / 117; the
+// launch takes the shape with the best product.  E.g. 2048 tokens x 5120
+// rows: 640 tiles of 128 x 128 (2.5 per CU, balance 0.83) against 1280 of
+// 64 x 128 (balance 1) -- the latter, 126 against 104 measured.
 template <uint32_t QT, int WM, int WN, int TM, int TN, int PF>
 int launch_dense_gemm_tiles(const DenseGemm& base, hipStream_t stream) {
     constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
@@ -60,13 +64,28 @@ int launch_dense_gemm_tiles(const DenseGemm& base, hipStream_t stream) {
     return launch_status();
 }
 
+// Mean over maximum tiles per CU for `tiles` tiles spread over the CUs.
+inline double cu_balance(long long tiles) {
+    const long long most = (tiles + kCUs - 1) / kCUs;
+    return static_cast<double>(tiles) / static_cast<double>(most * kCUs);
+}
+
 // Register sets for the stages ahead (PF), measured per tile: two for Q8_0's
 // 64 x 128 tiles, one elsewhere (equal or faster, fewer registers).
 template <uint32_t QT>
 int launch_dense_gemm(const DenseGemm& g, hipStream_t stream) {
-    const long long large = static_cast<long long>((g.rows + 127) / 128) * ((g.count + 127) / 128);
-    if (large >= 4LL * kCUs) return launch_dense_gemm_tiles<QT, 2, 4, 2, 1, 1>(g, stream);
-    if (QT == Q3X_HIP_MATRIX_Q8_0) return launch_dense_gemm_tiles<QT, 2, 4, 1, 1, 2>(g, stream);
+    const bool q8 = QT == Q3X_HIP_MATRIX_Q8_0;
+    auto tiles = [&](int bm, int bn) {
+        return static_cast<long long>((g.rows + bn - 1) / bn) * ((g.count + bm - 1) / bm);
+    };
+    const double large = (q8 ? 130.0 : 128.0) * cu_balance(tiles(128, 128));
+    const double wide = (q8 ? 120.0 : 126.0) * cu_balance(tiles(64, 128));
+    const double small = (q8 ? 118.0 : 117.0) * cu_balance(tiles(64, 64));
+    if (large >= wide && large >= small) return launch_dense_gemm_tiles<QT, 2, 4, 2, 1, 1>(g, stream);
+    if (wide >= small) {
+        if (q8) return launch_dense_gemm_tiles<QT, 2, 4, 1, 1, 2>(g, stream);
+        return launch_dense_gemm_tiles<QT, 2, 4, 1, 1, 1>(g, stream);
+    }
     return launch_dense_gemm_tiles<QT, 2, 2, 1, 1, 1>(g, stream);
 }
 
