@@ -125,38 +125,55 @@ __global__ __launch_bounds__(kNormThreads) void rms_kernel(float* __restrict__ h
 }
 
 // Causal depthwise convolution over the DQKV channels with CK - 1
-// remembered inputs, then SiLU (engine.cpp:251-261), for `count` tokens in
-// order (rows of qkv, in place); the history stays in registers.
+// remembered inputs, then SiLU (engine.cpp:251-261), for `count` tokens
+// (rows of qkv, in place).  A workgroup holds kConvChannels channels, each
+// cut into kConvSegments runs of consecutive tokens, one thread per run with
+// its window in registers.  Every thread first reads the CK - 1 raw inputs
+// before its run (the previous run's last rows, or the remembered history for
+// the first tokens); after one barrier the runs are convolved in place and
+// the thread holding the last token leaves the last CK - 1 raw inputs as the
+// new history.  The arithmetic per token is the reference's.  SEGMENTS: 16
+// for a chunk, 1 for a decode step (256 channels per workgroup).
 constexpr int kMaxConv = 8;
-__global__ __launch_bounds__(256) void delta_conv_kernel(float* __restrict__ qkv, const uint16_t* __restrict__ w,
-                                                         float* __restrict__ history, int channels, int CK,
-                                                         int count) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= channels) return;
-    const uint16_t* wc = w + static_cast<size_t>(c) * CK;
-    float* hist = history + static_cast<size_t>(c) * (CK - 1);
+constexpr int kConvThreads = 256;
+template <int SEGMENTS>
+__global__ __launch_bounds__(kConvThreads) void delta_conv_kernel(float* __restrict__ qkv,
+                                                                  const uint16_t* __restrict__ w,
+                                                                  float* __restrict__ history, int channels, int CK,
+                                                                  int count) {
+    constexpr int kChannels = kConvThreads / SEGMENTS;
+    const int c = blockIdx.x * kChannels + threadIdx.x % kChannels;
+    const int segment = threadIdx.x / kChannels;
+    const bool ok = c < channels;
+    const int per = (count + SEGMENTS - 1) / SEGMENTS;
+    const int t0 = min(count, segment * per), t1 = min(count, t0 + per);
+    float* hist = history + static_cast<size_t>(ok ? c : 0) * (CK - 1);
     float past[kMaxConv - 1], wt[kMaxConv];
 #pragma unroll
-    for (int i = 0; i < kMaxConv - 1; ++i) past[i] = i < CK - 1 ? hist[i] : 0.0f;
+    for (int i = 0; i < kMaxConv; ++i) wt[i] = ok && i < CK ? bf16_value(w[static_cast<size_t>(c) * CK + i]) : 0.0f;
 #pragma unroll
-    for (int i = 0; i < kMaxConv; ++i) wt[i] = i < CK ? bf16_value(wc[i]) : 0.0f;
+    for (int i = 0; i < kMaxConv - 1; ++i) {
+        const int tt = t0 - (CK - 1) + i;  // the raw input i places before the run's first token
+        past[i] = !ok || i >= CK - 1 ? 0.0f : tt >= 0 ? qkv[static_cast<size_t>(tt) * channels + c] : hist[tt + CK - 1];
+    }
+    __syncthreads();  // every raw input and history read precedes the writes
+    if (!ok) return;
+    float last = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxConv; ++i)
+        if (i == CK - 1) last = wt[i];
     constexpr int kAhead = 8;  // tokens whose inputs are requested together
     float xs[kAhead];
-    for (int t = 0; t < count; ++t) {
-        float* xp = qkv + static_cast<size_t>(t) * channels + c;
-        if (t % kAhead == 0) {
+    for (int t = t0; t < t1; ++t) {
+        if ((t - t0) % kAhead == 0) {
 #pragma unroll
             for (int u = 0; u < kAhead; ++u)
-                xs[u] = t + u < count ? qkv[static_cast<size_t>(t + u) * channels + c] : 0.0f;
+                xs[u] = t + u < t1 ? qkv[static_cast<size_t>(t + u) * channels + c] : 0.0f;
         }
         float x = 0.0f;
 #pragma unroll
         for (int u = 0; u < kAhead; ++u)
-            if (u == t % kAhead) x = xs[u];
-        float last = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kMaxConv; ++i)
-            if (i == CK - 1) last = wt[i];
+            if (u == (t - t0) % kAhead) x = xs[u];
         float sum = x * last;
 #pragma unroll
         for (int i = 0; i < kMaxConv - 1; ++i)
@@ -167,11 +184,13 @@ __global__ __launch_bounds__(256) void delta_conv_kernel(float* __restrict__ qkv
 #pragma unroll
         for (int i = 0; i < kMaxConv - 1; ++i)
             if (i == CK - 2) past[i] = x;
-        *xp = silu_ref(sum);
+        qkv[static_cast<size_t>(t) * channels + c] = silu_ref(sum);
     }
+    if (t0 < t1 && t1 == count) {
 #pragma unroll
-    for (int i = 0; i < kMaxConv - 1; ++i)
-        if (i < CK - 1) hist[i] = past[i];
+        for (int i = 0; i < kMaxConv - 1; ++i)
+            if (i < CK - 1) hist[i] = past[i];
+    }
 }
 
 // The DeltaNet memory S of a value head is stored column by column,
@@ -1108,8 +1127,12 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
         }
         if (rc) break;
         if (!L.attention) {
-            hipLaunchKernelGGL(delta_conv_kernel, dim3((DQKV + 255) / 256), dim3(256), 0, s, e.qkv, L.conv,
-                               L.conv_state, DQKV, c.CK, count);
+            if (count == 1)
+                hipLaunchKernelGGL(delta_conv_kernel<1>, dim3((DQKV + kConvThreads - 1) / kConvThreads),
+                                   dim3(kConvThreads), 0, s, e.qkv, L.conv, L.conv_state, DQKV, c.CK, count);
+            else
+                hipLaunchKernelGGL(delta_conv_kernel<16>, dim3((DQKV + kConvThreads / 16 - 1) / (kConvThreads / 16)),
+                                   dim3(kConvThreads), 0, s, e.qkv, L.conv, L.conv_state, DQKV, c.CK, count);
             if (count == 1) {
                 hipLaunchKernelGGL(delta_rule_kernel, dim3(c.VH), dim3(kDeltaThreads), 0, s, e.qkv, e.a, e.b, e.z,
                                    L.alog, L.dt, L.norm, L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD, 1);
