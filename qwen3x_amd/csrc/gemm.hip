@@ -45,13 +45,13 @@ struct DenseGemm {
 
 // Tile shapes (WM x WN waves, each TM x TN tiles of 32x32): 128 x 128 on 8
 // waves, 64 tokens x 128 weight rows on 8 waves, 64 x 64 on 4 waves.  A
-// launch's time goes as (its tile shape's rate) x (the CU balance: tiles per
-// CU on average over the most any CU takes, ceil(tiles / 256)) -- a tile
-// left over runs alone on its CU.  Rates measured on MI355X (TFLOP/s at
-// full balance, FP32 MFMA): Q8_0 130 / 120 / 118, Q4_0 128 / 126 / 117; the
-// launch takes the shape with the best product.  E.g. 2048 tokens x 5120
-// rows: 640 tiles of 128 x 128 (2.5 per CU, balance 0.83) against 1280 of
-// 64 x 128 (balance 1) -- the latter, 126 against 104 measured.
+// launch lasts about (tiles of the CU that takes the most, ceil(tiles /
+// 256)) x (one tile's work, padded rows and tokens included) / (the shape's
+// rate); the launch takes the shape with the least.  Rates measured on
+// MI355X (TFLOP/s over full tiles): Q8_0 130 / 120 / 118, Q4_0 128 / 126 /
+// 117.  E.g. 2048 tokens x 5120 rows: 640 tiles of 128 x 128 (3 on some CUs)
+// against 1280 of 64 x 128 (5 each, half the work each): the latter, 126
+// TFLOP/s against 104 measured; 48 rows: 32 tiles of 64 x 64.
 template <uint32_t QT, int WM, int WN, int TM, int TN, int PF>
 int launch_dense_gemm_tiles(const DenseGemm& base, hipStream_t stream) {
     constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
@@ -64,25 +64,20 @@ int launch_dense_gemm_tiles(const DenseGemm& base, hipStream_t stream) {
     return launch_status();
 }
 
-// Mean over maximum tiles per CU for `tiles` tiles spread over the CUs.
-inline double cu_balance(long long tiles) {
-    const long long most = (tiles + kCUs - 1) / kCUs;
-    return static_cast<double>(tiles) / static_cast<double>(most * kCUs);
-}
-
 // Register sets for the stages ahead (PF), measured per tile: two for Q8_0's
 // 64 x 128 tiles, one elsewhere (equal or faster, fewer registers).
 template <uint32_t QT>
 int launch_dense_gemm(const DenseGemm& g, hipStream_t stream) {
     const bool q8 = QT == Q3X_HIP_MATRIX_Q8_0;
-    auto tiles = [&](int bm, int bn) {
-        return static_cast<long long>((g.rows + bn - 1) / bn) * ((g.count + bm - 1) / bm);
+    auto cost = [&](int bm, int bn, double rate) {
+        const long long tiles = static_cast<long long>((g.rows + bn - 1) / bn) * ((g.count + bm - 1) / bm);
+        return static_cast<double>((tiles + kCUs - 1) / kCUs) * bm * bn / rate;
     };
-    const double large = (q8 ? 130.0 : 128.0) * cu_balance(tiles(128, 128));
-    const double wide = (q8 ? 120.0 : 126.0) * cu_balance(tiles(64, 128));
-    const double small = (q8 ? 118.0 : 117.0) * cu_balance(tiles(64, 64));
-    if (large >= wide && large >= small) return launch_dense_gemm_tiles<QT, 2, 4, 2, 1, 1>(g, stream);
-    if (wide >= small) {
+    const double large = cost(128, 128, q8 ? 130.0 : 128.0);
+    const double wide = cost(64, 128, q8 ? 120.0 : 126.0);
+    const double small = cost(64, 64, q8 ? 118.0 : 117.0);
+    if (large <= wide && large <= small) return launch_dense_gemm_tiles<QT, 2, 4, 2, 1, 1>(g, stream);
+    if (wide <= small) {
         if (q8) return launch_dense_gemm_tiles<QT, 2, 4, 1, 1, 2>(g, stream);
         return launch_dense_gemm_tiles<QT, 2, 4, 1, 1, 1>(g, stream);
     }
