@@ -651,37 +651,82 @@ __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
     }
 }
 
-// Prefill attention on the matrix cores: one wave per (query head
-// blockIdx.x, tile of 32 query rows blockIdx.y), causal over positions
-// 0 .. *position + row, FP32 MFMA (v_mfma_f32_32x32x2_f32, exact products,
-// FP32 sums).  Per block of 32 positions the wave forms S^T = K Q^T (rows
-// positions, columns queries), so lane l holds 16 of query l % 32's scores
-// and lane l ^ 32 the other 16: the online-softmax maximum and sum of a query
-// are a 16-register reduction and one swap between the wave's halves.  In
-// the same registers exp(S^T - m) is the A operand of P V (the pair index of
-// the MFMA k step is the half of the wave in both), so P is never moved; the
-// per-query rescale factors reach the output rows through a 32-float LDS
-// transpose.  Q stays in registers for the whole position loop.  Scores are
-// q . k / sqrt(AD) as engine.cpp:344-361; AD a multiple of 32, at most 256.
+// Prefill attention on the matrix cores, causal over positions 0 ..
+// *position + row, FP32 MFMA (v_mfma_f32_32x32x2_f32, exact products, FP32
+// sums).  A workgroup takes one tile of 32 query rows (the longest tiles
+// first) for up to kFlashWaves query heads of one KV head, one wave per
+// head.  Per block of 32 positions the K and V rows go global -> LDS once
+// for all of the workgroup's heads, by direct-to-LDS buffer loads into a
+// double buffer: the next block's copy is in flight while the current one is
+// used, and one barrier per block separates them.  Each wave forms S^T = K
+// Q^T (rows positions, columns queries), so lane l holds 16 of query l %
+// 32's scores and lane l ^ 32 the other 16: the online-softmax maximum and
+// sum of a query are a 16-register reduction and one swap between the
+// wave's halves.  In the same registers exp(S^T - m) is the A operand of P V
+// (the pair index of the MFMA k step is the half of the wave in both), so P
+// is never moved; the per-query rescale factors reach the output rows
+// through a 32-float LDS transpose.  Q stays in registers.  LDS rows are
+// padded (K pitch 260, V pitch 264 floats) so the K row reads of 16 lanes
+// and the V column reads of the two wave halves fall in distinct banks.
+// Scores are q . k / sqrt(AD) as engine.cpp:344-361; AD a multiple of 32, at
+// most 256.
 constexpr int kFlashQ = 32;
+constexpr int kFlashWaves = 4;
+constexpr int kFlashKPitch = 260, kFlashVPitch = 264;
+constexpr size_t kFlashLds =
+    (2 * kFlashQ * (kFlashKPitch + kFlashVPitch) + kFlashWaves * kFlashQ) * sizeof(float);
 
-__global__ __launch_bounds__(kWave, 1) void attention_prefill_kernel(
+__global__ __launch_bounds__(kFlashWaves * kWave, 1) void attention_prefill_kernel(
     const float* __restrict__ query, const float* __restrict__ gate, const float* __restrict__ key_cache,
     const float* __restrict__ value_cache, const int* __restrict__ position, float* __restrict__ out, int AH,
     int KVH, int AD, int count) {
-    __shared__ float row_scale[kFlashQ];
-    const int head = blockIdx.x, q0 = blockIdx.y * kFlashQ;
-    const int G = AH / KVH, kv = head / G;
+    extern __shared__ __attribute__((aligned(16))) float flash_lds[];
+    float* const kl = flash_lds;                                  // [2][32][kFlashKPitch]
+    float* const vl = kl + 2 * kFlashQ * kFlashKPitch;            // [2][32][kFlashVPitch]
+    const int G = AH / KVH;
+    const int subs = (G + kFlashWaves - 1) / kFlashWaves;
+    const int kv = blockIdx.x / subs, sub = blockIdx.x % subs;
+    const int q0 = (gridDim.y - 1 - blockIdx.y) * kFlashQ;  // longest tiles first
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x & (kWave - 1), li = lane & 31, kh = lane >> 5;
+    float* const row_scale = vl + 2 * kFlashQ * kFlashVPitch + wave * kFlashQ;
+    const int hg = sub * kFlashWaves + wave;  // head within the KV head's group
+    const bool active = hg < G;
+    const int head = kv * G + (active ? hg : 0);
     const int AS = AH * AD, NB = AD / 32;
     const size_t KVW = static_cast<size_t>(KVH) * AD;
-    const int lane = threadIdx.x, li = lane & 31, kh = lane >> 5;
     const int p0 = *position;
     const int rows = min(kFlashQ, count - q0);
     const int last = p0 + q0 + rows - 1;  // the tile's last query position
     const int my_pos = p0 + q0 + li;      // this lane's query (S^T column)
     const bool my_valid = li < rows;
     const float divisor = sqrtf(static_cast<float>(AD));
-    // Q row li, dims 32 b + 16 kh + (0 .. 15) of each 32-dim block b.
+
+    // Rows of block b0 into buffer `buf`: wave w copies K and V rows 8 w ..
+    // 8 w + 7 (positions past `last` repeat row `last`; their scores are
+    // masked and their weights are zero).  Each row is one 16-byte-per-lane
+    // load of AD floats; lanes past the row read zeros.
+    auto copy_block = [&](int b0, int buf) {
+#pragma unroll
+        for (int r = 0; r < kFlashQ / kFlashWaves; ++r) {
+            const int p = wave * (kFlashQ / kFlashWaves) + r;
+            const size_t at = static_cast<size_t>(min(b0 + p, last)) * KVW + static_cast<size_t>(kv) * AD;
+            const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(key_cache + at), 0, AD * 4, kBufferFlags);
+            const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(value_cache + at), 0, AD * 4, kBufferFlags);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                kr, (__attribute__((address_space(3))) void*)(kl + (buf * kFlashQ + p) * kFlashKPitch), 16, 16 * lane,
+                0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                vr, (__attribute__((address_space(3))) void*)(vl + (buf * kFlashQ + p) * kFlashVPitch), 16, 16 * lane,
+                0, 0, 0);
+        }
+    };
+    copy_block(0, 0);
+
+    // Q row li of this wave's head, dims 32 b + 16 kh + (0 .. 15) of each
+    // 32-dim block b.
     f32x4 qf[8][4];
     {
         const float* qr = query + static_cast<size_t>(q0 + min(li, rows - 1)) * AS + head * AD;
@@ -697,21 +742,28 @@ __global__ __launch_bounds__(kWave, 1) void attention_prefill_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
     float m = -INFINITY, l = 0.0f;  // of query li (the same in lanes li and li + 32)
-    const float* kbase = key_cache + static_cast<size_t>(kv) * AD;
-    const float* vbase = value_cache + static_cast<size_t>(kv) * AD;
-    for (int b0 = 0; b0 <= last; b0 += 32) {
+    int buf = 0;
+    for (int b0 = 0; b0 <= last; b0 += 32, buf ^= 1) {
+        // This block's rows have landed (every wave's copies), and every wave
+        // is done with the other buffer: the next block may overwrite it.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (b0 + 32 <= last) copy_block(b0 + 32, buf ^ 1);
+        if (!active) continue;
+        const float* kb = kl + buf * kFlashQ * kFlashKPitch;
+        const float* vb = vl + buf * kFlashQ * kFlashVPitch;
         // S^T[p][q] for positions b0 + p: two accumulators over alternate
         // 32-dim blocks, so consecutive MFMAs do not wait on each other.
         f32x16 s0, s1;
 #pragma unroll
         for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.0f;
-        const float* kr = kbase + static_cast<size_t>(min(b0 + li, last)) * KVW;
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             if (b < NB) {
                 f32x4 kf[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) kf[j] = *reinterpret_cast<const f32x4*>(kr + 32 * b + 16 * kh + 4 * j);
+                for (int j = 0; j < 4; ++j)
+                    kf[j] = *reinterpret_cast<const f32x4*>(kb + li * kFlashKPitch + 32 * b + 16 * kh + 4 * j);
 #pragma unroll
                 for (int st = 0; st < 16; ++st) {
                     if (b & 1)
@@ -759,17 +811,16 @@ __global__ __launch_bounds__(kWave, 1) void attention_prefill_kernel(
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             if (t < NB) {
-                float vb[16];
+                float vv[16];
 #pragma unroll
-                for (int u = 0; u < 16; ++u) {
-                    const int p = min(b0 + 8 * (u >> 2) + 4 * kh + (u & 3), last);
-                    vb[u] = vbase[static_cast<size_t>(p) * KVW + 32 * t + li];
-                }
+                for (int u = 0; u < 16; ++u)
+                    vv[u] = vb[(8 * (u >> 2) + 4 * kh + (u & 3)) * kFlashVPitch + 32 * t + li];
 #pragma unroll
-                for (int u = 0; u < 16; ++u) o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(sc[u], vb[u], o[t], 0, 0, 0);
+                for (int u = 0; u < 16; ++u) o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(sc[u], vv[u], o[t], 0, 0, 0);
             }
         }
     }
+    if (!active) return;
     // out = O / l * sigmoid(gate) for the tile's valid rows.
     if (kh == 0) row_scale[li] = my_valid ? 1.0f / l : 0.0f;
     wave_lds_sync();
@@ -1156,9 +1207,10 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                 hipLaunchKernelGGL(attention_combine_kernel, dim3(c.AH, 1), dim3(kHeadThreads), 0, s, e.scores,
                                    e.gate, e.attn_out, c.AH, c.AD);
             } else {
-                hipLaunchKernelGGL(attention_prefill_kernel, dim3(c.AH, (count + kFlashQ - 1) / kFlashQ), dim3(kWave),
-                                   0, s, e.query, e.gate, L.key_cache, L.value_cache, e.d_position, e.attn_out, c.AH,
-                                   c.KVH, c.AD, count);
+                const int subs = (c.AH / c.KVH + kFlashWaves - 1) / kFlashWaves;
+                hipLaunchKernelGGL(attention_prefill_kernel, dim3(c.KVH * subs, (count + kFlashQ - 1) / kFlashQ),
+                                   dim3(kFlashWaves * kWave), kFlashLds, s, e.query, e.gate, L.key_cache,
+                                   L.value_cache, e.d_position, e.attn_out, c.AH, c.KVH, c.AD, count);
             }
             rc = apply(L.o, type, e.attn_out, count, e.hidden, true, s);
         }
@@ -1400,7 +1452,10 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
     }
     if (rc == Q3X_HIP_OK) {
         plan(static_cast<uint8_t*>(e->arena));
-        if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(attention_prefill_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(kFlashLds)) != hipSuccess ||
+            hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
             hipHostMalloc(reinterpret_cast<void**>(&e->h_tokens), sizeof(int) * (2 + e->token_capacity),
                           hipHostMallocDefault) != hipSuccess ||
             hipMemsetAsync(e->arena, 0, total, e->stream) != hipSuccess ||
