@@ -349,47 +349,65 @@ __global__ __launch_bounds__(128) void delta_prep_kernel(float* __restrict__ qkv
     }
 }
 
-// delta_scan_kernel: one workgroup of 8 waves per value head; lane l of
-// wave w owns value column 16 w + l / 4 and keys 32 (l % 4) .. + 31, its
-// S entries in registers across the tokens.  A column's four key groups sit
-// in one quad of lanes, so the sums over keys (k S before the update, q S
-// after it) are two DPP adds: the tokens run with no barrier between them.
-// q, k and v of kScanTile tokens are staged in LDS at a time, the next
-// tile's loads in flight while the current one is processed.
-constexpr int kScanThreads = 512;
-constexpr int kScanKeys = 32;  // keys per thread
-constexpr int kScanLoads = 3 * kScanTile * 128 / kScanThreads;  // staged values per thread per tile
+// delta_scan_kernel: the value columns of a head update independently, so
+// a head's 128 columns are split over kScanSlices workgroups of 4 waves
+// (spreading the recurrence's arithmetic over that many CUs).  Lane l of
+// wave w owns value column 32 slice + 8 w + l / 8 and keys 16 (l % 8) .. +
+// 15, its S entries in registers across the tokens.  A column's eight key
+// groups sit in one row half of lanes, so the sums over keys (k S before the
+// update, q S after it) are three DPP adds: the tokens run with no barrier
+// between them.  Per key and token: k S, the decayed update S e^decay + k
+// (beta delta), and q S -- the decay multiplies k S once instead of every S
+// entry before it.  q, k and the slice's v of kScanTile tokens are staged in
+// LDS at a time, the next tile's loads in flight while the current one is
+// processed.
+constexpr int kScanThreads = 256;
+constexpr int kScanCols = 32;                         // value columns per workgroup
+constexpr int kScanSlices = 128 / kScanCols;          // workgroups per value head
+constexpr int kScanGroups = 8;                        // key groups per column (lanes)
+constexpr int kScanKeys = 128 / kScanGroups;          // keys per lane
+constexpr int kScanValues = (2 * 128 + kScanCols) * kScanTile;  // staged values per tile
+constexpr int kScanLoads = kScanValues / kScanThreads;          // per thread
 
 __global__ __launch_bounds__(kScanThreads) void delta_scan_kernel(const float* __restrict__ qkv,
                                                                   const float* __restrict__ scale,
                                                                   const float* __restrict__ beta,
                                                                   float* __restrict__ memory, float* __restrict__ out,
                                                                   int KH, int VH, int KD, int VD, int count) {
-    // [q | k | v] of the tile's tokens, 128 slots each (zeros past KD / VD).
-    __shared__ __attribute__((aligned(16))) float tile[3][kScanTile][128];
+    // q | k of the tile's tokens (128 slots each, zeros past KD), then the
+    // slice's v (zeros past VD).
+    __shared__ __attribute__((aligned(16))) float tile[kScanValues];
     __shared__ float st[kScanTile], bt[kScanTile];
-    const int head = blockIdx.x;
+    const float* const qt = tile;
+    const float* const kt = tile + kScanTile * 128;
+    const float* const vt = tile + 2 * kScanTile * 128;
+    const int head = blockIdx.x / kScanSlices, slice = blockIdx.x % kScanSlices;
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1), wave = t / kWave;
     const int DQK = KH * KD, DO = VH * VD, DQKV = 2 * DQK + DO;
     const int kh = head / (VH / KH);
-    const int c = wave * 16 + lane / 4, k0 = (lane & 3) * kScanKeys;
+    const int cl = wave * (kWave / kScanGroups) + lane / kScanGroups;  // column within the slice
+    const int c = slice * kScanCols + cl, k0 = (lane % kScanGroups) * kScanKeys;
     const bool col = c < VD;
     float* S = memory + (static_cast<size_t>(head) * VD + (col ? c : 0)) * KD;  // column c
     float s[kScanKeys];
     load_keys<kScanKeys>(S, k0, KD, col, s);
-    // Value e = t + i * kScanThreads of a tile: array e / (kScanTile * 128),
-    // token (e / 128) % kScanTile, slot e % 128.
     float pre[kScanLoads], pst = 0.0f, pbt = 0.0f;
     auto load_tile = [&](int r0) {
         const int nt = min(kScanTile, count - r0);
 #pragma unroll
         for (int i = 0; i < kScanLoads; ++i) {
             const int e = t + i * kScanThreads;
-            const int arr = e / (kScanTile * 128), rr = (e / 128) % kScanTile, k = e % 128;
-            const float* row = qkv + static_cast<size_t>(r0 + rr) * DQKV;
-            const int off = arr == 0 ? kh * KD + k : arr == 1 ? DQK + kh * KD + k : 2 * DQK + head * VD + k;
-            pre[i] = rr < nt && k < (arr == 2 ? VD : KD) ? row[off] : 0.0f;
+            float x = 0.0f;
+            if (e < 2 * kScanTile * 128) {
+                const int arr = e / (kScanTile * 128), rr = (e / 128) % kScanTile, k = e % 128;
+                if (rr < nt && k < KD)
+                    x = qkv[static_cast<size_t>(r0 + rr) * DQKV + (arr == 0 ? 0 : DQK) + kh * KD + k];
+            } else {
+                const int v = e - 2 * kScanTile * 128, rr = v / kScanCols, cc = slice * kScanCols + v % kScanCols;
+                if (rr < nt && cc < VD) x = qkv[static_cast<size_t>(r0 + rr) * DQKV + 2 * DQK + head * VD + cc];
+            }
+            pre[i] = x;
         }
         if (t < nt) {
             pst = scale[static_cast<size_t>(r0 + t) * VH + head];
@@ -401,7 +419,7 @@ __global__ __launch_bounds__(kScanThreads) void delta_scan_kernel(const float* _
         const int nt = min(kScanTile, count - r0);
         __syncthreads();  // the previous tile is consumed
 #pragma unroll
-        for (int i = 0; i < kScanLoads; ++i) (&tile[0][0][0])[t + i * kScanThreads] = pre[i];
+        for (int i = 0; i < kScanLoads; ++i) tile[t + i * kScanThreads] = pre[i];
         if (t < kScanTile) {
             st[t] = pst;
             bt[t] = pbt;
@@ -409,35 +427,32 @@ __global__ __launch_bounds__(kScanThreads) void delta_scan_kernel(const float* _
         __syncthreads();
         if (r0 + kScanTile < count) load_tile(r0 + kScanTile);
         for (int rr = 0; rr < nt; ++rr) {
-            const f32x4* kp = reinterpret_cast<const f32x4*>(&tile[1][rr][k0]);
-            const f32x4* qp = reinterpret_cast<const f32x4*>(&tile[0][rr][k0]);
+            const f32x4* kp = reinterpret_cast<const f32x4*>(kt + rr * 128 + k0);
+            const f32x4* qp = reinterpret_cast<const f32x4*>(qt + rr * 128 + k0);
             const float sc = st[rr], bb = bt[rr];
-            const float vv = tile[2][rr][c < 128 ? c : 0];
+            const float vv = vt[rr * kScanCols + cl];
             float p0 = 0.0f, p1 = 0.0f;
 #pragma unroll
             for (int j4 = 0; j4 < kScanKeys / 4; ++j4) {
                 const f32x4 kk = kp[j4];
-                s[4 * j4 + 0] *= sc;
-                s[4 * j4 + 1] *= sc;
-                s[4 * j4 + 2] *= sc;
-                s[4 * j4 + 3] *= sc;
                 p0 = fmaf(kk.x, s[4 * j4 + 0], p0);
                 p1 = fmaf(kk.y, s[4 * j4 + 1], p1);
                 p0 = fmaf(kk.z, s[4 * j4 + 2], p0);
                 p1 = fmaf(kk.w, s[4 * j4 + 3], p1);
             }
             float pred = p0 + p1;
-            pred += dpp_f32<0xB1>(pred);  // the quad's four key groups
-            pred += dpp_f32<0x4E>(pred);
-            const float delta = vv - pred;
+            pred += dpp_f32<0xB1>(pred);   // the eight key groups: pairs,
+            pred += dpp_f32<0x4E>(pred);   // quads,
+            pred += dpp_f32<0x141>(pred);  // the two quads of the row half
+            const float bd = bb * (vv - sc * pred);  // beta (v - k S e^decay)
             float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
             for (int j4 = 0; j4 < kScanKeys / 4; ++j4) {
                 const f32x4 kk = kp[j4], qq = qp[j4];
-                s[4 * j4 + 0] = fmaf(kk.x * bb, delta, s[4 * j4 + 0]);
-                s[4 * j4 + 1] = fmaf(kk.y * bb, delta, s[4 * j4 + 1]);
-                s[4 * j4 + 2] = fmaf(kk.z * bb, delta, s[4 * j4 + 2]);
-                s[4 * j4 + 3] = fmaf(kk.w * bb, delta, s[4 * j4 + 3]);
+                s[4 * j4 + 0] = fmaf(s[4 * j4 + 0], sc, kk.x * bd);
+                s[4 * j4 + 1] = fmaf(s[4 * j4 + 1], sc, kk.y * bd);
+                s[4 * j4 + 2] = fmaf(s[4 * j4 + 2], sc, kk.z * bd);
+                s[4 * j4 + 3] = fmaf(s[4 * j4 + 3], sc, kk.w * bd);
                 o0 = fmaf(qq.x, s[4 * j4 + 0], o0);
                 o1 = fmaf(qq.y, s[4 * j4 + 1], o1);
                 o0 = fmaf(qq.z, s[4 * j4 + 2], o0);
@@ -446,7 +461,8 @@ __global__ __launch_bounds__(kScanThreads) void delta_scan_kernel(const float* _
             float o = o0 + o1;
             o += dpp_f32<0xB1>(o);
             o += dpp_f32<0x4E>(o);
-            if ((lane & 3) == 0 && col) out[static_cast<size_t>(r0 + rr) * DO + head * VD + c] = o;
+            o += dpp_f32<0x141>(o);
+            if (lane % kScanGroups == 0 && col) out[static_cast<size_t>(r0 + rr) * DO + head * VD + c] = o;
         }
     }
     store_keys<kScanKeys>(S, k0, KD, col, s);
@@ -1190,8 +1206,8 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
             } else {
                 hipLaunchKernelGGL(delta_prep_kernel, dim3(c.KH, count), dim3(128), 0, s, e.qkv, e.a, e.b, L.alog,
                                    L.dt, c.KH, c.VH, c.KD, c.VD);
-                hipLaunchKernelGGL(delta_scan_kernel, dim3(c.VH), dim3(kScanThreads), 0, s, e.qkv, e.a, e.b,
-                                   L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD, count);
+                hipLaunchKernelGGL(delta_scan_kernel, dim3(c.VH * kScanSlices), dim3(kScanThreads), 0, s, e.qkv,
+                                   e.a, e.b, L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD, count);
                 hipLaunchKernelGGL(delta_norm_kernel, dim3(c.VH, count), dim3(128), 0, s, e.delta_out, e.z, L.norm,
                                    c.VH, c.VD);
             }
