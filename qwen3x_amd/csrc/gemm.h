@@ -18,6 +18,8 @@
 // ds_read_b128.
 #pragma once
 
+#include <utility>
+
 #include "common.h"
 
 namespace q3x {
@@ -109,6 +111,19 @@ struct Mfma16 { static constexpr bool value = false; };
 template <class P>
 struct Mfma16<P, decltype(void(P::kMfma16))> { static constexpr bool value = P::kMfma16; };
 
+// Policy::linear_total() (optional, with kLinearGrid): the number of tiles
+// of a 1-D grid that is sized for the most tiles possible (a grouped GEMM's
+// tile count is known only on the device); workgroups past it return, and
+// the XCD remap spreads the live tiles.  Default: the grid size.
+template <class P, class = void>
+struct LinearTotal {
+    __device__ static int get(const P&, int grid) { return grid; }
+};
+template <class P>
+struct LinearTotal<P, decltype(void(std::declval<const P&>().linear_total()))> {
+    __device__ static int get(const P& p, int) { return p.linear_total(); }
+};
+
 // WM x WN waves, each TM x TN tiles of 32x32.  Policy supplies the tile
 // geometry, A rows, weight rows and the output store (see dense / grouped
 // policies).  Grid: x = weight-row tiles (BN), y = A-row tiles (BM).
@@ -141,7 +156,8 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
     // consecutive x) then share one XCD's L2.
     int bx = blockIdx.x, by = blockIdx.y;
     if constexpr (Policy::kLinearGrid) {
-        const int total = gridDim.x, L = blockIdx.x;
+        const int total = LinearTotal<Policy>::get(pol, gridDim.x), L = blockIdx.x;
+        if (L >= total) return;
         const int q = total / kXcds, r = total % kXcds, xcd = L % kXcds, k = L / kXcds;
         const int t = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + k;
         bx = t % pol.tiles_x;

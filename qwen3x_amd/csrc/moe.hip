@@ -249,11 +249,14 @@ __global__ __launch_bounds__(kChunk) void moe_scatter_kernel(const int* __restri
 // gathered (a_index[position] = source row) or taken in position order; the
 // weights are expert tile_expert[ty] of the pool; out[position, n].
 struct GroupedGemm {
-    static constexpr bool kLinearGrid = false;
+    // A 1-D grid sized for the most tiles possible; the live ones, *ntiles
+    // A-row tiles times tiles_x, are remapped so that the weight-row tiles of
+    // one A-row tile (which read the same gathered A rows) share an XCD.
+    static constexpr bool kLinearGrid = true;
     static constexpr bool kPairedColumns = false;
     static constexpr bool kPartialTiles = true;  // every expert's last tile is short
     static constexpr bool kMfma16 = true;        // skip 16-row halves past the valid pairs
-    int tiles_x;  // unused (2-D grid)
+    int tiles_x;  // weight-row tiles
     const float* A;
     int a_cols;
     const int* a_index;
@@ -266,6 +269,7 @@ struct GroupedGemm {
     const int* ntiles;
     float* out;
     int out_cols;
+    __device__ int linear_total() const { return *ntiles * tiles_x; }
     __device__ bool tile(int ty, int, GemmTile& t) const {
         if (ty >= *ntiles) return false;
         t.group = tile_expert[ty];
@@ -667,20 +671,20 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
     if (I % 64 == 0) {
         // SwiGLU in the gate_up epilogue: h directly.
         GroupedGateUp g1{};
-        static_cast<GroupedGemm&>(g1) = GroupedGemm{0, X, H, src_token, gate_up, gu_row * 2 * I, gu_row,
+        const int nx = 2 * I / kGrpBN;
+        static_cast<GroupedGemm&>(g1) = GroupedGemm{nx, X, H, src_token, gate_up, gu_row * 2 * I, gu_row,
                                                     tile_expert, tile_start, tile_count, ntiles, nullptr, 0};
         g1.I = I;
         g1.h = h;
         hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGateUp, kTilePF<QT>>),
-                           dim3(2 * I / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0, stream, g1, 2 * I,
-                           H);
+                           dim3(nx * tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0, stream, g1, 2 * I, H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
     } else {
-        GroupedGemm g1{0, X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
+        const int nx = (2 * I + kGrpBN - 1) / kGrpBN;
+        GroupedGemm g1{nx, X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
                        ntiles, gu, 2 * I};
         hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm, kTilePF<QT>>),
-                           dim3((2 * I + kGrpBN - 1) / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0,
-                           stream, g1, 2 * I, H);
+                           dim3(nx * tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0, stream, g1, 2 * I, H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
         const size_t sw = static_cast<size_t>(P) * I;
         const int sw_blocks = static_cast<int>(std::min<size_t>((sw + 255) / 256, 65536));
@@ -688,11 +692,11 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
                            static_cast<const int*>(nvalid));
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
     }
-    GroupedGemm g2{0, h, I, nullptr, down, down_row * H, down_row, tile_expert, tile_start, tile_count,
+    const int nx2 = (H + kGrpBN - 1) / kGrpBN;
+    GroupedGemm g2{nx2, h, I, nullptr, down, down_row * H, down_row, tile_expert, tile_start, tile_count,
                    ntiles, d, H};
     hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm, kTilePF<QT>>),
-                       dim3((H + kGrpBN - 1) / kGrpBN, tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0,
-                       stream, g2, H, I);
+                       dim3(nx2 * tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0, stream, g2, H, I);
     if ((status = launch_status()) != Q3X_HIP_OK) return status;
     const size_t outs = static_cast<size_t>(tokens) * H;
     if (H % 4 == 0 && aligned(Y, 16)) {
