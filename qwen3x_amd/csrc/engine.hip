@@ -579,6 +579,23 @@ __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
     const float* vbase = value_cache + static_cast<size_t>(kv) * AD;
     const float divisor = sqrtf(static_cast<float>(AD));
     const bool kl = 4 * lane < AD;
+    // Every K and V load of a block, requested together; the first block's
+    // go out before q is read (their addresses do not depend on it).
+    float vr[kAttnBlock];
+    f32x4 kr[kRows];
+    auto load_block = [&](int b0) {
+        const int nb = min(kAttnBlock, t1 - b0);
+#pragma unroll
+        for (int j = 0; j < kAttnBlock; ++j)
+            vr[j] = j < nb && i < AD ? vbase[static_cast<size_t>(b0 + j) * KVW + i] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < kRows; ++u) {
+            const int j = u * kWaves + wave;
+            kr[u] = j < nb && kl ? *reinterpret_cast<const f32x4*>(kbase + static_cast<size_t>(b0 + j) * KVW + 4 * lane)
+                                 : f32x4{0, 0, 0, 0};
+        }
+    };
+    if (t0 < t1) load_block(t0);
     f32x4 q[kMaxGroup];
 #pragma unroll
     for (int g = 0; g < kMaxGroup; ++g)
@@ -593,17 +610,7 @@ __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
     __syncthreads();
     for (int b0 = t0; b0 < t1; b0 += kAttnBlock) {
         const int nb = min(kAttnBlock, t1 - b0);
-        float vr[kAttnBlock];
-#pragma unroll
-        for (int j = 0; j < kAttnBlock; ++j)
-            vr[j] = j < nb && i < AD ? vbase[static_cast<size_t>(b0 + j) * KVW + i] : 0.0f;
-        f32x4 kr[kRows];
-#pragma unroll
-        for (int u = 0; u < kRows; ++u) {
-            const int j = u * kWaves + wave;
-            kr[u] = j < nb && kl ? *reinterpret_cast<const f32x4*>(kbase + static_cast<size_t>(b0 + j) * KVW + 4 * lane)
-                                 : f32x4{0, 0, 0, 0};
-        }
+        if (b0 != t0) load_block(b0);
 #pragma unroll
         for (int u = 0; u < kRows; ++u) {
             const int j = u * kWaves + wave;
