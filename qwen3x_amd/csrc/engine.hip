@@ -4,11 +4,14 @@
 // Follows the reference's forward (engine.cpp:431-454) layer for layer:
 // embedding; per layer RMSNorm, the mixer (gated DeltaNet, engine.cpp:
 // 274-316, or full attention, :318-362), residual, RMSNorm, FFN or MoE,
-// residual; final RMSNorm and lm_head.  The matrices go through this
-// library's own entry points (q3x_hip_mv_multi for the projection groups,
-// q3x_hip_mv with accumulate for the output projections, which adds the
-// residual in the same operation, q3x_hip_moe_layer for MoE layers); the
-// kernels here are the small per-token operations between them.
+// residual; final RMSNorm and lm_head.  A decode step runs each projection
+// group (and lm_head) as one launch of the pipelined matvec (matvec.h) whose
+// input staging forms the preceding RMSNorm or SwiGLU on the way into LDS
+// (NormInput, SwiGLUInput below); output projections and down accumulate
+// into the residual, and an MoE layer adds its output to it directly
+// (moe.h).  A chunk goes through this library's own entry points
+// (q3x_hip_gemm, q3x_hip_moe_layer).  The kernels here are the per-token
+// operations between the matrices.
 //
 // Every buffer lives on the device for the life of the engine: the work
 // rows, the DeltaNet recurrent state (conv history and the KD x VD memory of
@@ -18,10 +21,11 @@
 // replayed for every token, as the reference captures its step
 // (arch/cuda/engine.cu:1995-2005).  A forward of several tokens runs them
 // as chunks of up to kChunk rows: the matrices as prefill GEMMs
-// (q3x_hip_gemm, q3x_hip_moe_layer's grouped path), the conv and delta rule
-// token by token inside one launch with the state in registers, norms, RoPE
-// and attention over all rows at once -- the role of the reference's
-// prefill_chunk_* (arch/cuda/engine.cu:1881-1960).
+// (q3x_hip_gemm, q3x_hip_moe_layer's grouped path), the conv over runs of
+// tokens and the delta-rule recurrence token by token with the state in
+// registers, norms, RoPE and attention (FP32 MFMA) over all rows at once --
+// the role of the reference's prefill_chunk_* (arch/cuda/engine.cu:
+// 1881-1960).
 #include <math.h>
 
 #include <algorithm>
