@@ -136,22 +136,30 @@ __global__ __launch_bounds__(kNormThreads) void rms_kernel(float* __restrict__ h
 // before its run (the previous run's last rows, or the remembered history for
 // the first tokens); after one barrier the runs are convolved in place and
 // the thread holding the last token leaves the last CK - 1 raw inputs as the
-// new history.  The arithmetic per token is the reference's.  SEGMENTS: 16
-// for a chunk, 1 for a decode step (256 channels per workgroup).
+// new history.  The arithmetic per token is the reference's (conv_token).
+// The history is kept in two copies, [2][channels][CK - 1]: a forward at
+// position p reads copy p % 2 and leaves copy (p + count) % 2, so a decode
+// step (delta_rule_kernel, which convolves its own channels) can read the
+// old history of a channel that another workgroup is updating.  SEGMENTS: 16
+// runs per channel.
 constexpr int kMaxConv = 8;
 constexpr int kConvThreads = 256;
 template <int SEGMENTS>
 __global__ __launch_bounds__(kConvThreads) void delta_conv_kernel(float* __restrict__ qkv,
                                                                   const uint16_t* __restrict__ w,
-                                                                  float* __restrict__ history, int channels, int CK,
-                                                                  int count) {
+                                                                  float* __restrict__ history,
+                                                                  const int* __restrict__ position, int channels,
+                                                                  int CK, int count) {
     constexpr int kChannels = kConvThreads / SEGMENTS;
     const int c = blockIdx.x * kChannels + threadIdx.x % kChannels;
     const int segment = threadIdx.x / kChannels;
     const bool ok = c < channels;
     const int per = (count + SEGMENTS - 1) / SEGMENTS;
     const int t0 = min(count, segment * per), t1 = min(count, t0 + per);
-    float* hist = history + static_cast<size_t>(ok ? c : 0) * (CK - 1);
+    const int p0 = *position;
+    const size_t copy = static_cast<size_t>(channels) * (CK - 1);
+    const float* hist = history + (p0 & 1) * copy + static_cast<size_t>(ok ? c : 0) * (CK - 1);
+    float* hist_out = history + ((p0 + count) & 1) * copy + static_cast<size_t>(ok ? c : 0) * (CK - 1);
     float past[kMaxConv - 1], wt[kMaxConv];
 #pragma unroll
     for (int i = 0; i < kMaxConv; ++i) wt[i] = ok && i < CK ? bf16_value(w[static_cast<size_t>(c) * CK + i]) : 0.0f;
@@ -193,8 +201,31 @@ __global__ __launch_bounds__(kConvThreads) void delta_conv_kernel(float* __restr
     if (t0 < t1 && t1 == count) {
 #pragma unroll
         for (int i = 0; i < kMaxConv - 1; ++i)
-            if (i < CK - 1) hist[i] = past[i];
+            if (i < CK - 1) hist_out[i] = past[i];
     }
+}
+
+// One token of the causal conv of one channel, then SiLU (the arithmetic of
+// delta_conv_kernel): the CK - 1 remembered inputs from `hist`, the weights
+// w[0 .. CK - 1] (BF16); the shifted history goes to `hist_out` if not null.
+__device__ __forceinline__ float conv_token(float x, const float* hist, const uint16_t* w, int CK, float* hist_out) {
+    float past[kMaxConv - 1];
+#pragma unroll
+    for (int i = 0; i < kMaxConv - 1; ++i) past[i] = i < CK - 1 ? hist[i] : 0.0f;
+    float last = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxConv; ++i)
+        if (i == CK - 1) last = bf16_value(w[i]);
+    float sum = x * last;
+#pragma unroll
+    for (int i = 0; i < kMaxConv - 1; ++i)
+        if (i < CK - 1) sum = fmaf(past[i], bf16_value(w[i]), sum);
+    if (hist_out) {
+#pragma unroll
+        for (int i = 0; i < kMaxConv - 1; ++i)
+            if (i < CK - 1) hist_out[i] = i + 1 < CK - 1 ? past[i + 1] : x;
+    }
+    return silu_ref(sum);
 }
 
 // The DeltaNet memory S of a value head is stored column by column,
@@ -241,8 +272,9 @@ constexpr int kDeltaKeys = 128 / kDeltaGroups;     // keys per thread
 __global__ __launch_bounds__(kDeltaThreads) void delta_rule_kernel(
     const float* __restrict__ qkv, const float* __restrict__ a, const float* __restrict__ b,
     const float* __restrict__ z, const float* __restrict__ alog, const uint16_t* __restrict__ dt,
-    const float* __restrict__ norm, float* __restrict__ memory, float* __restrict__ out, int KH, int VH, int KD,
-    int VD, int count) {
+    const float* __restrict__ norm, float* __restrict__ memory, float* __restrict__ out,
+    const uint16_t* __restrict__ conv_w, float* __restrict__ history, const int* __restrict__ position, int CK,
+    int KH, int VH, int KD, int VD) {
     __shared__ float qs[128], ks[128], part[kDeltaGroups][128], sum[128], partial[kDeltaThreads / kWave];
     const int head = blockIdx.x;
     const int t = threadIdx.x;
@@ -256,11 +288,30 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_rule_kernel(
     const float A = expf(alog[head]);
     const float bias = bf16_value(dt[head]);
     const float nv = norm[t < VD ? t : 0];
-    for (int r = 0; r < count; ++r) {
+    // The causal conv of this head's channels (q and k of its key head, its
+    // v), read from history copy p % 2; the new history goes to copy (p + 1)
+    // % 2 -- for q and k only from the key head's first value head.
+    const int pos = *position;
+    const size_t copy = static_cast<size_t>(DQKV) * (CK - 1);
+    const float* hin = history + (pos & 1) * copy;
+    float* hout = history + ((pos + 1) & 1) * copy;
+    const bool qk_writer = head % (VH / KH) == 0;
+    {
+        const int r = 0;
         const float* row = qkv + static_cast<size_t>(r) * DQKV;
-        const float qv = t < KD ? row[kh * KD + t] : 0.0f;
-        const float kv = t < KD ? row[DQK + kh * KD + t] : 0.0f;
-        const float vv = col ? row[2 * DQK + head * VD + v] : 0.0f;
+        const int cq = kh * KD + t, ck = DQK + kh * KD + t, cv = 2 * DQK + head * VD + v;
+        const float qv = t < KD ? conv_token(row[cq], hin + static_cast<size_t>(cq) * (CK - 1),
+                                             conv_w + static_cast<size_t>(cq) * CK, CK,
+                                             qk_writer ? hout + static_cast<size_t>(cq) * (CK - 1) : nullptr)
+                                : 0.0f;
+        const float kv = t < KD ? conv_token(row[ck], hin + static_cast<size_t>(ck) * (CK - 1),
+                                             conv_w + static_cast<size_t>(ck) * CK, CK,
+                                             qk_writer ? hout + static_cast<size_t>(ck) * (CK - 1) : nullptr)
+                                : 0.0f;
+        const float vv = col ? conv_token(row[cv], hin + static_cast<size_t>(cv) * (CK - 1),
+                                          conv_w + static_cast<size_t>(cv) * CK, CK,
+                                          group == 0 ? hout + static_cast<size_t>(cv) * (CK - 1) : nullptr)
+                             : 0.0f;
         const float qn = block_sum<kDeltaThreads>(qv * qv, partial);
         const float kn = block_sum<kDeltaThreads>(kv * kv, partial);
         if (t < KD) {
@@ -1058,7 +1109,7 @@ struct LayerWeights {
     const uint16_t *qnorm = nullptr, *knorm = nullptr;
     Mat gate, up, down;  // dense FFN
     q3x_hip_moe_layer_weights moe{};
-    float* conv_state = nullptr;  // DeltaNet: [DQKV, CK - 1]
+    float* conv_state = nullptr;  // DeltaNet: [2][DQKV, CK - 1] (copies by position parity)
     float* memory = nullptr;      //           [VH, VD, KD] (column by column)
     float* key_cache = nullptr;   // attention: [capacity, KVH, AD]
     float* value_cache = nullptr;
@@ -1205,16 +1256,15 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
         }
         if (rc) break;
         if (!L.attention) {
-            if (count == 1)
-                hipLaunchKernelGGL(delta_conv_kernel<1>, dim3((DQKV + kConvThreads - 1) / kConvThreads),
-                                   dim3(kConvThreads), 0, s, e.qkv, L.conv, L.conv_state, DQKV, c.CK, count);
-            else
-                hipLaunchKernelGGL(delta_conv_kernel<16>, dim3((DQKV + kConvThreads / 16 - 1) / (kConvThreads / 16)),
-                                   dim3(kConvThreads), 0, s, e.qkv, L.conv, L.conv_state, DQKV, c.CK, count);
             if (count == 1) {
+                // The conv of the step's channels runs inside the delta rule.
                 hipLaunchKernelGGL(delta_rule_kernel, dim3(c.VH), dim3(kDeltaThreads), 0, s, e.qkv, e.a, e.b, e.z,
-                                   L.alog, L.dt, L.norm, L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD, 1);
+                                   L.alog, L.dt, L.norm, L.memory, e.delta_out, L.conv, L.conv_state, e.d_position,
+                                   c.CK, c.KH, c.VH, c.KD, c.VD);
             } else {
+                hipLaunchKernelGGL(delta_conv_kernel<16>, dim3((DQKV + kConvThreads / 16 - 1) / (kConvThreads / 16)),
+                                   dim3(kConvThreads), 0, s, e.qkv, L.conv, L.conv_state, e.d_position, DQKV, c.CK,
+                                   count);
                 hipLaunchKernelGGL(delta_prep_kernel, dim3(c.KH, count), dim3(128), 0, s, e.qkv, e.a, e.b, L.alog,
                                    L.dt, c.KH, c.VH, c.KD, c.VD);
                 hipLaunchKernelGGL(delta_scan_kernel, dim3(c.VH * kScanSlices), dim3(kScanThreads), 0, s, e.qkv,
@@ -1403,7 +1453,7 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
                                           c.experts, c.top_k, c.H, c.I, c.shared_I};
     const int DQK = c.KH * c.KD, DO = c.VH * c.VD, DQKV = 2 * DQK + DO;
     const int AS = c.AH * c.AD, KVW = c.KVH * c.AD;
-    const size_t conv = static_cast<size_t>(DQKV) * (c.CK - 1);
+    const size_t conv = 2 * static_cast<size_t>(DQKV) * (c.CK - 1);
     const size_t memory = static_cast<size_t>(c.VH) * c.KD * c.VD;
     const size_t cache = static_cast<size_t>(context) * KVW;
     const int delta_layers = c.N - c.N / c.AI;
