@@ -30,9 +30,11 @@ constexpr int kRouterMaxExperts = 1024;
 constexpr int kRouterMaxTopK = 8;          // q3x_model::MAX_TOP_K (model_config.h:14)
 constexpr int kGroupThreads = 1024;
 constexpr int kChunk = 1024;               // pairs per grouping chunk
-// Grouped GEMM: 2 x 4 waves of one 32x32 tile -> 64 pairs x 128 weight rows
-// (measured ahead of 32-pair tiles, which waste fewer rows of an expert's
-// last tile but stream the weights twice as often per pair).
+// Grouped GEMM: 2 x 4 waves of one 32x32 tile -> 64 pairs x 128 weight rows,
+// or of two 32x32 tiles each -> 128 pairs (moe_grouped picks).  64 pairs was
+// measured ahead of 32-pair tiles, which waste fewer rows of an expert's last
+// tile but stream the weights twice as often per pair.  kGrpBM, the smaller
+// tile, bounds the tile count.
 constexpr int kGrpWM = 2, kGrpWN = 4, kGrpTM = 1, kGrpTN = 1;
 constexpr int kGrpBM = kGrpWM * kGrpTM * 32;
 // Register sets for the stages ahead in the 64 x 128 tile GEMMs (measured).
@@ -635,8 +637,8 @@ int moe_decode(const uint8_t* gate_up, const uint8_t* down, int experts, int H, 
     return Q3X_HIP_ENOTSUP;
 }
 
-template <uint32_t QT>
-int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
+template <uint32_t QT, int WM, int TM>
+int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
                 int tokens, const int* ids, const float* weights, int top_k, float* Y, int accumulate,
                 uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
     constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
@@ -658,7 +660,7 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
     int status = launch_status();
     if (status != Q3X_HIP_OK) return status;
     hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(kGroupThreads), 0, stream,
-                       static_cast<const int*>(chunk_counts), L.chunks, experts, kGrpBM, chunk_base, tile_expert,
+                       static_cast<const int*>(chunk_counts), L.chunks, experts, WM * TM * 32, chunk_base, tile_expert,
                        tile_start, tile_count, ntiles, nvalid);
     if ((status = launch_status()) != Q3X_HIP_OK) return status;
     hipLaunchKernelGGL(moe_scatter_kernel, dim3(L.chunks), dim3(kChunk), 0, stream, ids, P, top_k, experts,
@@ -676,15 +678,15 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
                                                     tile_expert, tile_start, tile_count, ntiles, nullptr, 0};
         g1.I = I;
         g1.h = h;
-        hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGateUp, kTilePF<QT>>),
-                           dim3(nx * tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0, stream, g1, 2 * I, H);
+        hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, kGrpWN, TM, kGrpTN, GroupedGateUp, kTilePF<QT>>),
+                           dim3(nx * tiles_bound), dim3(WM * kGrpWN * kWave), 0, stream, g1, 2 * I, H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
     } else {
         const int nx = (2 * I + kGrpBN - 1) / kGrpBN;
         GroupedGemm g1{nx, X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
                        ntiles, gu, 2 * I};
-        hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm, kTilePF<QT>>),
-                           dim3(nx * tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0, stream, g1, 2 * I, H);
+        hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, kGrpWN, TM, kGrpTN, GroupedGemm, kTilePF<QT>>),
+                           dim3(nx * tiles_bound), dim3(WM * kGrpWN * kWave), 0, stream, g1, 2 * I, H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
         const size_t sw = static_cast<size_t>(P) * I;
         const int sw_blocks = static_cast<int>(std::min<size_t>((sw + 255) / 256, 65536));
@@ -695,8 +697,8 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
     const int nx2 = (H + kGrpBN - 1) / kGrpBN;
     GroupedGemm g2{nx2, h, I, nullptr, down, down_row * H, down_row, tile_expert, tile_start, tile_count,
                    ntiles, d, H};
-    hipLaunchKernelGGL((gemm_mfma_kernel<QT, kGrpWM, kGrpWN, kGrpTM, kGrpTN, GroupedGemm, kTilePF<QT>>),
-                       dim3(nx2 * tiles_bound), dim3(kGrpWM * kGrpWN * kWave), 0, stream, g2, H, I);
+    hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, kGrpWN, TM, kGrpTN, GroupedGemm, kTilePF<QT>>),
+                       dim3(nx2 * tiles_bound), dim3(WM * kGrpWN * kWave), 0, stream, g2, H, I);
     if ((status = launch_status()) != Q3X_HIP_OK) return status;
     const size_t outs = static_cast<size_t>(tokens) * H;
     if (H % 4 == 0 && aligned(Y, 16)) {
@@ -707,6 +709,23 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
     hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0,
                        stream, d, pos_of_pair, ids, experts, weights, tokens, top_k, H, Y, accumulate);
     return launch_status();
+}
+
+template <uint32_t QT>
+int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
+                int tokens, const int* ids, const float* weights, int top_k, float* Y, int accumulate,
+                uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
+    // 128-pair tiles (two 32-pair tiles per wave) once an expert averages 32
+    // or more pairs: a routed expert's group is rarely a whole number of
+    // tiles, and every tile streams the expert's weights and pays its stages'
+    // loads and barriers whatever its valid pairs.  At 2048 tokens x top 8 of
+    // 256 experts (64 pairs per expert on average) 128-pair tiles measured
+    // 1.21 ms against 1.32 ms for 64-pair ones (96-pair: 1.24 ms).
+    if (static_cast<long long>(tokens) * top_k >= 32LL * experts)
+        return moe_grouped_tiles<QT, 2, 2>(gate_up, down, experts, H, I, X, tokens, ids, weights, top_k, Y,
+                                           accumulate, ws, L, stream);
+    return moe_grouped_tiles<QT, 2, 1>(gate_up, down, experts, H, I, X, tokens, ids, weights, top_k, Y,
+                                       accumulate, ws, L, stream);
 }
 
 // ------------------------------------------------------------ MoE layer ----
