@@ -42,12 +42,9 @@ struct q3x_hip_engine;
 namespace q3x {
 namespace {
 
-constexpr float kEps = 1e-6f;           // engine.cpp:26 EPS
 constexpr float kTheta = 10000000.0f;   // engine.cpp:26 THETA
 constexpr int kNormThreads = 1024;
 constexpr int kHeadThreads = 256;
-
-__device__ __forceinline__ float bf16_value(uint16_t v) { return __uint_as_float(static_cast<uint32_t>(v) << 16); }
 
 // Sum over the workgroup in a fixed order: each wave's DPP sum, then the
 // wave partials in wave order.  Every thread receives the total.
@@ -963,70 +960,6 @@ __device__ __forceinline__ float* lds_x(uint8_t* xl, int i) {
     return reinterpret_cast<float*>(xl + x_block_offset(i / kBlock) + 4 * (i % kBlock));
 }
 
-// Input staging for a decode step's projections (mv_pipe_kernel's `In`):
-// x = RMSNorm(h) * (1 + w) of the raw residual h (engine.cpp:228-233),
-// formed by every workgroup of the matvec launch on its way into LDS.  Each
-// thread loads its 16-byte chunks of h together with their four norm
-// weights (one round trip; the first kHeld chunks stay in registers) and
-// copies h to LDS; after one barrier every wave sums the squares of all of
-// h from LDS in the same fixed order (lane l takes chunks l, l + 64, ...
-// with FMAs, then the wave's DPP tree), so every wave of every workgroup --
-// whatever the launch shape -- holds the same scale; then each thread
-// scales its own chunks.  Requires w 8-byte aligned.
-struct NormInput {
-    static constexpr int kHeld = 4;
-    const uint16_t* w;
-    __device__ void stage(const float* x, uint8_t* xl, int bpr, float* /*work*/) const {
-        const int chunks = bpr * 8;
-        const int B = blockDim.x;
-        const f32x4* xs = reinterpret_cast<const f32x4*>(x);
-        const uint2* ws = reinterpret_cast<const uint2*>(w);
-        auto at = [&](int c) { return reinterpret_cast<f32x4*>(xl + x_block_offset(c >> 3) + 16 * (c & 7)); };
-        f32x4 xr[kHeld];
-        uint2 wr[kHeld];
-#pragma unroll
-        for (int k = 0; k < kHeld; ++k) {
-            const int c = threadIdx.x + k * B;
-            if (c < chunks) {
-                xr[k] = xs[c];
-                wr[k] = ws[c];
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < kHeld; ++k) {
-            const int c = threadIdx.x + k * B;
-            if (c < chunks) *at(c) = xr[k];
-        }
-        for (int c = threadIdx.x + kHeld * B; c < chunks; c += B) *at(c) = xs[c];
-        __syncthreads();
-        float square = 0.0f;
-        for (int c = threadIdx.x % kWave; c < chunks; c += kWave) {
-            const f32x4 v = *at(c);
-            square = fmaf(v.x, v.x, square);
-            square = fmaf(v.y, v.y, square);
-            square = fmaf(v.z, v.z, square);
-            square = fmaf(v.w, v.w, square);
-        }
-        const float total = wave_sum_f32(square);
-        const float scale = 1.0f / sqrtf(total / static_cast<float>(bpr * kBlock) + kEps);
-        __syncthreads();  // every wave's reads of h precede the scaled writes
-        auto put = [&](int c, f32x4 v, uint2 q) {
-            v.x = v.x * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.x)));
-            v.y = v.y * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.x >> 16)));
-            v.z = v.z * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.y)));
-            v.w = v.w * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.y >> 16)));
-            *at(c) = v;
-        };
-#pragma unroll
-        for (int k = 0; k < kHeld; ++k) {
-            const int c = threadIdx.x + k * B;
-            if (c < chunks) put(c, xr[k], wr[k]);
-        }
-        for (int c = threadIdx.x + kHeld * B; c < chunks; c += B) put(c, *at(c), ws[c]);
-        __syncthreads();
-    }
-};
-
 // Input staging for a decode step's down projection: x = silu(gate) * up
 // (engine.cpp:371-376; swiglu_kernel's arithmetic) formed on the way into
 // LDS from the gate|up matvec's two outputs.
@@ -1293,14 +1226,17 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
         }
         if (rc) break;
         if (c.experts) {
-            hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden, nullptr, L.post_norm,
-                               c.H, e.normalized);
-            rc = step ? moe_layer_decode_add(L.moe, e.normalized, e.hidden, e.moe_ws, e.moe_ws_bytes, s)
+            // Decode: the post-attention norm inside the router and expert
+            // launches, the layer's output added to the residual in place.
+            rc = step ? moe_layer_decode_add(L.moe, e.hidden, L.post_norm, e.hidden, e.moe_ws, e.moe_ws_bytes, s)
                       : Q3X_HIP_ENOTSUP;
             pending = rc == Q3X_HIP_ENOTSUP;
-            if (pending)
+            if (pending) {
+                hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden, nullptr,
+                                   L.post_norm, c.H, e.normalized);
                 rc = q3x_hip_moe_layer(&L.moe, e.normalized, count, e.branch, nullptr, nullptr, e.moe_ws,
                                        e.moe_ws_bytes, s);
+            }
         } else {
             const Mat gate_up[2] = {L.gate, L.up};
             float* const ffn[2] = {e.ffn_gate, e.ffn_up};

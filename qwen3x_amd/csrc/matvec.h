@@ -625,5 +625,73 @@ int launch_mv(const Rows& rows, int nrows, int bpr, bool staged, hipStream_t str
     return launch_staged<QT, 64>(rows, nrows, bpr, stream);
 }
 
+constexpr float kEps = 1e-6f;  // RMSNorm epsilon, engine.cpp:26 EPS
+
+__device__ __forceinline__ float bf16_value(uint16_t v) { return __uint_as_float(static_cast<uint32_t>(v) << 16); }
+
+// Input staging for a decode step's projections (mv_pipe_kernel's `In`):
+// x = RMSNorm(h) * (1 + w) of the raw residual h (engine.cpp:228-233),
+// formed by every workgroup of the matvec launch on its way into LDS.  Each
+// thread loads its 16-byte chunks of h together with their four norm
+// weights (one round trip; the first kHeld chunks stay in registers) and
+// copies h to LDS; after one barrier every wave sums the squares of all of
+// h from LDS in the same fixed order (lane l takes chunks l, l + 64, ...
+// with FMAs, then the wave's DPP tree), so every wave of every workgroup --
+// whatever the launch shape -- holds the same scale; then each thread
+// scales its own chunks.  Requires w 8-byte aligned.
+struct NormInput {
+    static constexpr int kHeld = 4;
+    const uint16_t* w;
+    __device__ void stage(const float* x, uint8_t* xl, int bpr, float* /*work*/) const {
+        const int chunks = bpr * 8;
+        const int B = blockDim.x;
+        const f32x4* xs = reinterpret_cast<const f32x4*>(x);
+        const uint2* ws = reinterpret_cast<const uint2*>(w);
+        auto at = [&](int c) { return reinterpret_cast<f32x4*>(xl + x_block_offset(c >> 3) + 16 * (c & 7)); };
+        f32x4 xr[kHeld];
+        uint2 wr[kHeld];
+#pragma unroll
+        for (int k = 0; k < kHeld; ++k) {
+            const int c = threadIdx.x + k * B;
+            if (c < chunks) {
+                xr[k] = xs[c];
+                wr[k] = ws[c];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kHeld; ++k) {
+            const int c = threadIdx.x + k * B;
+            if (c < chunks) *at(c) = xr[k];
+        }
+        for (int c = threadIdx.x + kHeld * B; c < chunks; c += B) *at(c) = xs[c];
+        __syncthreads();
+        float square = 0.0f;
+        for (int c = threadIdx.x % kWave; c < chunks; c += kWave) {
+            const f32x4 v = *at(c);
+            square = fmaf(v.x, v.x, square);
+            square = fmaf(v.y, v.y, square);
+            square = fmaf(v.z, v.z, square);
+            square = fmaf(v.w, v.w, square);
+        }
+        const float total = wave_sum_f32(square);
+        const float scale = 1.0f / sqrtf(total / static_cast<float>(bpr * kBlock) + kEps);
+        __syncthreads();  // every wave's reads of h precede the scaled writes
+        auto put = [&](int c, f32x4 v, uint2 q) {
+            v.x = v.x * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.x)));
+            v.y = v.y * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.x >> 16)));
+            v.z = v.z * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.y)));
+            v.w = v.w * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.y >> 16)));
+            *at(c) = v;
+        };
+#pragma unroll
+        for (int k = 0; k < kHeld; ++k) {
+            const int c = threadIdx.x + k * B;
+            if (c < chunks) put(c, xr[k], wr[k]);
+        }
+        for (int c = threadIdx.x + kHeld * B; c < chunks; c += B) put(c, *at(c), ws[c]);
+        __syncthreads();
+    }
+};
+
 }  // namespace q3x
 

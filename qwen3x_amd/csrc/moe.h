@@ -8,10 +8,13 @@ namespace q3x {
 // One token of the MoE layer of q3x_hip_moe_layer (engine.cpp:406-430), its
 // result added to Y: Y += routed sum + gated shared expert, the layer output
 // formed in full first and added once, as the reference adds the layer's
-// output to its residual (engine.cpp:240-242).  Q3X_HIP_ENOTSUP (and Y left
-// unchanged) where the shape or alignment needs the grouped path; the caller
-// then runs q3x_hip_moe_layer and adds its output itself.
-int moe_layer_decode_add(const q3x_hip_moe_layer_weights& layer, const float* X, float* Y, void* workspace,
-                         size_t workspace_bytes, hipStream_t stream);
+// output to its residual (engine.cpp:240-242).  With norm_w, X is the raw
+// residual and the layer's input RMSNorm(X) * (1 + norm_w) (engine.cpp:
+// 228-233, the post-attention norm) is formed inside the router and expert
+// launches; X may then be Y itself.  Q3X_HIP_ENOTSUP (and Y left unchanged)
+// where the shape or alignment needs the grouped path; the caller then
+// normalises X, runs q3x_hip_moe_layer and adds its output itself.
+int moe_layer_decode_add(const q3x_hip_moe_layer_weights& layer, const float* X, const uint16_t* norm_w, float* Y,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 }  // namespace q3x

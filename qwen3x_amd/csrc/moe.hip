@@ -601,7 +601,8 @@ int launch_moe_down(const uint8_t* down, int experts, int H, int I, const int* i
 template <uint32_t QT>
 int moe_decode(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
                const int* ids, const float* weights, int top_k, float* Y, int accumulate,
-               uint8_t* ws, const MoeLayout& L, const SharedExpert& shared, hipStream_t stream) {
+               uint8_t* ws, const MoeLayout& L, const SharedExpert& shared, hipStream_t stream,
+               const uint16_t* norm_w = nullptr) {
     constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
     float* h = reinterpret_cast<float*>(ws + L.gu);  // [top_k (+1), I]
     const size_t gu_row = static_cast<size_t>(H / kBlock) * BB;
@@ -620,7 +621,10 @@ int moe_decode(const uint8_t* gate_up, const uint8_t* down, int experts, int H, 
         gate.shared_up = shared.up;
         gate.shared_I = shared.I;
         // One 64-lane row group, two row iterations (gate, up) per step.
-        int status = launch_pipe<QT, 64, 2>(gate, slots * 2 * I, H / kBlock, 16, stream, 2);
+        // With norm_w, X is the raw residual, normalised in the staging.
+        int status = norm_w ? launch_pipe<QT, 64, 2, ExpertGateUpRows, 1, 4, NormInput>(
+                                  gate, slots * 2 * I, H / kBlock, 16, stream, 2, NormInput{norm_w})
+                            : launch_pipe<QT, 64, 2>(gate, slots * 2 * I, H / kBlock, 16, stream, 2);
         if (status == Q3X_HIP_OK) {
             const int bpr = I / kBlock;
             status = bpr <= 16   ? launch_moe_down<QT, 16>(down, experts, H, I, ids, weights, top_k, h, Y,
@@ -741,17 +745,42 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
 __global__ __launch_bounds__(256) void router_gemv_bf16_kernel(const uint16_t* __restrict__ router,
                                                                const uint16_t* __restrict__ gate_row, int experts,
                                                                int H, const float* __restrict__ x,
+                                                               const uint16_t* __restrict__ norm_w,
                                                                float* __restrict__ logits,
                                                                float* __restrict__ gate_logit) {
     const int lane = threadIdx.x & (kWave - 1);
     const int r = blockIdx.x * 4 + threadIdx.x / kWave;
     if (r > experts) return;  // whole waves leave together
+    // With norm_w, x is the raw residual and each wave normalises it as
+    // NormInput stages it for the experts' matvec (same sum order, same
+    // products), so router and experts see identical normalised values.
+    float scale = 0.0f;
+    if (norm_w) {
+        float square = 0.0f;
+        for (int c = lane; c < H / 4; c += kWave) {
+            const f32x4 v = reinterpret_cast<const f32x4*>(x)[c];
+            square = fmaf(v.x, v.x, square);
+            square = fmaf(v.y, v.y, square);
+            square = fmaf(v.z, v.z, square);
+            square = fmaf(v.w, v.w, square);
+        }
+        scale = 1.0f / sqrtf(wave_sum_f32(square) / static_cast<float>(H) + kEps);
+    }
+    auto normed = [&](f32x4 v, int c) {
+        if (norm_w) {
+            v.x = v.x * scale * (1.0f + bf16_value(norm_w[c]));
+            v.y = v.y * scale * (1.0f + bf16_value(norm_w[c + 1]));
+            v.z = v.z * scale * (1.0f + bf16_value(norm_w[c + 2]));
+            v.w = v.w * scale * (1.0f + bf16_value(norm_w[c + 3]));
+        }
+        return v;
+    };
     const uint16_t* row = r < experts ? router + static_cast<size_t>(r) * H : gate_row;
     float acc = 0.0f;
     for (int c = 8 * lane; c < H; c += 8 * kWave) {
         const u32x4 w = *reinterpret_cast<const u32x4*>(row + c);
-        const f32x4 x0 = *reinterpret_cast<const f32x4*>(x + c);
-        const f32x4 x1 = *reinterpret_cast<const f32x4*>(x + c + 4);
+        const f32x4 x0 = normed(*reinterpret_cast<const f32x4*>(x + c), c);
+        const f32x4 x1 = normed(*reinterpret_cast<const f32x4*>(x + c + 4), c + 4);
         acc = fmaf(__uint_as_float(w.x << 16), x0.x, acc);
         acc = fmaf(__uint_as_float(w.x & 0xffff0000u), x0.y, acc);
         acc = fmaf(__uint_as_float(w.y << 16), x0.z, acc);
@@ -909,7 +938,7 @@ inline MoeLayerLayout moe_layer_layout(int tokens, int experts, int top_k, int H
 template <uint32_t QT>
 int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens, float* Y, int* ids,
                   float* weights, uint8_t* ws, const MoeLayerLayout& L, hipStream_t stream,
-                  bool accumulate = false) {
+                  bool accumulate = false, const uint16_t* norm_w = nullptr) {
     constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
     const int E = w.experts, H = w.H, I = w.I, SI = w.shared_I, K = w.top_k;
     float* logits = reinterpret_cast<float*>(ws + L.logits);
@@ -930,7 +959,7 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
     if (tokens == 1) {
         hipLaunchKernelGGL(router_gemv_bf16_kernel, dim3((E + 1 + 3) / 4), dim3(256), 0, stream,
                            reinterpret_cast<const uint16_t*>(router), reinterpret_cast<const uint16_t*>(gate_row),
-                           E, H, X, logits, gate);
+                           E, H, X, norm_w, logits, gate);
         status = launch_status();
     } else {
         RouterGemm g{};
@@ -946,7 +975,7 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
     if (tokens == 1) {
         const SharedExpert shared{sg, su, sd, SI, gate};
         status = moe_decode<QT>(gate_up, down, E, H, I, X, sel, wts, K, Y, accumulate ? 1 : 0, rws, L.R, shared,
-                                stream);
+                                stream, norm_w);
         if (status != Q3X_HIP_ENOTSUP || accumulate) return status;
     }
     // Prefill (or an unaligned decode): the grouped routed experts write Y,
@@ -1062,7 +1091,7 @@ extern "C" size_t q3x_hip_moe_layer_workspace_bytes(const q3x_hip_moe_layer_weig
 
 static int moe_layer_checked(const q3x_hip_moe_layer_weights* layer, const float* X, int tokens, float* Y,
                              int* ids, float* weights, void* workspace, size_t workspace_bytes,
-                             hipStream_t stream, bool accumulate) {
+                             hipStream_t stream, bool accumulate, const uint16_t* norm_w = nullptr) {
     if (layer && layer->type == Q3X_HIP_MATRIX_BF16) return Q3X_HIP_ENOTSUP;
     if (!X || !Y || !workspace || !moe_layer_ok(layer, tokens)) return Q3X_HIP_EINVAL;
     const q3x_hip_moe_layer_weights& w = *layer;
@@ -1074,8 +1103,8 @@ static int moe_layer_checked(const q3x_hip_moe_layer_weights* layer, const float
         return Q3X_HIP_EINVAL;
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     return w.type == Q3X_HIP_MATRIX_Q8_0
-               ? moe_layer_run<Q3X_HIP_MATRIX_Q8_0>(w, X, tokens, Y, ids, weights, ws, L, stream, accumulate)
-               : moe_layer_run<Q3X_HIP_MATRIX_Q4_0>(w, X, tokens, Y, ids, weights, ws, L, stream, accumulate);
+               ? moe_layer_run<Q3X_HIP_MATRIX_Q8_0>(w, X, tokens, Y, ids, weights, ws, L, stream, accumulate, norm_w)
+               : moe_layer_run<Q3X_HIP_MATRIX_Q4_0>(w, X, tokens, Y, ids, weights, ws, L, stream, accumulate, norm_w);
 }
 
 extern "C" int q3x_hip_moe_layer(const q3x_hip_moe_layer_weights* layer, const float* X, int tokens, float* Y,
@@ -1084,7 +1113,9 @@ extern "C" int q3x_hip_moe_layer(const q3x_hip_moe_layer_weights* layer, const f
     return moe_layer_checked(layer, X, tokens, Y, ids, weights, workspace, workspace_bytes, stream, false);
 }
 
-int q3x::moe_layer_decode_add(const q3x_hip_moe_layer_weights& layer, const float* X, float* Y, void* workspace,
-                              size_t workspace_bytes, hipStream_t stream) {
-    return moe_layer_checked(&layer, X, 1, Y, nullptr, nullptr, workspace, workspace_bytes, stream, true);
+int q3x::moe_layer_decode_add(const q3x_hip_moe_layer_weights& layer, const float* X, const uint16_t* norm_w,
+                              float* Y, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    // NormInput loads the norm weights four at a time (8 bytes).
+    if (norm_w && !aligned(norm_w, 8)) return Q3X_HIP_ENOTSUP;
+    return moe_layer_checked(&layer, X, 1, Y, nullptr, nullptr, workspace, workspace_bytes, stream, true, norm_w);
 }
