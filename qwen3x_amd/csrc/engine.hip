@@ -7,9 +7,9 @@
 // residual; final RMSNorm and lm_head.  A decode step runs each projection
 // group (and lm_head) as one launch of the pipelined matvec (matvec.h) whose
 // input staging forms the preceding RMSNorm or SwiGLU on the way into LDS
-// (NormInput, SwiGLUInput below); output projections and down accumulate
-// into the residual, and an MoE layer adds its output to it directly
-// (moe.h).  A chunk goes through this library's own entry points
+// (NormInput in matvec.h, SwiGLUInput below); output projections and down
+// accumulate into the residual, and an MoE layer normalises the residual
+// inside its own launches and adds its output to it directly (moe.h).  A chunk goes through this library's own entry points
 // (q3x_hip_gemm, q3x_hip_moe_layer).  The kernels here are the per-token
 // operations between the matrices.
 //
