@@ -59,6 +59,24 @@ __device__ float block_sum(float v, float* partial) {
     __syncthreads();
     return total;
 }
+// Two sums at once (one pair of barriers), each in block_sum's order.
+template <int THREADS>
+__device__ float2 block_sum2(float u, float v, float* partial) {
+    const float wu = wave_sum_f32(u), wv = wave_sum_f32(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        partial[threadIdx.x / kWave] = wu;
+        partial[THREADS / kWave + threadIdx.x / kWave] = wv;
+    }
+    __syncthreads();
+    float2 total{0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < THREADS / kWave; ++i) {
+        total.x += partial[i];
+        total.y += partial[THREADS / kWave + i];
+    }
+    __syncthreads();
+    return total;
+}
 template <int THREADS>
 __device__ float block_max(float v, float* partial) {
     const float w = wave_max_f32(v);
@@ -272,7 +290,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_rule_kernel(
     const float* __restrict__ norm, float* __restrict__ memory, float* __restrict__ out,
     const uint16_t* __restrict__ conv_w, float* __restrict__ history, const int* __restrict__ position, int CK,
     int KH, int VH, int KD, int VD) {
-    __shared__ float qs[128], ks[128], part[kDeltaGroups][128], sum[128], partial[kDeltaThreads / kWave];
+    __shared__ float qs[128], ks[128], part[kDeltaGroups][128], sum[128], partial[2 * kDeltaThreads / kWave];
     const int head = blockIdx.x;
     const int t = threadIdx.x;
     const int DQK = KH * KD, DO = VH * VD, DQKV = 2 * DQK + DO;
@@ -288,6 +306,9 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_rule_kernel(
     // The causal conv of this head's channels (q and k of its key head, its
     // v), read from history copy p % 2; the new history goes to copy (p + 1)
     // % 2 -- for q and k only from the key head's first value head.
+    // Per-head and per-column inputs requested up front, with S.
+    const float a_in = a[head], b_in = b[head];
+    const float z_in = t < VD ? z[static_cast<size_t>(head) * VD + t] : 0.0f;
     const int pos = *position;
     const size_t copy = static_cast<size_t>(DQKV) * (CK - 1);
     const float* hin = history + (pos & 1) * copy;
@@ -309,15 +330,15 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_rule_kernel(
                                           conv_w + static_cast<size_t>(cv) * CK, CK,
                                           group == 0 ? hout + static_cast<size_t>(cv) * (CK - 1) : nullptr)
                              : 0.0f;
-        const float qn = block_sum<kDeltaThreads>(qv * qv, partial);
-        const float kn = block_sum<kDeltaThreads>(kv * kv, partial);
+        const float2 n2 = block_sum2<kDeltaThreads>(qv * qv, kv * kv, partial);
+        const float qn = n2.x, kn = n2.y;
         if (t < KD) {
             qs[t] = qv * (1.0f / sqrtf(qn + kEps)) / sqrtf(static_cast<float>(KD));
             ks[t] = kv * (1.0f / sqrtf(kn + kEps));
         }
         __syncthreads();
-        const float beta = sigmoid_ref(b[static_cast<size_t>(r) * VH + head]);
-        const float decay = -A * softplus_ref(a[static_cast<size_t>(r) * VH + head] + bias);
+        const float beta = sigmoid_ref(b_in);
+        const float decay = -A * softplus_ref(a_in + bias);
         const float scale = expf(decay);
         float pred = 0.0f;
 #pragma unroll
@@ -348,17 +369,22 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_rule_kernel(
         __syncthreads();  // every read of part / sum / qs / ks above is done
         part[group][v] = o;
         __syncthreads();
-        float result = 0.0f;
-        if (t < VD) {
-            result = part[0][t];
+        // Every wave forms all 128 column results (lane l: columns l and
+        // l + 64; zero past VD) and their squares' sum itself, so the gated
+        // norm needs no further barrier; waves 0 and 1 store.
+        const int lane = t & (kWave - 1);
+        float r0 = part[0][lane], r1 = part[0][lane + kWave];
 #pragma unroll
-            for (int g = 1; g < kDeltaGroups; ++g) result += part[g][t];
+        for (int g = 1; g < kDeltaGroups; ++g) {
+            r0 += part[g][lane];
+            r1 += part[g][lane + kWave];
         }
-        const float sq = block_sum<kDeltaThreads>(result * result, partial);
+        const float sq = wave_sum_f32(fmaf(r1, r1, r0 * r0));
         if (t < VD) {
+            const float result = t < kWave ? r0 : r1;
             const float g = 1.0f / sqrtf(sq / static_cast<float>(VD) + kEps);
             const size_t at = static_cast<size_t>(r) * DO + head * VD + t;
-            out[at] = result * (g * nv * silu_ref(z[at]));
+            out[at] = result * (g * nv * silu_ref(z_in));
         }
     }
     store_keys<kDeltaKeys>(S, group * kDeltaKeys, KD, col, s);
