@@ -107,6 +107,9 @@ int q3x_hip_dequant(const void* w, uint32_t type, int cols, int row0, int nrows,
 /* Per-token router: softmax over `experts` logits, top_k sequential argmax
  * (strict '>', lowest index wins ties), weights renormalised over the
  * selection.  logits [tokens, experts]; ids, weights [tokens, top_k].
+ * Exact: the softmax repeats the reference's operations (exp with the host
+ * libm's expf arithmetic, the total added in expert order, correctly rounded
+ * divisions), so ids and weights equal the reference's bit for bit.
  * Replaces router_top_k (engine.cpp:377-405; router_top_k_kernel
  * engine.cu:1153-1184, which runs one thread for one token).
  * Requires 1 <= top_k <= min(experts, 8) and experts <= 1024. */

@@ -22,6 +22,7 @@
 #include "moe.h"
 
 #include "gemm.h"
+#include "libm_expf.h"
 #include "matvec.h"
 
 namespace q3x {
@@ -45,22 +46,28 @@ constexpr int kGrpBN = kGrpWN * kGrpTN * 32;
 // ---------------------------------------------------------------- router ----
 
 // One wavefront per token; lane l holds experts [PER*l, PER*l + PER), so lane
-// order is expert order.  Softmax with the maximum subtracted, then top_k
-// argmax passes, each over keys (0 for an expert already chosen or past the
-// end, else the probability's bits + 1: probabilities are >= 0, so their bits
-// order like the values).  A lane keeps its best key (lowest index among
-// equal ones); the wave's largest key is found with DPP and readlanes, and
-// the lowest lane holding it wins, i.e. the lowest expert index among equal
-// probabilities, as the reference's strict '>' scan picks.  Weights = p / (sum
-// of the selected p, added in slot order).  No LDS: every exchange is a DPP
-// move or a readlane, so one token costs a few hundred instructions.
+// order is expert order.  The softmax is the reference's operation for
+// operation (engine.cpp:380-387): the maximum (exact in any order), p = exp(l -
+// max) with libm's expf arithmetic (libm_expf.h), the total added in expert
+// order from zero, and p / total correctly rounded.  The total's order is
+// sequential, so the wave writes p to LDS and every lane runs the same chain
+// of adds over it (broadcast reads).  Then top_k argmax passes, each over
+// keys (0 for an expert already chosen or past the end, else the
+// probability's bits + 1: probabilities are >= 0, so their bits order like
+// the values).  A lane keeps its best key (lowest index among equal ones);
+// the wave's largest key is found with DPP and readlanes, and the lowest lane
+// holding it wins, i.e. the lowest expert index among equal probabilities, as
+// the reference's strict '>' scan picks.  Weights = p / (sum of the selected
+// p, added in slot order), correctly rounded (engine.cpp:388-404).
 template <int PER>
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int tokens,
                                                           int experts, int top_k, int* __restrict__ ids,
                                                           float* __restrict__ weights) {
+    __shared__ __attribute__((aligned(16))) float probs[4][kRouterMaxExperts];
     const int lane = threadIdx.x & (kWave - 1);
-    const int token = blockIdx.x * 4 + threadIdx.x / kWave;
-    if (token >= tokens) return;  // whole waves leave together
+    const int wave = threadIdx.x / kWave;
+    const int token = blockIdx.x * 4 + wave;
+    if (token >= tokens) return;  // whole waves leave together; no block barrier below
     const float* row = logits + static_cast<size_t>(token) * experts;
     const int first = PER * lane;
     float p[PER];
@@ -70,16 +77,27 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
 #pragma unroll
     for (int j = 0; j < PER; ++j) local_max = local_max < p[j] ? p[j] : local_max;
     const float maximum = wave_max_f32(local_max);
-    float local_sum = 0.0f;
+    float* mine_p = probs[wave];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-        p[j] = first + j < experts ? expf(p[j] - maximum) : 0.0f;
-        local_sum += p[j];
+        p[j] = first + j < experts ? libm_expf(p[j] - maximum) : 0.0f;
+        mine_p[first + j] = p[j];  // zeros past the end pad the last group of four
     }
-    const float total = wave_sum_f32(local_sum);
+    wave_lds_sync();
+    // The padding zeros add nothing: total + 0 == total for total >= +0.
+    float total = 0.0f;
+    const int groups4 = (experts + 3) / 4;
+#pragma unroll 4
+    for (int q = 0; q < groups4; ++q) {
+        const f32x4 v = reinterpret_cast<const f32x4*>(mine_p)[q];
+        total += v.x;
+        total += v.y;
+        total += v.z;
+        total += v.w;
+    }
     uint32_t key[PER];
 #pragma unroll
-    for (int j = 0; j < PER; ++j) key[j] = first + j < experts ? __float_as_uint(p[j] / total) + 1u : 0u;
+    for (int j = 0; j < PER; ++j) key[j] = first + j < experts ? __float_as_uint(__fdiv_rn(p[j], total)) + 1u : 0u;
 
     float chosen[kRouterMaxTopK];
     int chosen_id[kRouterMaxTopK];
@@ -115,7 +133,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
         if (slot == lane) { mine = chosen[slot]; mine_id = chosen_id[slot]; }
     if (lane < top_k) {
         ids[static_cast<size_t>(token) * top_k + lane] = mine_id;
-        weights[static_cast<size_t>(token) * top_k + lane] = mine / selected_total;
+        weights[static_cast<size_t>(token) * top_k + lane] = __fdiv_rn(mine, selected_total);
     }
 }
 

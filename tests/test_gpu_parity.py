@@ -262,28 +262,42 @@ def test_gemm_parity(type_, rows, cols, count):
 
 # ---------------------------------------------------------------- router ----
 
-@pytest.mark.parametrize("tokens,experts,top_k", [(1, 256, 8), (2048, 256, 8), (37, 6, 3), (100, 1024, 8),
-                                                  (5, 64, 1)])
-def test_router_parity(tokens, experts, top_k):
+def _router_logits(rng, tokens, experts, kind):
+    if kind == "normal":
+        logits = rng.normal(0, 1, (tokens, experts)).astype(np.float32)
+        logits[::7, 3] = logits[::7, 5]  # exact ties
+    elif kind == "grid":
+        # values on a coarse grid: many equal probabilities, and distinct ones
+        # that the division by the total can round together
+        logits = (rng.integers(-6, 7, (tokens, experts)) * 0.125).astype(np.float32)
+    else:
+        # a wide spread: exp underflows to subnormals and to zero, -inf logits
+        logits = rng.normal(0, 40, (tokens, experts)).astype(np.float32)
+        logits[::5, 0] = -np.inf
+        logits[::3, 1] = -120.0
+    return logits
+
+
+@pytest.mark.parametrize("tokens,experts,top_k,kind", [
+    (1, 256, 8, "normal"), (2048, 256, 8, "normal"), (37, 6, 3, "normal"), (100, 1024, 8, "normal"),
+    (5, 64, 1, "normal"), (513, 256, 8, "grid"), (64, 130, 8, "grid"), (300, 256, 8, "wide"),
+    (9, 1000, 5, "wide")])
+def test_router_parity(tokens, experts, top_k, kind):
+    # The GPU softmax is the reference's operation for operation (libm's expf
+    # arithmetic, the total in expert order, correctly rounded divisions), so
+    # ids and weights are exact.
     torch = _torch()
     rng = np.random.default_rng(tokens + experts)
-    logits = rng.normal(0, 1, (tokens, experts)).astype(np.float32)
-    logits[::7, 3] = logits[::7, 5]  # exact ties
-    ids_o, w_o, probs_o = oracle.router_top_k(logits, top_k)
+    logits = _router_logits(rng, tokens, experts, kind)
+    ids_o, w_o, _ = oracle.router_top_k(logits, top_k)
     ids = torch.empty((tokens, top_k), dtype=torch.int32, device="cuda:0")
     w = torch.empty((tokens, top_k), dtype=torch.float32, device="cuda:0")
+    say(f"router tokens={tokens} experts={experts} top_k={top_k} {kind}")
     q3x.router_top_k(dev(logits), tokens, experts, top_k, ids, w)
     ids_g, w_g = host(ids), host(w)
-    for t in range(tokens):
-        if not np.array_equal(ids_g[t], ids_o[t]):
-            # Only a near-tie (probabilities within a few ulp) may reorder.
-            p = probs_o[t]
-            for a, b in zip(ids_g[t], ids_o[t]):
-                if a != b:
-                    assert abs(p[a] - p[b]) <= 4 * np.spacing(np.float32(max(p[a], p[b]))), (t, a, b)
-        else:
-            assert np.allclose(w_g[t], w_o[t], rtol=2e-6, atol=0), t
-    assert np.allclose(w_g.sum(1), 1.0, atol=1e-6)
+    bad = np.nonzero(~np.all(ids_g == ids_o, axis=1))[0]
+    assert bad.size == 0, f"{bad.size} tokens select other experts, first {bad[:4]}"
+    assert np.array_equal(bits(w_g), bits(w_o))
 
 
 # ------------------------------------------------------------------- MoE ----
