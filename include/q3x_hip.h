@@ -134,6 +134,35 @@ int q3x_hip_moe_routed(const void* gate_up, const void* down, uint32_t type,
                        int accumulate, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
 
+/* Size of the library's static per-device scratch that
+ * q3x_hip_moe_routed_noalloc runs on: 32 MiB holds the workspace of 256
+ * tokens at the 35B-A3B expert shape (H 2048, I 512, top 8), the reference's
+ * prefill chunk (engine.cu:45). */
+#define Q3X_HIP_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+enum {
+    Q3X_HIP_ESCRATCH = -5,  /* request needs more workspace than
+                               Q3X_HIP_NOALLOC_SCRATCH_BYTES */
+};
+
+/* q3x_hip_moe_routed without a workspace argument, for callers that cannot
+ * allocate (code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  Same arguments,
+ * kernels and results as q3x_hip_moe_routed, run on a workspace the library
+ * holds in a static __device__ array of Q3X_HIP_NOALLOC_SCRATCH_BYTES per
+ * device (held until the process ends); the call allocates and frees
+ * nothing.  Returns Q3X_HIP_ESCRATCH, touching nothing, when
+ * q3x_hip_moe_workspace_bytes(tokens, experts, top_k, H, I) exceeds that
+ * size.  Runs on the current device (the stream's).  Every call on a device
+ * shares that device's scratch: calls that overlap on one device (different
+ * streams, or threads without ordering) race; calls ordered on one stream
+ * do not.  The first call on a device looks the scratch address up
+ * (hipGetSymbolAddress), so make one call before capturing a graph. */
+int q3x_hip_moe_routed_noalloc(const void* gate_up, const void* down, uint32_t type,
+                               int experts, int H, int I, const float* X, int tokens,
+                               const int* ids, const float* weights, int top_k, float* Y,
+                               int accumulate, hipStream_t stream);
+
 /* The weights of one MoE layer (the reference's MoeWeights, engine.cu:97-101,
  * engine.cpp:53-57; shapes as model.bin lays them out, engine.cpp:543-550).
  * Every pointer is a device pointer; the struct itself is read on the host. */

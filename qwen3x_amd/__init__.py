@@ -29,6 +29,9 @@ EINVAL = -1
 ERUNTIME = -2
 ENOTSUP = -3
 EMODEL = -4
+ESCRATCH = -5
+# Static per-device scratch of q3x_hip_moe_routed_noalloc (Q3X_HIP_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 TENSOR_F32 = 3
 MODEL_HEADER_BYTES = 72
@@ -54,6 +57,7 @@ SIGNATURES = {
     "q3x_hip_router_topk": (_I, [_P, _I, _I, _I, _P, _P, _P]),
     "q3x_hip_moe_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),
     "q3x_hip_moe_routed": (_I, [_P, _P, _U, _I, _I, _I, _P, _I, _P, _P, _I, _P, _I, _P, _S, _P]),
+    "q3x_hip_moe_routed_noalloc": (_I, [_P, _P, _U, _I, _I, _I, _P, _I, _P, _P, _I, _P, _I, _P]),
     "q3x_hip_quantize": (_I, [_U, _P, _I, _I, _P, _P]),
     "q3x_hip_moe_layer_workspace_bytes": (_S, [_P, _I]),
     "q3x_hip_moe_layer": (_I, [_P, _P, _I, _P, _P, _P, _P, _S, _P]),

@@ -156,6 +156,7 @@ extern "C" const char* q3x_hip_strerror(int code) {
     case Q3X_HIP_ERUNTIME: return "HIP runtime error";
     case Q3X_HIP_ENOTSUP: return "matrix type not handled by this backend";
     case Q3X_HIP_EMODEL: return "model.bin rejected";
+    case Q3X_HIP_ESCRATCH: return "request needs more workspace than the library's static scratch";
     default: return "unknown error";
     }
 }
