@@ -136,6 +136,15 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(
                 f"{LIB_PATH} is missing: build it with `make -C {_PKG_DIR}` "
                 "(or __graft_entry__.build()); there is no fallback path")
+        # torch's ROCm wheel bundles its own libamdhip64 (the same soname).
+        # Loaded after torch, this library binds to that runtime; loaded
+        # first, it would pull in /opt/rocm's copy and the process would hold
+        # two HIP runtimes, whose device memory and streams do not mix with
+        # torch's tensors.  So torch, where installed, is loaded first.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         handle = ctypes.CDLL(LIB_PATH)
         for name, (restype, argtypes) in SIGNATURES.items():
             fn = getattr(handle, name)

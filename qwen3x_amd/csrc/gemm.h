@@ -9,15 +9,22 @@
 // the row-major [tokens, rows] output.
 //
 // Per K stage (one 32-column block): the workgroup loads its A tile
-// (BM x 32 FP32) and its weight blocks (BN rows x 1 block), dequantises the
-// weights to FP32 (d * q is exact in FP32: an 11-bit significand times an
-// 8-bit integer), writes both to a double-buffered LDS tile, and each wave
-// runs 16 MFMA k-steps per 32x32 tile.  The 32 k values of a block are fed
-// in the order k = 16*(lane/32) + s (s = 0..15), the same permutation for A
-// and B, so a lane reads 16 consecutive floats of each operand row with four
+// (BM x 32 FP32) and its weight blocks (BN rows x 1 block), converts the
+// block values q (Q8_0 int8, Q4_0 nibble - 8) to FP32 and keeps each row's
+// fp16 scale d apart, writes both to a double-buffered LDS tile, and each
+// wave runs 16 MFMA k-steps per 32x32 tile into a block accumulator that
+// starts from zero.  The block's sum then enters the output accumulator as
+// acc = fma(d, inner, acc): the reference's per-block factorisation
+// (arch/cpu.cpp:64-73, 91-101: inner = sum q * x, sum += d * inner), which
+// keeps the rounding error of a K-long sum at the reference's level rather
+// than that of one K-long chain of products.  BF16 weights have no block
+// scale and accumulate directly.  The 32 k values of a block are fed in the
+// order k = 16*(lane/32) + s (s = 0..15), the same permutation for A and B,
+// so a lane reads 16 consecutive floats of each operand row with four
 // ds_read_b128.
 #pragma once
 
+#include <type_traits>
 #include <utility>
 
 #include "common.h"
@@ -65,8 +72,10 @@ struct BlockPart {
             __builtin_memcpy(raw + 1, blk + 2 + 4 * WORDS * part, 4 * WORDS);
         }
     }
-    // out[e] for e < N, in the column order of column().
-    __device__ static __forceinline__ void dequant(const uint32_t* raw, float* out) {
+    // The block values as FP32, out[e] for e < N in the column order of
+    // column(): q for Q8_0, nibble - 8 for Q4_0 (the scale is applied per
+    // block, scale()), the exact BF16 value for BF16.
+    __device__ static __forceinline__ void values(const uint32_t* raw, float* out) {
         if constexpr (kBF16) {
 #pragma unroll
             for (int i = 0; i < WORDS; ++i) {
@@ -75,7 +84,6 @@ struct BlockPart {
             }
             return;
         }
-        const float d = f16_fast(raw[0]);
 #pragma unroll
         for (int i = 0; i < WORDS; ++i) {
             const uint32_t w = raw[1 + i];
@@ -83,14 +91,16 @@ struct BlockPart {
             for (int b = 0; b < 4; ++b) {
                 const uint32_t byte = (w >> (8 * b)) & 0xffu;
                 if constexpr (kQ4) {
-                    out[4 * i + b] = d * static_cast<float>(static_cast<int>(byte & 15u) - 8);
-                    out[N / 2 + 4 * i + b] = d * static_cast<float>(static_cast<int>(byte >> 4) - 8);
+                    out[4 * i + b] = static_cast<float>(static_cast<int>(byte & 15u) - 8);
+                    out[N / 2 + 4 * i + b] = static_cast<float>(static_cast<int>(byte >> 4) - 8);
                 } else {
-                    out[4 * i + b] = d * static_cast<float>(static_cast<int8_t>(byte));
+                    out[4 * i + b] = static_cast<float>(static_cast<int8_t>(byte));
                 }
             }
         }
     }
+    // The block's fp16 scale d (exact in FP32).
+    __device__ static __forceinline__ float scale(const uint32_t* raw) { return f16_fast(raw[0]); }
     // Column within the block of output element e.
     __device__ static __forceinline__ int column(int part, int e) { return part * N + e; }
     // LDS chunk (4 columns) of the activations' 16-byte chunk c (elements
@@ -148,6 +158,9 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
 
     __shared__ __attribute__((aligned(16))) float As[2][BM * kGemmLd];
     __shared__ __attribute__((aligned(16))) float Bs[2][BN * kGemmLd];
+    // Block scales of the stage's weight rows (quantized types).
+    constexpr bool kScaled = QT != Q3X_HIP_MATRIX_BF16;
+    __shared__ float Ds[2][kScaled ? BN : 1];
 
     // Tile coordinates: a 2-D grid (x = weight-row tiles, y = A-row tiles), or
     // a 1-D grid over gx * gy tiles (Policy::kLinearGrid) remapped so that
@@ -215,7 +228,8 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
             const int n = tid / PARTS + p * B_ROWS_PER_PASS;
             if (n < BN) {
                 float vals[PER_PART];
-                Part::dequant(b_raw[r][p], vals);
+                Part::values(b_raw[r][p], vals);
+                if (kScaled && b_part == 0) Ds[buf][n] = Part::scale(b_raw[r][p]);
 #pragma unroll
                 for (int e = 0; e < PER_PART; e += 4) {
                     const int c = Part::column(b_part, e);
@@ -234,47 +248,79 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
         for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    // 16x16 form: acc16[i][mh][j][nh] is block (rows mh*16.., cols nh*16..)
-    // of tile (i, j); lane l holds rows 4*(l/16) + r, column l % 16.
-    f32x4 acc16[TM][2][TN][2];
+    // 16x16 form: acc16[q][j][nh] is block (rows 16q.., cols nh*16..) of the
+    // wave's 32-row tile q / 2, column tile j: subtile q = 2 i + mh holds rows
+    // (wm * TM + i) * 32 + mh * 16 + [0, 16); lane l holds rows 4*(l/16) + r,
+    // column l % 16.
+    constexpr int NSUB = 2 * TM;
+    f32x4 acc16[NSUB][TN][2];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int q = 0; q < NSUB; ++q)
 #pragma unroll
-        for (int mh = 0; mh < 2; ++mh)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-#pragma unroll
-                for (int nh = 0; nh < 2; ++nh) acc16[i][mh][j][nh] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int nh = 0; nh < 2; ++nh) acc16[q][j][nh] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int l16 = lane & 15, g16 = lane >> 4;
 
     const int nblk = cols / kBlock;
     // A wave whose A rows all lie past the tile's valid rows (the last tile
     // of an expert's group) has nothing to compute: it only helps stage the
-    // tiles, leaving the SIMD's matrix core to the other waves.
+    // tiles, leaving the SIMD's matrix core to the other waves.  Its active
+    // 16-row subtiles form a prefix of the subtile order.
     const bool active = !Policy::kPartialTiles || wm * TM * 32 < tile.mcount;
+    const int nsub = Policy::kPartialTiles ? min(NSUB, (tile.mcount - wm * TM * 32 + 15) / 16) : NSUB;
+
+    // Quantized types: each tile's MFMA chain sums one block into a block
+    // accumulator from zero, and the block enters acc as acc = fma(d, inner,
+    // acc), blocks in order.  A tile's fold is issued after the next tile's
+    // MFMA chain, so the matrix core runs while the VALU folds; the last
+    // tile of a stage is folded in the next stage, right after its first
+    // chain (or after the loop), with the scales of its own stage kept in
+    // registers (the next stage's staging overwrites them in LDS).  A wave
+    // with one 32x32 tile alternates two block accumulators between stages.
+    constexpr int NT32 = TM * TN;
+    constexpr int SETS = NT32 == 1 ? 2 : 1;
+    f32x16 blk[SETS][NT32];
+    float d_old[TN], d_new[TN];
+    f32x4 blk16[NSUB][TN][2];
+    float d16_old[TN][2], d16_new[TN][2];
+    auto fold32 = [&](int t, const f32x16& b, const float* d) {
+        const int i = t / TN, j = t % TN;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(d[j], b[r], acc[i][j][r]);
+    };
+    auto fold16 = [&](int q, float (*d)[2]) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int nh = 0; nh < 2; ++nh)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc16[q][j][nh][r] = fmaf(d[j][nh], blk16[q][j][nh][r], acc16[q][j][nh][r]);
+    };
+    // The pending subtile of the previous stage (the last active one).
+    auto fold16_pending = [&]() {
+#pragma unroll
+        for (int q = 0; q < NSUB; ++q)
+            if (q == nsub - 1) fold16(q, d16_old);
+    };
+
     // One K stage kb: first stage kb + 1 (in registers since the previous
     // stage) goes to the other LDS buffer, which the previous barrier freed;
     // then the loads of stage kb + 1 + PF are issued into the register set
     // just emptied; then the MFMAs of stage kb; then the barrier.  At the LDS
     // store the only loads in flight are the ones it consumes (so the
     // compiler waits for exactly those), and the new loads overlap a whole
-    // stage of MFMAs and the barrier.  Stage s lives in register set s % PF.
-    auto step = [&](int kb, int r) {
+    // stage of MFMAs and the barrier.  Stage s lives in register set s % PF;
+    // P is the stage's parity (the block accumulator set of one-tile waves).
+    auto step = [&](int kb, int r, auto parity) {
+        constexpr int P = decltype(parity)::value;
         const int buf = kb & 1;
         if (kb + 1 < nblk) store_stage(buf ^ 1, r);
         if (kb + 1 + PF < nblk) load_stage(kb + 1 + PF, r);
         if (M16 && active) {
             // Lane group g16 supplies k = 8 * g16 + s of MFMA step s (the same
             // k order for both operands), i.e. 8 consecutive LDS columns.
-            f32x4 af[TM][2][2], bf[TN][2][2];
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int mh = 0; mh < 2; ++mh) {
-                    const float* src = &As[buf][((wm * TM + i) * 32 + mh * 16 + l16) * kGemmLd + 8 * g16];
-                    af[i][mh][0] = *reinterpret_cast<const f32x4*>(src);
-                    af[i][mh][1] = *reinterpret_cast<const f32x4*>(src + 4);
-                }
+            f32x4 bf[TN][2][2];
 #pragma unroll
             for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -283,20 +329,47 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
                     bf[j][nh][0] = *reinterpret_cast<const f32x4*>(src);
                     bf[j][nh][1] = *reinterpret_cast<const f32x4*>(src + 4);
                 }
+            if constexpr (kScaled) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+                for (int j = 0; j < TN; ++j)
 #pragma unroll
-                for (int mh = 0; mh < 2; ++mh) {
-                    if (Policy::kPartialTiles && (wm * TM + i) * 32 + mh * 16 >= tile.mcount) continue;
+                    for (int nh = 0; nh < 2; ++nh) d16_new[j][nh] = Ds[buf][(wn * TN + j) * 32 + nh * 16 + l16];
+                // One active subtile: its pending block is folded before the
+                // chain reuses its accumulator.
+                if (kb > 0 && nsub == 1) fold16_pending();
+            }
 #pragma unroll
-                    for (int s = 0; s < 8; ++s)
+            for (int q = 0; q < NSUB; ++q) {
+                if (q >= nsub) break;
+                const float* asrc = &As[buf][((wm * TM + q / 2) * 32 + (q & 1) * 16 + l16) * kGemmLd + 8 * g16];
+                const f32x4 af0 = *reinterpret_cast<const f32x4*>(asrc);
+                const f32x4 af1 = *reinterpret_cast<const f32x4*>(asrc + 4);
 #pragma unroll
-                        for (int j = 0; j < TN; ++j)
+                for (int s = 0; s < 8; ++s) {
+                    const float a = s < 4 ? af0[s] : af1[s - 4];
 #pragma unroll
-                            for (int nh = 0; nh < 2; ++nh)
-                                acc16[i][mh][j][nh] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                                    af[i][mh][s >> 2][s & 3], bf[j][nh][s >> 2][s & 3], acc16[i][mh][j][nh], 0, 0, 0);
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int nh = 0; nh < 2; ++nh) {
+                            const float b = bf[j][nh][s >> 2][s & 3];
+                            if constexpr (kScaled)
+                                blk16[q][j][nh] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                                    a, b, s == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : blk16[q][j][nh], 0, 0, 0);
+                            else
+                                acc16[q][j][nh] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc16[q][j][nh], 0, 0, 0);
+                        }
                 }
+                if constexpr (kScaled) {
+                    if (q == 0 && kb > 0 && nsub > 1) fold16_pending();
+                    if (q > 0) fold16(q - 1, d16_new);
+                }
+            }
+            if constexpr (kScaled) {
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int nh = 0; nh < 2; ++nh) d16_old[j][nh] = d16_new[j][nh];
+            }
         } else if (active) {
             f32x4 af[TM][4], bf[TN][4];
 #pragma unroll
@@ -311,15 +384,38 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
 #pragma unroll
                 for (int q = 0; q < 4; ++q) bf[j][q] = *reinterpret_cast<const f32x4*>(src + 4 * q);
             }
+            if constexpr (kScaled) {
 #pragma unroll
-            for (int s = 0; s < 16; ++s)
+                for (int j = 0; j < TN; ++j) d_new[j] = Ds[buf][(wn * TN + j) * 32 + li];
+                constexpr int S = P % SETS;
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
+                for (int t = 0; t < NT32; ++t) {
+                    const int i = t / TN, j = t % TN;
 #pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s >> 2][s & 3],
-                                                                         bf[j][s >> 2][s & 3],
-                                                                         acc[i][j], 0, 0, 0);
+                    for (int s = 0; s < 16; ++s)
+                        blk[S][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s >> 2][s & 3], bf[j][s >> 2][s & 3],
+                                                                         s == 0 ? f32x16{} : blk[S][t], 0, 0, 0);
+                    if (t == 0 && kb > 0) {
+                        // The previous stage's last tile: in the other set
+                        // for one-tile waves, else the last tile of this set.
+                        if constexpr (SETS == 2) fold32(0, blk[S ^ 1][0], d_old);
+                        else fold32(NT32 - 1, blk[0][NT32 - 1], d_old);
+                    }
+                    if (t > 0) fold32(t - 1, blk[S][t - 1], d_new);
+                }
+#pragma unroll
+                for (int j = 0; j < TN; ++j) d_old[j] = d_new[j];
+            } else {
+#pragma unroll
+                for (int s = 0; s < 16; ++s)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s >> 2][s & 3],
+                                                                             bf[j][s >> 2][s & 3],
+                                                                             acc[i][j], 0, 0, 0);
+            }
         }
         __syncthreads();
     };
@@ -330,15 +426,22 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
     for (int q = 1; q <= PF; ++q)
         if (q < nblk) load_stage(q, q % PF);
     __syncthreads();
-    if constexpr (PF == 1) {
-        for (int kb = 0; kb < nblk; ++kb) step(kb, 0);
-    } else {
-        for (int kb = 0; kb < nblk; kb += 2) {
-            step(kb, 1);                           // stage kb + 1 is in set 1
-            if (kb + 1 < nblk) step(kb + 1, 0);    // stage kb + 2 is in set 0
+    // Stages in pairs, so each knows its parity at compile time.
+    for (int kb = 0; kb < nblk; kb += 2) {
+        step(kb, PF == 1 ? 0 : 1, std::integral_constant<int, 0>{});         // PF 2: stage kb + 1 is in set 1
+        if (kb + 1 < nblk) step(kb + 1, 0, std::integral_constant<int, 1>{});  // PF 2: stage kb + 2 is in set 0
+    }
+    // The last stage's pending tile.
+    if (kScaled && active) {
+        if constexpr (M16) {
+            fold16_pending();
+        } else if constexpr (SETS == 2) {
+            if ((nblk - 1) & 1) fold32(0, blk[1][0], d_old);
+            else fold32(0, blk[0][0], d_old);
+        } else {
+            fold32(NT32 - 1, blk[0][NT32 - 1], d_old);
         }
     }
-
     if constexpr (M16) {
         // v_mfma_f32_16x16x4_f32: register r of lane l holds C[4*(l/16) + r][l%16].
 #pragma unroll
@@ -355,11 +458,11 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
                         if constexpr (Policy::kPairedColumns) {
                             // Column q < 16 and its partner q + 16 sit in the
                             // same lane: blocks nh = 0 and nh = 1.
-                            if (nb < rows) pol.store_pair(tile, m, nb, acc16[i][mh][j][0][r], acc16[i][mh][j][1][r]);
+                            if (nb < rows) pol.store_pair(tile, m, nb, acc16[2 * i + mh][j][0][r], acc16[2 * i + mh][j][1][r]);
                         } else {
 #pragma unroll
                             for (int nh = 0; nh < 2; ++nh)
-                                if (nb + 16 * nh < rows) pol.store(tile, m, nb + 16 * nh, acc16[i][mh][j][nh][r]);
+                                if (nb + 16 * nh < rows) pol.store(tile, m, nb + 16 * nh, acc16[2 * i + mh][j][nh][r]);
                         }
                     }
                 }
