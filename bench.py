@@ -267,9 +267,60 @@ def time_graph(torch, fn, calls, replays, warmup=2):
     return start.elapsed_time(end) / (replays * calls)
 
 
-def extra_configs(torch, q3x, wl, only=None):
+def cpu_median(fn, seconds, max_reps=25):
+    """Median seconds of fn() over repeats filling about `seconds` (>= 3
+    repeats after one warm-up)."""
+    fn()
+    times = []
+    while len(times) < 3 or (sum(times) < seconds and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+class CpuReference:
+    """The reference CPU path, single thread, on host copies of a config's
+    weights: the reference's own try_mv (arch/cpu.cpp:192-226, scalar on
+    x86) from oracle/_ref, or this repository's bit-identical restatement
+    when the reference build is absent.  Prefill is the reference's
+    token-by-token loop (engine.cpp:580-583), timed on a token subset and
+    scaled linearly (every token does the same work)."""
+
+    def __init__(self):
+        import oracle
+        self.oracle = oracle
+        self.ref = oracle.ref()
+        self.kind = "reference" if self.ref is not None else "port"
+
+    def mv(self, w, type_, rows, cols, x, y):
+        if self.ref is not None:
+            self.ref.q3xr_try_mv(w.ctypes.data, type_, rows, cols, x.ctypes.data, y.ctypes.data)
+        else:
+            self.oracle.lib().q3xo_mv_rows(w.ctypes.data, type_, 0, rows, cols, x.ctypes.data, y.ctypes.data)
+
+    def entry(self, value, unit, sample):
+        return {"value": value, "unit": unit, "cores": 1, "kind": self.kind,
+                "sample": f"{sample}; single thread; host nproc={os.cpu_count()}"}
+
+
+def cpu_matvecs(cpu, mats, seconds):
+    """Seconds of one pass of the reference mv over `mats` (one token)."""
+    import numpy as np
+    hosts = [(m, np.ascontiguousarray(m.weight.cpu().numpy())) for m in mats]
+    x = np.random.default_rng(1).normal(0, 1, max(m.cols for m in mats)).astype(np.float32)
+    ys = [np.empty(m.rows, np.float32) for m in mats]
+
+    def one_pass():
+        for (m, w), y in zip(hosts, ys):
+            cpu.mv(w, m.type, m.rows, m.cols, x, y)
+    return cpu_median(one_pass, seconds)
+
+
+def extra_configs(torch, q3x, wl, only=None, cpu=False):
     out = {}
     want = (lambda c: only is None or c in only)
+    ref_cpu = CpuReference() if cpu else None
     if want("cfg0"):
         # config 0: one Q8_0 4096x4096 matvec, copies rotated
         m = wl.dense_matrices(0)[0]
@@ -279,6 +330,10 @@ def extra_configs(torch, q3x, wl, only=None):
         y = torch.empty(4096, dtype=torch.float32, device="cuda")
         ms = time_graph(torch, lambda i: q3x.mv(q3x.Linear(ws[i % n], 4096, 4096, m.type), x, y), 4 * n, 20)
         out["cfg0_q8_mv_4096"] = {"GBps": mv_bytes(m) / (ms * 1e-3) / 1e9, "us": ms * 1e3, "copies": n}
+        if ref_cpu:
+            t, reps = cpu_matvecs(ref_cpu, [m], 1.0)
+            out["cfg0_q8_mv_4096"]["cpu_baseline"] = ref_cpu.entry(
+                mv_bytes(m) / t / 1e9, "GB/s", f"the 4096x4096 matvec, median of {reps} calls ({t * 1e3:.1f} ms each)")
         del ws
     if want("cfg2"):
         # config 2: Q8_0 prefill GEMM, N in {512, 4096}
@@ -296,6 +351,16 @@ def extra_configs(torch, q3x, wl, only=None):
             out[f"cfg2_q8_gemm_N{count}"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
                                              "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
             del X, H, Ys
+        if ref_cpu:
+            # one token through gate, up and down, the reference's prefill unit
+            t, reps = cpu_matvecs(ref_cpu, mats, 2.0)
+            per_token = sum(2.0 * mm.rows * mm.cols for mm in mats)
+            for count in (512, 4096):
+                out[f"cfg2_q8_gemm_N{count}"]["cpu_baseline"] = ref_cpu.entry(
+                    per_token / t / 1e12, "TFLOP/s",
+                    f"the reference's prefill, one mv per token and matrix (engine.cpp:580-583): {reps} tokens "
+                    f"through gate/up/down ({t * 1e3:.0f} ms per token, median), scaled to N={count}: "
+                    f"{count * t:.1f} s")
         del mats
     if want("cfg3"):
         # config 3: Q4_0 27B FFN at N = 1 (matvec) and N = 512 (GEMM)
@@ -326,6 +391,15 @@ def extra_configs(torch, q3x, wl, only=None):
         flops = sum(2.0 * 512 * mm.rows * mm.cols for mm in mats)
         out["cfg3_q4_gemm_N512"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
                                     "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+        if ref_cpu:
+            t, reps = cpu_matvecs(ref_cpu, mats, 2.0)
+            out["cfg3_q4_mv_27b_ffn"]["cpu_baseline"] = ref_cpu.entry(
+                alg / t / 1e9, "GB/s", f"gate, up and down matvecs, median of {reps} passes ({t * 1e3:.0f} ms each)")
+            per_token = sum(2.0 * mm.rows * mm.cols for mm in mats)
+            out["cfg3_q4_gemm_N512"]["cpu_baseline"] = ref_cpu.entry(
+                per_token / t / 1e12, "TFLOP/s",
+                f"the reference's prefill, one mv per token and matrix (engine.cpp:580-583): {reps} tokens "
+                f"({t * 1e3:.0f} ms per token, median), scaled to N=512: {512 * t:.1f} s")
         del mats, X, H, Ys
     if want("cfg4"):
         # config 4: Q4_0 routed MoE (router + experts), decode and 2048-token prefill
@@ -349,15 +423,72 @@ def extra_configs(torch, q3x, wl, only=None):
             if T == 1:
                 per_expert = (moe.gate_up.numel() + moe.down.numel()) // moe.experts
                 alg = k * per_expert
-                out["cfg4_q4_moe_decode"] = {"GBps": alg / (ms * 1e-3) / 1e9, "us": ms * 1e3,
-                                             "router_us": router_ms * 1e3,
-                                             "note": "router + 8 experts per call; the same token's 14 MB of "
-                                                     "expert weights repeat, so the Infinity Cache serves them"}
+                # Decode from HBM: 64 distinct tokens in turn, so consecutive
+                # calls read other experts and a rotation (64 x 14 MB) is far
+                # past the 256 MB Infinity Cache.
+                R = 64
+                logits_r = wl.router_logits(4, R, moe.experts)
+                X_r = wl.activations(4, R, moe.H, salt=3)
+                ids_r = torch.empty((R, k), dtype=torch.int32, device="cuda")
+                wts_r = torch.empty((R, k), dtype=torch.float32, device="cuda")
+
+                def run_moe_rot(i):
+                    j = i % R
+                    q3x.router_top_k(logits_r[j:j + 1], 1, moe.experts, k, ids_r[j], wts_r[j])
+                    q3x.moe_routed(moe.gate_up_linear, moe.down_linear, X_r[j:j + 1], 1, ids_r[j], wts_r[j], k, Y,
+                                   workspace=wsb)
+                ms_rot = time_graph(torch, run_moe_rot, R, 10)
+                distinct = int(torch.unique(ids_r).numel())
+                out["cfg4_q4_moe_decode"] = {
+                    "GBps": alg / (ms_rot * 1e-3) / 1e9, "us": ms_rot * 1e3, "bytes": alg,
+                    "router_us": router_ms * 1e3, "us_same_token": ms * 1e3,
+                    "note": f"router + 8 experts per call, 64 distinct tokens in turn ({distinct} of 256 experts "
+                            "read per rotation); us_same_token repeats one token, whose 14 MB the Infinity "
+                            "Cache then serves"}
+                if ref_cpu:
+                    import numpy as np
+                    gu_h = np.ascontiguousarray(moe.gate_up.cpu().numpy())
+                    dn_h = np.ascontiguousarray(moe.down.cpu().numpy())
+                    lg_h = np.ascontiguousarray(logits_r.cpu().numpy())
+                    X_h = np.ascontiguousarray(X_r.cpu().numpy())
+                    sel = np.empty(k, np.int32)
+                    prob = np.empty(moe.experts, np.float32)
+                    y_h = np.empty(moe.H, np.float32)
+                    state = {"j": 0}
+
+                    def cpu_token():
+                        j = state["j"] % R
+                        state["j"] += 1
+                        self_ref = ref_cpu.ref
+                        if self_ref is not None:
+                            self_ref.q3xr_router_top_k(lg_h[j].ctypes.data, moe.experts, k, sel.ctypes.data,
+                                                       prob.ctypes.data)
+                            w_sel = np.ascontiguousarray(prob[sel])
+                            self_ref.q3xr_moe_routed(moe.type, gu_h.ctypes.data, dn_h.ctypes.data, moe.experts,
+                                                     moe.H, moe.I, X_h[j].ctypes.data, sel.ctypes.data,
+                                                     w_sel.ctypes.data, k, y_h.ctypes.data)
+                        else:
+                            ids_o, w_o, _ = ref_cpu.oracle.router_top_k(lg_h[j], k)
+                            ref_cpu.oracle.moe_routed(gu_h, dn_h, moe.type, moe.experts, moe.H, moe.I, X_h[j],
+                                                      ids_o, w_o, threads=1)
+                    t_tok, reps = cpu_median(cpu_token, 2.0, 64)
+                    out["cfg4_q4_moe_decode"]["cpu_baseline"] = ref_cpu.entry(
+                        alg / t_tok / 1e9, "GB/s",
+                        f"router_top_k + the routed loop of moe() (engine.cpp:377-420) per token, median of {reps} "
+                        f"of the same 64 tokens ({t_tok * 1e3:.1f} ms each)")
+                    flops_tok = 2.0 * k * 3 * moe.I * moe.H
+                    cpu4_prefill = ref_cpu.entry(
+                        flops_tok / t_tok / 1e12, "TFLOP/s",
+                        f"the reference's prefill is the same per-token loop (engine.cpp:580-583): "
+                        f"{t_tok * 1e3:.1f} ms per token (median of {reps}), scaled to T=2048: {2048 * t_tok:.1f} s")
+                del logits_r, X_r, ids_r, wts_r
             else:
                 flops = 2.0 * T * k * (2 * moe.I * moe.H + moe.H * moe.I)
                 out["cfg4_q4_moe_prefill_T2048"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
                                                     "router_ms": router_ms,
                                                     "frac_fp32_mfma": flops / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+                if ref_cpu:
+                    out["cfg4_q4_moe_prefill_T2048"]["cpu_baseline"] = cpu4_prefill
             del logits, X, ids, wts, Y, wsb
         # The whole MoE layer (engine.cpp:406-430): BF16 router, top-k,
         # routed experts and the sigmoid-gated shared expert, one call.
@@ -466,7 +597,7 @@ def main():
         roofline_only(torch, q3x, wl, args.steps)
         return
     if args.only:
-        print(json.dumps(extra_configs(torch, q3x, wl, set(args.only.split(",")))), flush=True)
+        print(json.dumps(extra_configs(torch, q3x, wl, set(args.only.split(",")), cpu=not args.no_cpu)), flush=True)
         return
     head = headline(torch, q3x, wl, args.steps, args.warmup)
     lm = head["lm_head"]
@@ -488,6 +619,9 @@ def main():
                                "(q/k/v/o 4096->4096, gate/up 4096->12288, down 12288->4096) + lm_head "
                                "4096->151936, batch 1", "launches": LAYER_LAUNCHES, "step_bytes": head["step_bytes"],
                    "weight_copies_rotated": head["copies"], "frac_of_hbm_peak": round(head["value"] / HBM_PEAK_GBS, 4),
+                   "seeds": {"base": wl.SEED_BASE, "rule": "config c: weights (SEED_BASE + c) * 1000 + matrix "
+                             "index, activations (SEED_BASE + c) * 1000 + 500 + salt, router logits "
+                             "(SEED_BASE + c) * 1000 + 700 + tokens (torch.Generator on cuda:0)"},
                    "per_launch": head["per_launch"]},
         "roofline": {"bound": "hbm", "achieved": round(lm["GBps"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(lm["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -496,7 +630,7 @@ def main():
                      "traffic_source": "profiles/pmc_traffic_lm_head_q8_0.txt" if traffic else None},
     }
     if not args.no_configs:
-        result["configs"] = extra_configs(torch, q3x, wl)
+        result["configs"] = extra_configs(torch, q3x, wl, cpu=not args.no_cpu)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(head["mats"], args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -53,6 +53,7 @@ _REF_SIGS = {
     "q3xr_moe_layer": (None, [_U, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "q3xr_model_load": (_I, [ctypes.c_char_p, _P, _P, _S, ctypes.POINTER(_S), ctypes.POINTER(ctypes.c_char_p)]),
     "q3xr_forward": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _P]),
+    "q3xr_moe_routed": (None, [_U, _P, _P, _I, _I, _I, _P, _P, _P, _I, _P]),
 }
 
 _lib = None

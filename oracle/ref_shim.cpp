@@ -79,6 +79,24 @@ void q3xr_moe_q4(const uint16_t* router, const void* gate_up, const void* down,
 }
 
 
+// The routed loop of moe() (engine.cpp:411-420) for one token with the
+// selection given: out = 0, then per slot expert_mv of gate_up, silu(gate) *
+// up, expert_mv of down and out += weight * down, with the reference's own
+// expert_mv and silu.  For the CPU baseline of the routed-expert benchmark.
+void q3xr_moe_routed(uint32_t type, const void* gate_up, const void* down, int experts, int H, int I,
+                     const float* input, const int* ids, const float* weights, int top_k, float* out) {
+    const auto t = static_cast<q3x_model::MatrixType>(type);
+    const q3x_backend::ExpertLinear gu {gate_up, experts, 2 * I, H, t};
+    const q3x_backend::ExpertLinear dn {down, experts, H, I, t};
+    std::vector<float> gate_up_out(2 * static_cast<size_t>(I)), h(I), d(H);
+    std::fill(out, out + H, 0.0f);
+    for (int slot = 0; slot < top_k; ++slot) {
+        q3x_backend::expert_mv(gu, ids[slot], input, gate_up_out.data());
+        for (int i = 0; i < I; ++i) h[i] = q3x_backend::silu(gate_up_out[i]) * gate_up_out[I + i];
+        q3x_backend::expert_mv(dn, ids[slot], h.data(), d.data());
+        for (int i = 0; i < H; ++i) out[i] += weights[slot] * d[i];
+    }
+}
 // engine.cpp:207-212, the BF16 branch of mv().
 void q3xr_mv_bf16(const uint16_t* weights, int rows, int cols, const float* x, float* y) {
     q3x_backend::mv({weights, rows, cols, q3x_model::MATRIX_BF16}, x, y);
