@@ -16,6 +16,7 @@ import numpy as np
 _DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_DIR, "liboracle.so")
 REF_PATH = os.path.join(_DIR, "_ref", "libq3x_ref.so")
+REF_AVX512_PATH = os.path.join(_DIR, "_ref", "libq3x_ref_avx512.so")
 
 Q8_0 = 1
 Q4_0 = 2
@@ -40,6 +41,7 @@ _SIGS = {
     "q3xo_quantize": (_I, [_U, _P, _S, _P]),
     "q3xo_mv_bf16": (_I, [_P, _I, _I, _P, _P]),
     "q3xo_moe_layer": (_I, [_P, _P, _P, _P, _P, _P, _P, _U, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _I]),
+    "q3xo_set_bf16_lanes": (_I, [_I]),
 }
 _REF_SIGS = {
     "q3xr_quantized_bytes": (_I, [_U, _I, _I, ctypes.POINTER(_S)]),
@@ -78,12 +80,59 @@ def lib():
     return _lib
 
 
+def host_has_avx512() -> bool:
+    """Whether this host's CPU reports AVX-512 F and BW (the reference's
+    x86 kernels need both, arch/cpu.cpp:112)."""
+    try:
+        flags = open("/proc/cpuinfo").read().split()
+    except OSError:
+        return False
+    return "avx512f" in flags and "avx512bw" in flags
+
+
+_builds = {}
+
+
+def ref_builds():
+    """The reference builds this host can run: [(name, handle, bf16_lanes)].
+    "x86-64-v3" is the portable build (scalar BF16 dots); "avx512" is built
+    with AVX-512 as the reference's -march=native build is on such a host
+    (BF16 matvec and FP32 dots through arch/x86/kernels.h)."""
+    out = []
+    for name, path, lanes, ok in (("x86-64-v3", REF_PATH, 1, True),
+                                  ("avx512", REF_AVX512_PATH, 16, host_has_avx512())):
+        if ok and os.path.exists(path):
+            if name not in _builds:
+                _builds[name] = _bind(path, _REF_SIGS)
+            out.append((name, _builds[name], lanes))
+    return out
+
+
 def ref():
-    """The reference build, or None when it was not built (no reference tree)."""
+    """The reference build matching this host's -march=native build: the
+    AVX-512 one where the CPU has AVX-512 F and BW, else the portable one;
+    None when neither was built (no reference tree)."""
     global _ref
-    if _ref is None and os.path.exists(REF_PATH):
-        _ref = _bind(REF_PATH, _REF_SIGS)
+    if _ref is None:
+        builds = ref_builds()
+        if builds:
+            _ref = builds[-1][1]
     return _ref
+
+
+def ref_variant():
+    """(name, bf16_lanes) of the build ref() returns, or None."""
+    h = ref()
+    for name, handle, lanes in ref_builds():
+        if handle is h:
+            return name, lanes
+    return None
+
+
+def set_bf16_lanes(lanes: int) -> None:
+    """Which reference BF16 dot the oracle restates: 1 (portable loop) or 16
+    (AVX-512)."""
+    assert lib().q3xo_set_bf16_lanes(lanes)
 
 
 def default_threads() -> int:
@@ -173,22 +222,29 @@ def moe_routed(gate_up: np.ndarray, down: np.ndarray, type_: int, experts: int, 
     return Y
 
 
-def mv_bf16(weights: np.ndarray, x: np.ndarray) -> np.ndarray:
-    """y = W x for a BF16 matrix given as uint16 [rows, cols] (engine.cpp:200-212)."""
+def mv_bf16(weights: np.ndarray, x: np.ndarray, bf16_lanes: int = 1) -> np.ndarray:
+    """y = W x for a BF16 matrix given as uint16 [rows, cols] (engine.cpp:200-212;
+    bf16_lanes 16: the AVX-512 dot of arch/x86/kernels.h:21-37)."""
     weights = np.ascontiguousarray(weights, np.uint16)
     x = np.ascontiguousarray(x, np.float32)
     rows, cols = weights.shape
     y = np.empty(rows, np.float32)
-    assert lib().q3xo_mv_bf16(_p(weights), rows, cols, _p(x), _p(y))
+    set_bf16_lanes(bf16_lanes)
+    try:
+        assert lib().q3xo_mv_bf16(_p(weights), rows, cols, _p(x), _p(y))
+    finally:
+        set_bf16_lanes(1)
     return y
 
 
 def moe_layer(router: np.ndarray, gate_up: np.ndarray, down: np.ndarray, shared_gate: np.ndarray,
               shared_up: np.ndarray, shared_down: np.ndarray, shared_scale: np.ndarray, type_: int,
               experts: int, H: int, I: int, shared_I: int, top_k: int, X: np.ndarray,
-              threads: int | None = None):
-    """The whole MoE layer (engine.cpp:406-430) for every row of X.
-    Returns (Y [T, H], ids [T, top_k], weights [T, top_k])."""
+              threads: int | None = None, bf16_lanes: int = 1):
+    """The whole MoE layer (engine.cpp:406-430) for every row of X, its BF16
+    router and gate dots as the portable loop (bf16_lanes 1) or the AVX-512
+    kernel (16) computes them.  Returns (Y [T, H], ids [T, top_k], weights
+    [T, top_k])."""
     X = np.ascontiguousarray(np.atleast_2d(X), np.float32)
     T = X.shape[0]
     Y = np.empty((T, H), np.float32)
@@ -196,9 +252,13 @@ def moe_layer(router: np.ndarray, gate_up: np.ndarray, down: np.ndarray, shared_
     weights = np.empty((T, top_k), np.float32)
     router = np.ascontiguousarray(router, np.uint16)
     shared_scale = np.ascontiguousarray(shared_scale, np.uint16)
-    assert lib().q3xo_moe_layer(_p(router), _p(gate_up), _p(down), _p(shared_gate), _p(shared_up),
-                                _p(shared_down), _p(shared_scale), type_, experts, H, I, shared_I, top_k,
-                                _p(X), T, _p(Y), _p(ids), _p(weights), threads or default_threads())
+    set_bf16_lanes(bf16_lanes)
+    try:
+        assert lib().q3xo_moe_layer(_p(router), _p(gate_up), _p(down), _p(shared_gate), _p(shared_up),
+                                    _p(shared_down), _p(shared_scale), type_, experts, H, I, shared_I, top_k,
+                                    _p(X), T, _p(Y), _p(ids), _p(weights), threads or default_threads())
+    finally:
+        set_bf16_lanes(1)
     return Y, ids, weights
 
 

@@ -325,10 +325,44 @@ static float bf16_value(uint16_t value) {
 }
 
 /* engine.cpp:200-205: sum += f32(a) * b, contracted to an FMA by the build. */
-static float dot_bf16(const uint16_t* a, const float* b, int n) {
+static float dot_bf16_scalar(const uint16_t* a, const float* b, int n) {
     float sum = 0.0f;
     for (int i = 0; i < n; ++i) sum = fmaf(bf16_value(a[i]), b[i], sum);
     return sum;
+}
+
+/* arch/x86/kernels.h:21-37, the BF16 dot a reference built with AVX-512 F and
+ * BW takes (arch/cpu.cpp:112-114, 202): lane j of a 16-wide vector
+ * accumulates fma(w[i], x[i]) for i = j mod 16 in element order; the lanes
+ * are reduced as GCC's _mm512_reduce_add_ps does (upper 8 + lower 8, upper 4
+ * + lower 4, then elements 0 + 2 and 1 + 3, then those two); the tail past
+ * the last 16 adds sum = fma(w[i], x[i], sum) in order. */
+static float dot_bf16_x16(const uint16_t* a, const float* b, int n) {
+    float lane[16] = {0};
+    int i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int j = 0; j < 16; ++j) lane[j] = fmaf(bf16_value(a[i + j]), b[i + j], lane[j]);
+    float t3[8], t6[4];
+    for (int j = 0; j < 8; ++j) t3[j] = lane[8 + j] + lane[j];
+    for (int j = 0; j < 4; ++j) t6[j] = t3[4 + j] + t3[j];
+    const float t8_0 = t6[0] + t6[2], t8_1 = t6[1] + t6[3];
+    float sum = t8_0 + t8_1;
+    for (; i < n; ++i) sum = fmaf(bf16_value(a[i]), b[i], sum);
+    return sum;
+}
+
+/* Which BF16 dot the reference build in use takes: 1 (portable scalar loop)
+ * or 16 (AVX-512). */
+static int bf16_lanes = 1;
+
+int q3xo_set_bf16_lanes(int lanes) {
+    if (lanes != 1 && lanes != 16) return 0;
+    bf16_lanes = lanes;
+    return 1;
+}
+
+static float dot_bf16(const uint16_t* a, const float* b, int n) {
+    return bf16_lanes == 16 ? dot_bf16_x16(a, b, n) : dot_bf16_scalar(a, b, n);
 }
 
 /* engine.cpp:207-212 (the BF16 branch of mv) */

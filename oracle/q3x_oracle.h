@@ -73,6 +73,11 @@ int q3xo_moe_layer(const uint16_t* router, const void* gate_up, const void* down
                    const uint16_t* shared_scale, uint32_t type, int experts, int H, int I,
                    int shared_I, int top_k, const float* X, int tokens, float* Y, int* ids,
                    float* weights, int threads);
+/* The BF16 dot of q3xo_mv_bf16 and q3xo_moe_layer: lanes 1 = the reference's
+ * portable loop (engine.cpp:200-205), 16 = its AVX-512 kernel
+ * (arch/x86/kernels.h:21-37), as a reference built with AVX-512 takes.
+ * Process-wide; 1 = ok, 0 = other values. */
+int q3xo_set_bf16_lanes(int lanes);
 /* pack_weights.py quantizers applied to float32 values (n % 32 == 0).
  * 1 = ok, 0 = partial block or non-finite input. */
 int q3xo_quantize(uint32_t type, const float* values, size_t n, void* out);

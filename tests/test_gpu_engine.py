@@ -35,7 +35,7 @@ def test_engine_logits_match_the_reference_forward(name):
     tokens = rng.integers(0, fields["V"], 12).astype(np.int32)
     want = oracle.ref_forward(fields, image, table, tokens)
     weights = dev(image)
-    say(f"engine {name}: {len(tokens)} tokens")
+    say(f"engine {name}: {len(tokens)} tokens, reference {oracle.ref_variant()[0]} build")
     with q3x.Engine(config, weights, context=len(tokens)) as engine:
         for i, tok in enumerate(tokens):
             engine.forward([tok])

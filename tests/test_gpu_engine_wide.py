@@ -60,7 +60,7 @@ def _check(got, want, what):
 @pytest.mark.parametrize("name", sorted(WIDE))
 def test_wide_prefill_then_decode_match_the_reference_forward(name, references):
     torch = _torch()
-    say(f"engine {name}: waiting for the reference forward")
+    say(f"engine {name}: waiting for the reference forward ({oracle.ref_variant()[0]} build)")
     config, image, tokens, want = references[name].result()
     say(f"engine {name}: prefill {PROMPT} (chunk {CHUNK}) + decode {DECODE}")
     weights = dev(image)
