@@ -59,24 +59,6 @@ __device__ float block_sum(float v, float* partial) {
     __syncthreads();
     return total;
 }
-// Two sums at once (one pair of barriers), each in block_sum's order.
-template <int THREADS>
-__device__ float2 block_sum2(float u, float v, float* partial) {
-    const float wu = wave_sum_f32(u), wv = wave_sum_f32(v);
-    if ((threadIdx.x & (kWave - 1)) == 0) {
-        partial[threadIdx.x / kWave] = wu;
-        partial[THREADS / kWave + threadIdx.x / kWave] = wv;
-    }
-    __syncthreads();
-    float2 total{0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < THREADS / kWave; ++i) {
-        total.x += partial[i];
-        total.y += partial[THREADS / kWave + i];
-    }
-    __syncthreads();
-    return total;
-}
 template <int THREADS>
 __device__ float block_max(float v, float* partial) {
     const float w = wave_max_f32(v);
@@ -154,7 +136,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_kernel(float* __restrict__ h
 // new history.  The arithmetic per token is the reference's (conv_token).
 // The history is kept in two copies, [2][channels][CK - 1]: a forward at
 // position p reads copy p % 2 and leaves copy (p + count) % 2, so a decode
-// step (delta_rule_kernel, which convolves its own channels) can read the
+// step (delta_step_kernel, which convolves its own channels) can read the
 // old history of a channel that another workgroup is updating.  SEGMENTS: 16
 // runs per channel.
 constexpr int kMaxConv = 8;
@@ -271,134 +253,17 @@ __device__ __forceinline__ void store_keys(float* col, int k0, int KD, bool ok, 
     }
 }
 
-// One value head of the gated delta rule (engine.cpp:262-316) for `count`
-// tokens in order: L2-normalised q and k of its key head (q also divided by
-// sqrt(KD)), beta = sigmoid(b), decay = -exp(A_log) * softplus(a + dt_bias);
-// the KD x VD memory S decays by exp(decay), takes k (beta (v - k S)), and
-// gives out = q S; then the gated RMSNorm with the FP32 norm weight and
-// SiLU(z) (engine.cpp:234-239).  1024 threads: thread t owns value column
-// t % 128 and keys 16 (t / 128) .. + 15, so its S entries stay in registers
-// across the tokens; sums over keys add the eight key groups' partials in a
-// fixed order.  Requires KD <= 128, VD <= 128.
-constexpr int kDeltaThreads = 1024;
-constexpr int kDeltaGroups = kDeltaThreads / 128;  // key groups
-constexpr int kDeltaKeys = 128 / kDeltaGroups;     // keys per thread
-
-__global__ __launch_bounds__(kDeltaThreads) void delta_rule_kernel(
-    const float* __restrict__ qkv, const float* __restrict__ a, const float* __restrict__ b,
-    const float* __restrict__ z, const float* __restrict__ alog, const uint16_t* __restrict__ dt,
-    const float* __restrict__ norm, float* __restrict__ memory, float* __restrict__ out,
-    const uint16_t* __restrict__ conv_w, float* __restrict__ history, const int* __restrict__ position, int CK,
-    int KH, int VH, int KD, int VD) {
-    __shared__ float qs[128], ks[128], part[kDeltaGroups][128], sum[128], partial[2 * kDeltaThreads / kWave];
-    const int head = blockIdx.x;
-    const int t = threadIdx.x;
-    const int DQK = KH * KD, DO = VH * VD, DQKV = 2 * DQK + DO;
-    const int kh = head / (VH / KH);
-    const int v = t & 127, group = t >> 7;
-    const bool col = v < VD;
-    float* S = memory + (static_cast<size_t>(head) * VD + (col ? v : 0)) * KD;  // column v
-    float s[kDeltaKeys];
-    load_keys<kDeltaKeys>(S, group * kDeltaKeys, KD, col, s);
-    const float A = expf(alog[head]);
-    const float bias = bf16_value(dt[head]);
-    const float nv = norm[t < VD ? t : 0];
-    // The causal conv of this head's channels (q and k of its key head, its
-    // v), read from history copy p % 2; the new history goes to copy (p + 1)
-    // % 2 -- for q and k only from the key head's first value head.
-    // Per-head and per-column inputs requested up front, with S.
-    const float a_in = a[head], b_in = b[head];
-    const float z_in = t < VD ? z[static_cast<size_t>(head) * VD + t] : 0.0f;
-    const int pos = *position;
-    const size_t copy = static_cast<size_t>(DQKV) * (CK - 1);
-    const float* hin = history + (pos & 1) * copy;
-    float* hout = history + ((pos + 1) & 1) * copy;
-    const bool qk_writer = head % (VH / KH) == 0;
-    {
-        const int r = 0;
-        const float* row = qkv + static_cast<size_t>(r) * DQKV;
-        const int cq = kh * KD + t, ck = DQK + kh * KD + t, cv = 2 * DQK + head * VD + v;
-        const float qv = t < KD ? conv_token(row[cq], hin + static_cast<size_t>(cq) * (CK - 1),
-                                             conv_w + static_cast<size_t>(cq) * CK, CK,
-                                             qk_writer ? hout + static_cast<size_t>(cq) * (CK - 1) : nullptr)
-                                : 0.0f;
-        const float kv = t < KD ? conv_token(row[ck], hin + static_cast<size_t>(ck) * (CK - 1),
-                                             conv_w + static_cast<size_t>(ck) * CK, CK,
-                                             qk_writer ? hout + static_cast<size_t>(ck) * (CK - 1) : nullptr)
-                                : 0.0f;
-        const float vv = col ? conv_token(row[cv], hin + static_cast<size_t>(cv) * (CK - 1),
-                                          conv_w + static_cast<size_t>(cv) * CK, CK,
-                                          group == 0 ? hout + static_cast<size_t>(cv) * (CK - 1) : nullptr)
-                             : 0.0f;
-        const float2 n2 = block_sum2<kDeltaThreads>(qv * qv, kv * kv, partial);
-        const float qn = n2.x, kn = n2.y;
-        if (t < KD) {
-            qs[t] = qv * (1.0f / sqrtf(qn + kEps)) / sqrtf(static_cast<float>(KD));
-            ks[t] = kv * (1.0f / sqrtf(kn + kEps));
-        }
-        __syncthreads();
-        const float beta = sigmoid_ref(b_in);
-        const float decay = -A * softplus_ref(a_in + bias);
-        const float scale = expf(decay);
-        float pred = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kDeltaKeys; ++j) {
-            const int key = group * kDeltaKeys + j;
-            s[j] *= scale;
-            if (key < KD) pred = fmaf(ks[key], s[j], pred);
-        }
-        part[group][v] = pred;
-        __syncthreads();
-        if (t < 128) {
-            float p = part[0][t];
-#pragma unroll
-            for (int g = 1; g < kDeltaGroups; ++g) p += part[g][t];
-            sum[t] = p;
-        }
-        __syncthreads();
-        const float delta = vv - sum[v];
-        float o = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kDeltaKeys; ++j) {
-            const int key = group * kDeltaKeys + j;
-            if (key < KD) {
-                s[j] = fmaf(ks[key] * beta, delta, s[j]);
-                o = fmaf(qs[key], s[j], o);
-            }
-        }
-        __syncthreads();  // every read of part / sum / qs / ks above is done
-        part[group][v] = o;
-        __syncthreads();
-        // Every wave forms all 128 column results (lane l: columns l and
-        // l + 64; zero past VD) and their squares' sum itself, so the gated
-        // norm needs no further barrier; waves 0 and 1 store.
-        const int lane = t & (kWave - 1);
-        float r0 = part[0][lane], r1 = part[0][lane + kWave];
-#pragma unroll
-        for (int g = 1; g < kDeltaGroups; ++g) {
-            r0 += part[g][lane];
-            r1 += part[g][lane + kWave];
-        }
-        const float sq = wave_sum_f32(fmaf(r1, r1, r0 * r0));
-        if (t < VD) {
-            const float result = t < kWave ? r0 : r1;
-            const float g = 1.0f / sqrtf(sq / static_cast<float>(VD) + kEps);
-            const size_t at = static_cast<size_t>(r) * DO + head * VD + t;
-            out[at] = result * (g * nv * silu_ref(z_in));
-        }
-    }
-    store_keys<kDeltaKeys>(S, group * kDeltaKeys, KD, col, s);
-}
-
 // Prefill form of the delta rule, in three launches so that only the
 // recurrence itself runs token by token:
 //   delta_prep_kernel (row r, key head kh; parallel): q, k of the head
 //     L2-normalised in place (q also divided by sqrt(KD)); for the value
 //     heads of kh, b <- beta = sigmoid(b) and a <- exp(decay) in place;
 //   delta_scan_kernel (value head; sequential over the rows): the memory
-//     update of delta_rule_kernel, writing q S unnormalised;
-//   delta_norm_kernel (row, value head; parallel): the gated RMSNorm.
-// The arithmetic of each step is delta_rule_kernel's.
+//     update of the gated delta rule (engine.cpp:262-316), writing q S
+//     unnormalised;
+//   delta_norm_kernel (row, value head; parallel): the gated RMSNorm
+//     (engine.cpp:234-239).
+// A decode step runs the same arithmetic for one token (delta_step_kernel).
 constexpr int kScanTile = 32;  // rows of q / k staged in LDS at a time
 
 __global__ __launch_bounds__(128) void delta_prep_kernel(float* __restrict__ qkv, float* __restrict__ a,
@@ -542,6 +407,114 @@ __global__ __launch_bounds__(kScanThreads) void delta_scan_kernel(const float* _
             o += dpp_f32<0x141>(o);
             if (lane % kScanGroups == 0 && col) out[static_cast<size_t>(r0 + rr) * DO + head * VD + c] = o;
         }
+    }
+    store_keys<kScanKeys>(S, k0, KD, col, s);
+}
+
+// One decode token of the gated delta rule (engine.cpp:262-316) in the
+// layout of delta_scan_kernel: a value head's columns over kScanSlices
+// workgroups of 4 waves, lane l of wave w owning column 32 slice + 8 w + l / 8
+// and keys 16 (l % 8) .. + 15, the sums over keys DPP adds inside row halves,
+// and the scan's arithmetic per token (k S once scaled by e^decay, S e^decay +
+// k (beta delta), q S).  The token's causal conv runs here too (conv_token):
+// thread t convolves q channel t (t < 128) or k channel t - 128 of the key
+// head and the first kScanCols threads the slice's v channels, from history
+// copy p % 2 into copy (p + 1) % 2 -- q and k only from slice 0 of the key
+// head's first value head; then the L2 norms of q and k (q also divided by
+// sqrt(KD)), beta = sigmoid(b) and e^decay as delta_prep_kernel forms them.
+// Writes q S unnormalised and, for the gated RMSNorm that follows in the out
+// projection's input staging (GatedNormInput), gate = norm * silu(z) of each
+// column, formed once here (delta_norm_kernel, the fallback, uses z itself).
+__global__ __launch_bounds__(kScanThreads) void delta_step_kernel(
+    const float* __restrict__ qkv, const float* __restrict__ a, const float* __restrict__ b,
+    const float* __restrict__ z, const float* __restrict__ alog, const uint16_t* __restrict__ dt,
+    const float* __restrict__ norm, float* __restrict__ memory, float* __restrict__ out,
+    float* __restrict__ gate, const uint16_t* __restrict__ conv_w, float* __restrict__ history,
+    const int* __restrict__ position, int CK, int KH, int VH, int KD, int VD) {
+    __shared__ __attribute__((aligned(16))) float qk[256];  // q (0 .. 127), k (128 .. 255), zeros past KD
+    __shared__ float vs[kScanCols];
+    __shared__ float squares[kScanThreads / kWave];
+    const int head = blockIdx.x / kScanSlices, slice = blockIdx.x % kScanSlices;
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1), wave = t / kWave;
+    const int DQK = KH * KD, DO = VH * VD, DQKV = 2 * DQK + DO;
+    const int per = VH / KH, kh = head / per;
+    const int cl = wave * (kWave / kScanGroups) + lane / kScanGroups;  // column within the slice
+    const int c = slice * kScanCols + cl, k0 = (lane % kScanGroups) * kScanKeys;
+    const bool col = c < VD;
+    float* S = memory + (static_cast<size_t>(head) * VD + (col ? c : 0)) * KD;  // column c
+    float s[kScanKeys];
+    load_keys<kScanKeys>(S, k0, KD, col, s);
+    const float a_in = a[head], b_in = b[head];
+    const int pos = *position;
+    const size_t copy = static_cast<size_t>(DQKV) * (CK - 1);
+    const float* hin = history + (pos & 1) * copy;
+    float* hout = history + ((pos + 1) & 1) * copy;
+    const bool qk_writer = head % per == 0 && slice == 0;
+    // q | k channel of this thread (t < 128: q, else k), convolved.
+    const int ch = t & 127;
+    float x = 0.0f;
+    if (ch < KD) {
+        const int ci = (t < 128 ? 0 : DQK) + kh * KD + ch;
+        x = conv_token(qkv[ci], hin + static_cast<size_t>(ci) * (CK - 1), conv_w + static_cast<size_t>(ci) * CK, CK,
+                       qk_writer ? hout + static_cast<size_t>(ci) * (CK - 1) : nullptr);
+    }
+    if (t < kScanCols) {
+        const int cv = slice * kScanCols + t;
+        float v = 0.0f;
+        if (cv < VD) {
+            const int ci = 2 * DQK + head * VD + cv;  // each v channel belongs to one slice
+            v = conv_token(qkv[ci], hin + static_cast<size_t>(ci) * (CK - 1), conv_w + static_cast<size_t>(ci) * CK,
+                           CK, hout + static_cast<size_t>(ci) * (CK - 1));
+        }
+        vs[t] = v;
+    }
+    // L2 norms: waves 0, 1 hold q, waves 2, 3 hold k.
+    const float sq = wave_sum_f32(x * x);
+    if (lane == 0) squares[wave] = sq;
+    __syncthreads();
+    if (t < 128) qk[t] = x * (1.0f / sqrtf(squares[0] + squares[1] + kEps)) / sqrtf(static_cast<float>(KD));
+    else qk[t] = x * (1.0f / sqrtf(squares[2] + squares[3] + kEps));
+    __syncthreads();
+    const float bb = sigmoid_ref(b_in);
+    const float sc = expf(-expf(alog[head]) * softplus_ref(a_in + bf16_value(dt[head])));
+    const f32x4* kp = reinterpret_cast<const f32x4*>(qk + 128 + k0);
+    const f32x4* qp = reinterpret_cast<const f32x4*>(qk + k0);
+    float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+    for (int j4 = 0; j4 < kScanKeys / 4; ++j4) {
+        const f32x4 kk = kp[j4];
+        p0 = fmaf(kk.x, s[4 * j4 + 0], p0);
+        p1 = fmaf(kk.y, s[4 * j4 + 1], p1);
+        p0 = fmaf(kk.z, s[4 * j4 + 2], p0);
+        p1 = fmaf(kk.w, s[4 * j4 + 3], p1);
+    }
+    float pred = p0 + p1;
+    pred += dpp_f32<0xB1>(pred);   // the eight key groups: pairs,
+    pred += dpp_f32<0x4E>(pred);   // quads,
+    pred += dpp_f32<0x141>(pred);  // the two quads of the row half
+    const float bd = bb * (vs[cl] - sc * pred);  // beta (v - k S e^decay)
+    float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+    for (int j4 = 0; j4 < kScanKeys / 4; ++j4) {
+        const f32x4 kk = kp[j4], qq = qp[j4];
+        s[4 * j4 + 0] = fmaf(s[4 * j4 + 0], sc, kk.x * bd);
+        s[4 * j4 + 1] = fmaf(s[4 * j4 + 1], sc, kk.y * bd);
+        s[4 * j4 + 2] = fmaf(s[4 * j4 + 2], sc, kk.z * bd);
+        s[4 * j4 + 3] = fmaf(s[4 * j4 + 3], sc, kk.w * bd);
+        o0 = fmaf(qq.x, s[4 * j4 + 0], o0);
+        o1 = fmaf(qq.y, s[4 * j4 + 1], o1);
+        o0 = fmaf(qq.z, s[4 * j4 + 2], o0);
+        o1 = fmaf(qq.w, s[4 * j4 + 3], o1);
+    }
+    float o = o0 + o1;
+    o += dpp_f32<0xB1>(o);
+    o += dpp_f32<0x4E>(o);
+    o += dpp_f32<0x141>(o);
+    if (lane % kScanGroups == 0 && col) {
+        const size_t at = static_cast<size_t>(head) * VD + c;
+        out[at] = o;
+        gate[at] = norm[c] * silu_ref(z[at]);
     }
     store_keys<kScanKeys>(S, k0, KD, col, s);
 }
@@ -1007,6 +980,77 @@ struct SwiGLUInput {
     }
 };
 
+// Input staging of a DeltaNet layer's out projection in a decode step
+// (mv_pipe_kernel's `In`): x = the gated RMSNorm of the delta rule's raw
+// output o (engine.cpp:234-239): per value head h, g = 1 / sqrt(mean(o_h^2) +
+// eps), x = o * (g * gate), gate = norm[j] * silu(z) formed by
+// delta_step_kernel.  Every workgroup forms it on the way into LDS: each
+// thread loads its chunks of o and gate in one round trip (the first kHeld
+// stay in registers) and copies o to LDS; then 16-lane groups take the heads
+// (group G: heads G, G + groups, ...), lane i summing the squares of columns
+// i, i + 16, ... in order with FMAs and the group adding its lanes with DPP,
+// so every workgroup holds the same scales; then each thread scales its
+// chunks.  Requires VD % 4 == 0 and at most 256 heads (the scales use the
+// 1 KB work area).
+struct GatedNormInput {
+    static constexpr int kHeld = 4;
+    const float* gate;  // [VH * VD]: norm[j] * silu(z)
+    int VD;
+    __device__ void stage(const float* o, uint8_t* xl, int bpr, float* work) const {
+        const int chunks = bpr * 8;
+        const int heads = bpr * kBlock / VD;
+        const int B = blockDim.x;
+        const f32x4* os = reinterpret_cast<const f32x4*>(o);
+        const f32x4* gs = reinterpret_cast<const f32x4*>(gate);
+        auto at = [&](int ck) { return reinterpret_cast<f32x4*>(xl + x_block_offset(ck >> 3) + 16 * (ck & 7)); };
+        f32x4 orr[kHeld], grr[kHeld];
+#pragma unroll
+        for (int k = 0; k < kHeld; ++k) {
+            const int ck = threadIdx.x + k * B;
+            if (ck < chunks) {
+                orr[k] = os[ck];
+                grr[k] = gs[ck];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kHeld; ++k) {
+            const int ck = threadIdx.x + k * B;
+            if (ck < chunks) *at(ck) = orr[k];
+        }
+        for (int ck = threadIdx.x + kHeld * B; ck < chunks; ck += B) *at(ck) = os[ck];
+        __syncthreads();
+        const int li = threadIdx.x & 15, group = threadIdx.x / 16, groups = B / 16;
+        for (int h0 = 0; h0 < heads; h0 += groups) {
+            // Every lane of the block takes part (group_sum needs whole waves).
+            const int h = h0 + group;
+            float sq = 0.0f;
+            if (h < heads)
+                for (int j = li; j < VD; j += 16) {
+                    const float v = *lds_x(xl, h * VD + j);
+                    sq = fmaf(v, v, sq);
+                }
+            const float total = group_sum<16>(sq);
+            if (li == 0 && h < heads) work[h] = 1.0f / sqrtf(total / static_cast<float>(VD) + kEps);
+        }
+        __syncthreads();
+        auto put = [&](int ck, f32x4 v, f32x4 w) {
+            const float g = work[4 * ck / VD];
+            v.x = v.x * (g * w.x);
+            v.y = v.y * (g * w.y);
+            v.z = v.z * (g * w.z);
+            v.w = v.w * (g * w.w);
+            *at(ck) = v;
+        };
+#pragma unroll
+        for (int k = 0; k < kHeld; ++k) {
+            const int ck = threadIdx.x + k * B;
+            if (ck < chunks) put(ck, orr[k], grr[k]);
+        }
+        for (int ck = threadIdx.x + kHeld * B; ck < chunks; ck += B) put(ck, *at(ck), gs[ck]);
+        __syncthreads();
+    }
+};
+
 // The first index of the largest logit (std::max_element, engine.cpp:606-610).
 __global__ __launch_bounds__(kNormThreads) void argmax_kernel(const float* __restrict__ x, int n, int* __restrict__ out) {
     __shared__ float bv[kNormThreads / kWave];
@@ -1096,6 +1140,7 @@ struct q3x_hip_engine {
     void* arena = nullptr;
     float *hidden = nullptr, *normalized = nullptr, *branch = nullptr, *logits = nullptr;
     float *qkv = nullptr, *z = nullptr, *a = nullptr, *b = nullptr, *delta_out = nullptr;
+    float* delta_gate = nullptr;  // a decode step's norm[j] * silu(z) of the gated RMSNorm, [VH * VD]
     float *query_and_gate = nullptr, *query = nullptr, *gate = nullptr, *key = nullptr, *value = nullptr;
     float *attn_out = nullptr, *scores = nullptr, *ffn_gate = nullptr, *ffn_up = nullptr;
     float *recurrent = nullptr, *checkpoint_recurrent = nullptr, *checkpoint_logits = nullptr;
@@ -1183,7 +1228,7 @@ int mv_staged(const Mat* m, float* const* y, const bool* add, int n, uint32_t ty
 int enqueue(q3x_hip_engine& e, int count, bool logits) {
     const q3x_hip_model_config& c = e.c;
     hipStream_t s = e.stream;
-    const int DQKV = 2 * c.KH * c.KD + c.VH * c.VD;
+    const int DO = c.VH * c.VD, DQKV = 2 * c.KH * c.KD + DO;
     const uint32_t type = c.matrix_type;
     const dim3 eg((c.H + 255) / 256, count);
     if (type == Q3X_HIP_MATRIX_Q8_0)
@@ -1216,10 +1261,22 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
         if (rc) break;
         if (!L.attention) {
             if (count == 1) {
-                // The conv of the step's channels runs inside the delta rule.
-                hipLaunchKernelGGL(delta_rule_kernel, dim3(c.VH), dim3(kDeltaThreads), 0, s, e.qkv, e.a, e.b, e.z,
-                                   L.alog, L.dt, L.norm, L.memory, e.delta_out, L.conv, L.conv_state, e.d_position,
-                                   c.CK, c.KH, c.VH, c.KD, c.VD);
+                // The conv of the step's channels runs inside the delta rule;
+                // the gated norm inside the out projection's staging.
+                hipLaunchKernelGGL(delta_step_kernel, dim3(c.VH * kScanSlices), dim3(kScanThreads), 0, s, e.qkv, e.a,
+                                   e.b, e.z, L.alog, L.dt, L.norm, L.memory, e.delta_out, e.delta_gate, L.conv,
+                                   L.conv_state, e.d_position, c.CK, c.KH, c.VH, c.KD, c.VD);
+                const bool add_out[1] = {true};
+                float* const out_y[1] = {e.hidden};
+                rc = c.VD % 4 == 0 && c.VH <= 256
+                         ? mv_staged(&L.out, out_y, add_out, 1, type, DO, e.delta_out,
+                                     GatedNormInput{e.delta_gate, c.VD}, s)
+                         : Q3X_HIP_ENOTSUP;
+                if (rc == Q3X_HIP_ENOTSUP) {
+                    hipLaunchKernelGGL(delta_norm_kernel, dim3(c.VH, 1), dim3(128), 0, s, e.delta_out, e.z, L.norm,
+                                       c.VH, c.VD);
+                    rc = apply(L.out, type, e.delta_out, count, e.hidden, true, s);
+                }
             } else {
                 hipLaunchKernelGGL(delta_conv_kernel<16>, dim3((DQKV + kConvThreads / 16 - 1) / (kConvThreads / 16)),
                                    dim3(kConvThreads), 0, s, e.qkv, L.conv, L.conv_state, e.d_position, DQKV, c.CK,
@@ -1230,8 +1287,8 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                                    e.a, e.b, L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD, count);
                 hipLaunchKernelGGL(delta_norm_kernel, dim3(c.VH, count), dim3(128), 0, s, e.delta_out, e.z, L.norm,
                                    c.VH, c.VD);
+                rc = apply(L.out, type, e.delta_out, count, e.hidden, true, s);
             }
-            rc = apply(L.out, type, e.delta_out, count, e.hidden, true, s);
         } else {
             hipLaunchKernelGGL(attention_prep_kernel, dim3(c.AH + c.KVH, count), dim3(kHeadThreads), 0, s,
                                e.query_and_gate, e.key, e.value, L.qnorm, L.knorm, e.d_position, e.query, e.gate,
@@ -1446,6 +1503,7 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
         e->a = f(R * c.VH);
         e->b = f(R * c.VH);
         e->delta_out = f(R * DO);
+        e->delta_gate = f(DO);
         e->query_and_gate = f(R * 2 * AS);
         e->query = f(R * AS);
         e->gate = f(R * AS);
