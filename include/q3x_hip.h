@@ -350,6 +350,10 @@ int q3x_hip_model_moe_layer(const q3x_hip_model* model, int layer,
 
 typedef struct q3x_hip_engine q3x_hip_engine;
 
+enum {
+    Q3X_HIP_ESTATE = -6, /* engine left failed by an earlier forward; reset or restore it */
+};
+
 /* An engine over `weights`, a device buffer laid out as q3x_hip_model_schema
  * gives for `config` (the buffer of q3x_hip_model_load qualifies), with room
  * for `context` tokens (1 .. 262144).  A forward of several tokens runs as
@@ -363,14 +367,20 @@ int q3x_hip_engine_create(const q3x_hip_model_config* config, const void* weight
                           q3x_hip_engine** engine, const char** error);
 void q3x_hip_engine_destroy(q3x_hip_engine* engine);
 
-/* Position 0 and a zero recurrent state (state_reset, engine.cpp:158-162). */
+/* Position 0 and a zero recurrent state (state_reset, engine.cpp:158-162).
+ * Also clears the failed state a forward can leave (below). */
 int q3x_hip_engine_reset(q3x_hip_engine* engine);
 
 /* tokens[0 .. count) (host) through the model at the current position, one
  * token at a time as the reference's state_forward (engine.cpp:586-589);
  * the logits of the last token when compute_logits.  Returns when done.
  * Q3X_HIP_EINVAL for a token outside [0, V) or more tokens than the context
- * has left (nothing is run). */
+ * has left (nothing is run).  A failure once work has been queued (a later
+ * prefill chunk, the decode graph, the wait for the stream) returns its
+ * code after the queued work has ended and leaves the engine failed: the
+ * state may hold part of the tokens, so every forward returns
+ * Q3X_HIP_ESTATE, running nothing, until q3x_hip_engine_reset or
+ * q3x_hip_engine_checkpoint_restore (the reference aborts instead). */
 int q3x_hip_engine_forward(q3x_hip_engine* engine, const int* tokens, int count, int compute_logits);
 
 /* The last computed logits [V] into host memory (state_copy_logits). */
@@ -380,7 +390,8 @@ int q3x_hip_engine_logits(const q3x_hip_engine* engine, float* logits);
 int q3x_hip_engine_argmax(const q3x_hip_engine* engine, int* token);
 
 /* Save / restore position, recurrent state and logits
- * (state_checkpoint_save / _restore, engine.cpp:590-604). */
+ * (state_checkpoint_save / _restore, engine.cpp:590-604).  A restore also
+ * clears the failed state. */
 int q3x_hip_engine_checkpoint_save(q3x_hip_engine* engine);
 int q3x_hip_engine_checkpoint_restore(q3x_hip_engine* engine);
 

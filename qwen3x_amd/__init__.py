@@ -30,6 +30,7 @@ ERUNTIME = -2
 ENOTSUP = -3
 EMODEL = -4
 ESCRATCH = -5
+ESTATE = -6
 # Static per-device scratch of q3x_hip_moe_routed_noalloc (Q3X_HIP_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = 32 << 20
 

@@ -1132,6 +1132,10 @@ struct q3x_hip_engine {
     int capacity = 0;
     int chunk = 0;                // rows of a prefill chunk
     int position = 0;             // host mirror of *d_position
+    // A forward failed after it had started work on the device: the state
+    // may hold part of its tokens.  Forward refuses to run until a reset or
+    // a checkpoint restore puts the state back in order.
+    bool failed = false;
     int checkpoint_position = 0;
     Mat embedding, lm_head;
     const uint16_t* final_norm = nullptr;
@@ -1588,17 +1592,35 @@ extern "C" int q3x_hip_engine_reset(q3x_hip_engine* e) {
         hipStreamSynchronize(e->stream) != hipSuccess)
         return Q3X_HIP_ERUNTIME;
     e->position = 0;
+    e->failed = false;
     return Q3X_HIP_OK;
 }
 
+namespace {
+
+// Work of a forward may already be queued when a later step fails (a prefill
+// chunk after the first, the decode graph, the wait for the stream): let the
+// queued work end, and refuse further forwards until the state is reset,
+// where the reference would abort.
+int forward_failed(q3x_hip_engine& e, int rc) {
+    (void)hipStreamSynchronize(e.stream);
+    (void)hipGetLastError();
+    e.failed = true;
+    return rc;
+}
+
+}  // namespace
+
 extern "C" int q3x_hip_engine_forward(q3x_hip_engine* e, const int* tokens, int count, int compute_logits) {
     if (!e || !tokens || count <= 0) return Q3X_HIP_EINVAL;
+    if (e->failed) return Q3X_HIP_ESTATE;
     if (count > e->capacity - e->position) return Q3X_HIP_EINVAL;
     for (int i = 0; i < count; ++i)
         if (tokens[i] < 0 || tokens[i] >= e->c.V) return Q3X_HIP_EINVAL;
     e->h_tokens[0] = 0;  // step: index of the next token in the list
     e->h_tokens[1] = e->position;
     for (int i = 0; i < count; ++i) e->h_tokens[2 + i] = tokens[i];
+    // Nothing has reached the device if the token copy cannot be queued.
     if (hipMemcpyAsync(e->d_step, e->h_tokens, sizeof(int) * (2 + count), hipMemcpyHostToDevice, e->stream) !=
         hipSuccess)
         return Q3X_HIP_ERUNTIME;
@@ -1606,14 +1628,14 @@ extern "C" int q3x_hip_engine_forward(q3x_hip_engine* e, const int* tokens, int 
         hipGraphExec_t& g = e->graph[compute_logits ? 1 : 0];
         if (!g) {
             const int rc = capture(*e, compute_logits != 0);
-            if (rc) return rc;
+            if (rc) return forward_failed(*e, rc);
         }
-        if (hipGraphLaunch(g, e->stream) != hipSuccess) return Q3X_HIP_ERUNTIME;
+        if (hipGraphLaunch(g, e->stream) != hipSuccess) return forward_failed(*e, Q3X_HIP_ERUNTIME);
     } else {
         for (int done = 0; done < count;) {
             const int n = std::min(e->chunk, count - done);
             const int rc = enqueue(*e, n, compute_logits && done + n == count);
-            if (rc) return rc;
+            if (rc) return forward_failed(*e, rc);
             done += n;
         }
     }
@@ -1623,9 +1645,9 @@ extern "C" int q3x_hip_engine_forward(q3x_hip_engine* e, const int* tokens, int 
         hipError_t q;
         while ((q = hipStreamQuery(e->stream)) == hipErrorNotReady) {
         }
-        if (q != hipSuccess) return Q3X_HIP_ERUNTIME;
+        if (q != hipSuccess) return forward_failed(*e, Q3X_HIP_ERUNTIME);
     } else if (hipStreamSynchronize(e->stream) != hipSuccess) {
-        return Q3X_HIP_ERUNTIME;
+        return forward_failed(*e, Q3X_HIP_ERUNTIME);
     }
     e->position += count;
     return Q3X_HIP_OK;
@@ -1668,6 +1690,7 @@ extern "C" int q3x_hip_engine_checkpoint_restore(q3x_hip_engine* e) {
         hipStreamSynchronize(e->stream) != hipSuccess)
         return Q3X_HIP_ERUNTIME;
     e->position = e->checkpoint_position;
+    e->failed = false;
     return Q3X_HIP_OK;
 }
 

@@ -157,6 +157,7 @@ extern "C" const char* q3x_hip_strerror(int code) {
     case Q3X_HIP_ENOTSUP: return "matrix type not handled by this backend";
     case Q3X_HIP_EMODEL: return "model.bin rejected";
     case Q3X_HIP_ESCRATCH: return "request needs more workspace than the library's static scratch";
+    case Q3X_HIP_ESTATE: return "engine failed in an earlier forward; reset or restore it";
     default: return "unknown error";
     }
 }

@@ -40,6 +40,8 @@ def test_strerror():
     assert "invalid" in q3x.strerror(q3x.EINVAL)
     assert q3x.strerror(q3x.ENOTSUP)
     assert q3x.strerror(12345) == "unknown error"
+    assert "reset" in q3x.strerror(q3x.ESTATE)
+    assert "scratch" in q3x.strerror(q3x.ESCRATCH)
 
 
 def test_quantized_bytes_match_the_oracle_rules():

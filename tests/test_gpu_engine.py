@@ -107,3 +107,7 @@ def test_checkpoint_reset_and_errors():
         with pytest.raises(q3x.Q3xHipError):
             e.forward([fields["V"]])
         assert e.position == 5
+        # a rejected call leaves the engine usable (it is not a failed forward)
+        e.forward(cont)
+        assert e.position == 8
+        assert np.array_equal(e.logits().view(np.uint32), after.view(np.uint32))

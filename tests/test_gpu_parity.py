@@ -14,7 +14,7 @@ import pytest
 
 import oracle
 import qwen3x_amd as q3x
-from tests.helpers import Q4_0, Q8_0, bits, dequant_numpy, random_blocks, row_bound
+from tests.helpers import Q4_0, Q8_0, bits, dequant_numpy, q4_blocks, random_blocks, row_bound
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -151,6 +151,89 @@ def test_mv_unaligned_pointers_take_the_generic_path(type_):
     y = torch.empty(rows, dtype=torch.float32, device="cuda:0")
     q3x.mv(q3x.Linear(wbuf[2:], rows, cols, type_), xbuf[1:], y)
     check_bound(host(y), want, wd, x, "unaligned mv")
+
+
+def _q4_sparse(rng, rows, cols, live):
+    """Q4_0 rows whose nibbles are all 8 (weight zero) except a fraction `live`
+    drawn uniformly from 0..15; returns the bytes and the nibbles [rows, cols]."""
+    nb = rows * cols // 32
+    scales = rng.normal(0.0, 0.02, nb).astype(np.float16).view(np.uint16)
+    n = np.full((nb, 32), 8, np.int64)
+    m = rng.random((nb, 32)) < live
+    n[m] = rng.integers(0, 16, int(m.sum()))
+    packed = (n[:, :16] | (n[:, 16:] << 4)).astype(np.uint8)
+    return q4_blocks(scales, packed), n.reshape(rows, cols)
+
+
+def q4_mix_error_bound(w, nib, rows, cols, x):
+    """First-order bound on |y - W x| for the Q4_0 matvec's subnormal-half form.
+
+    Per block b the kernel forms s(n) = sum n_i x_i 2^-24 as two chains of 16
+    FMAs (elements 0..15 and 16..31, the second scaled by 16) joined by one
+    FMA, subtracts s(8) formed the same way with every nibble 8, and scales
+    by 2^24 (exact).  Each of those roundings is relative to a partial sum of
+    |n_i x_i| or |8 x_i|, so the block's inner product carries at most
+    gamma(18) * sum_i (n_i + 8) |x_i|, times |d_b| after the scale multiply.
+    The row sum of B blocks (per-lane partial sums, then a butterfly over at
+    most 64 lanes) adds at most gamma(B + 8) * sum_b |d_b inner_b|.  The
+    reference's direct form (arch/cpu.cpp:91-106) has gamma(32) * sum_i
+    |n_i - 8| |x_i| per block instead: near zero on blocks that are mostly
+    nibble 8, where this form keeps the sum_i (n_i + 8) |x_i| term."""
+    u = 2.0 ** -24
+
+    def gamma(k):
+        return k * u / (1 - k * u)
+
+    nb = cols // 32
+    blk = w.reshape(rows * nb, 18)
+    d = np.abs(blk[:, 0:2].copy().view(np.float16).astype(np.float64)).reshape(rows, nb)
+    ax = np.abs(x.astype(np.float64)).reshape(nb, 32)
+    n = nib.astype(np.float64).reshape(rows, nb, 32)
+    inner_terms = ((n + 8.0) * ax[None]).sum(axis=2)              # [rows, nb]
+    inner_abs = np.abs(((n - 8.0) * x.astype(np.float64).reshape(nb, 32)[None]).sum(axis=2))
+    return (d * gamma(18) * inner_terms).sum(axis=1) + gamma(nb + 8) * (d * (inner_abs + gamma(18) * inner_terms)).sum(axis=1)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 2048), (64, 5120), (16, 17408)])
+@pytest.mark.parametrize("live", [0.0, 0.05, 0.5])
+@pytest.mark.parametrize("aligned", [True, False])
+def test_mv_q4_sparse_blocks_error_bound(rows, cols, live, aligned):
+    # Blocks that are mostly nibble 8 (zero weights) at the production widths:
+    # the staged kernel's subnormal-half form (aligned) and the generic
+    # kernel's signed-byte form (unaligned) against W x in double, within the
+    # analytic bound above and the north-star bound; rows of zero weights give
+    # exactly zero.
+    torch = _torch()
+    rng = np.random.default_rng(int(cols + 1000 * live + rows))
+    w, nib = _q4_sparse(rng, rows, cols, live)
+    nib[rows // 2] = 8                                  # one row of zero weights
+    w = w.reshape(rows, cols // 32, 18)
+    w[rows // 2, :, 2:] = 0x88
+    w = w.reshape(-1)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    wd = dequant_numpy(w, Q4_0, rows, cols)
+    exact = wd.astype(np.float64) @ x.astype(np.float64)
+    want = oracle.mv(w, Q4_0, rows, cols, x)
+    say(f"q4 sparse mv {rows}x{cols} live={live} aligned={aligned}")
+    if aligned:
+        wt, xt = dev(w), dev(x)
+    else:
+        wt = torch.zeros(w.size + 16, dtype=torch.uint8, device="cuda:0")
+        wt[2:2 + w.size] = dev(w)
+        wt = wt[2:]
+        xbuf = torch.zeros(cols + 1, dtype=torch.float32, device="cuda:0")
+        xbuf[1:] = dev(x)
+        xt = xbuf[1:]
+    y = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda:0")
+    q3x.mv(q3x.Linear(wt, rows, cols, Q4_0), xt, y)
+    got = host(y)
+    assert got[rows // 2] == 0.0 and want[rows // 2] == 0.0
+    err = np.abs(got.astype(np.float64) - exact)
+    bound = q4_mix_error_bound(w, nib, rows, cols, x)
+    assert np.all(err <= bound), f"worst {(err / bound).max()} of the bound"
+    check_bound(got, want, wd, x, f"q4 sparse {rows}x{cols}")
+    ref_err = np.abs(want.astype(np.float64) - exact)
+    say(f"  max |err| gpu {err.max():.3e}  reference form {ref_err.max():.3e}  bound {bound.max():.3e}")
 
 
 @pytest.mark.parametrize("type_,rows,cols", [(Q8_0, 70000, 2048), (Q4_0, 70000, 2048), (Q8_0, 20000, 768),
