@@ -338,12 +338,23 @@ __global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int n
 
     // Ring of D steps in flight: step s lives in pre[s % D].
     u32x4 pre[D][RS][J];
-    // Loads of row i of step (batch b, pass p) into pre[d][i]; `live` false
-    // gives zeros.
-    auto issue_row = [&](int d, int b, int p, int i, bool live) {
-        const int row = gw + (b * RS + i) * GW;
+    // Row starts of the batch being requested, found once per batch (the
+    // passes of a batch only add their offset); null for rows past the
+    // matrix -- every row of a batch past the wave's last -- and rows of an
+    // expert id out of range.
+    const uint8_t* qrow[RS];
+    auto find_rows = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < RS; ++i) {
+            const int row = gw + (b * RS + i) * GW;
+            qrow[i] = row < nrows ? rows.row(row) : nullptr;
+        }
+    };
+    // Loads of row i of the requested batch's pass p into pre[d][i]; a null
+    // row gives zeros.
+    auto issue_row = [&](int d, int p, int i) {
         const int b0 = p * LPR;
-        const uint8_t* base = live && row < nrows ? rows.row(row) : nullptr;  // null: expert id out of range
+        const uint8_t* base = qrow[i];
         const uint8_t* src = base ? base + static_cast<size_t>(b0) * BB : rows.any();
         const int bytes = base ? min(LPR, bpr - b0) * BB : 0;
         const __amdgpu_buffer_rsrc_t rsrc =
@@ -353,11 +364,12 @@ __global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int n
             pre[d][i][j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * lane + 1024 * j, 0, kNonTemporal);
     };
     int qb = 0, qp = 0;  // batch and pass of the next step to request
+    find_rows(0);
 #pragma unroll
     for (int d = 0; d < D; ++d) {
 #pragma unroll
-        for (int i = 0; i < RS; ++i) issue_row(d, qb, qp, i, d < steps);
-        if (++qp == npass) { qp = 0; ++qb; }
+        for (int i = 0; i < RS; ++i) issue_row(d, qp, i);
+        if (++qp == npass) { qp = 0; find_rows(++qb); }
     }
 
     // x into LDS once per workgroup (overlaps the first weight loads), then
@@ -380,7 +392,6 @@ __global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int n
         for (int d = 0; d < D; ++d) {
             const int s = s0 + d;
             if (s >= steps) break;
-            const bool more = s + D < steps;
             const int b0 = cp * LPR;
             const int nblk = min(LPR, bpr - b0);
             const int col = li < nblk ? b0 + li : 0;
@@ -401,7 +412,7 @@ __global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int n
 #pragma unroll
                     for (int j = 0; j < J; ++j)
                         *reinterpret_cast<u32x4*>(wl + gg * S::SEGP + 1024 * j + 16 * lane) = pre[d][it * G + gg][j];
-                    issue_row(d, qb, qp, it * G + gg, more);  // step s + D into the slot just emptied
+                    issue_row(d, qp, it * G + gg);  // step s + D into the slot just emptied
                 }
                 wave_lds_sync();
                 if (li < nblk) {
@@ -410,7 +421,7 @@ __global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int n
                 }
                 wave_lds_sync();
             }
-            if (++qp == npass) { qp = 0; ++qb; }
+            if (++qp == npass) { qp = 0; find_rows(++qb); }
             if (cp == npass - 1) {
                 if constexpr (decltype(rows)::kSwiGLUPairs) {
                     // Iteration 0 is a gate row, iteration 1 its up row.
