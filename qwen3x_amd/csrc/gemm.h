@@ -33,7 +33,14 @@ namespace q3x {
 
 constexpr int kGemmPad = 4;            // floats of padding per LDS tile row
 constexpr int kXcds = 8;               // MI355X: 8 XCDs of 32 CUs
-constexpr int kGemmLd = 32 + kGemmPad; // LDS row pitch (floats)
+constexpr int kGemmLd = 32 + kGemmPad; // LDS row pitch (floats), 32x32x2 operand reads
+// LDS row pitch of the 16x16x4 operand reads.  Lane group g (lanes 16g ..
+// 16g + 15, rows 0..15) reads the 16-byte chunks g and g + 4 of its row:
+// with 40-float rows that is conflict-free (measured 112 TB/s of LDS reads
+// per GPU, as the 32x32 reads at pitch 36), where the 36-float pitch costs
+// 1.44x (70 TB/s).  The 8 pad floats of a weight row hold its block scale,
+// so two workgroups of 128 x 128 tiles still fit one CU's 160 KiB.
+constexpr int kGemmLd16 = 40;
 
 struct GemmTile {
     int m0;      // first A row of the tile (policy-defined numbering)
@@ -121,6 +128,18 @@ struct Mfma16 { static constexpr bool value = false; };
 template <class P>
 struct Mfma16<P, decltype(void(P::kMfma16))> { static constexpr bool value = P::kMfma16; };
 
+// Policy::kBlockFold (optional, default true): quantized blocks enter the
+// output as acc = fma(d, inner, acc), inner = the block's MFMA sum from zero
+// -- the reference's per-block factorisation, which keeps the rounding
+// error at the reference's level however long K is.  false: the weight tile
+// holds d * q (exact in FP32: an 11-bit scale times a 4- or 8-bit value) and
+// one MFMA chain runs over all of K -- about 8% faster on the grouped MoE
+// GEMMs, whose K (the hidden size, the expert width) is short.
+template <class P, class = void>
+struct BlockFold { static constexpr bool value = true; };
+template <class P>
+struct BlockFold<P, decltype(void(P::kBlockFold))> { static constexpr bool value = P::kBlockFold; };
+
 // Policy::linear_total() (optional, with kLinearGrid): the number of tiles
 // of a 1-D grid that is sized for the most tiles possible (a grouped GEMM's
 // tile count is known only on the device); workgroups past it return, and
@@ -156,11 +175,20 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
     constexpr int PER_PART = 32 / PARTS;
     static_assert(PARTS * B_ROWS_PER_PASS == NT, "thread split");
 
-    __shared__ __attribute__((aligned(16))) float As[2][BM * kGemmLd];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BN * kGemmLd];
-    // Block scales of the stage's weight rows (quantized types).
+    constexpr bool M16 = Mfma16<Policy>::value;
+    constexpr int LD = M16 ? kGemmLd16 : kGemmLd;
+    // Block scales of the stage's weight rows (quantized types): their own
+    // array, or (16x16 layout) float 32 of the weight row's padding.
     constexpr bool kScaled = QT != Q3X_HIP_MATRIX_BF16;
-    __shared__ float Ds[2][kScaled ? BN : 1];
+    constexpr bool kFold = kScaled && BlockFold<Policy>::value;
+    constexpr int A_FLOATS = BM * LD, B_FLOATS = BN * LD, D_FLOATS = kFold && !M16 ? BN : 0;
+    __shared__ __attribute__((aligned(16))) float lds_tiles[2 * (A_FLOATS + B_FLOATS + D_FLOATS)];
+    auto As = [&](int buf) { return lds_tiles + buf * A_FLOATS; };
+    auto Bs = [&](int buf) { return lds_tiles + 2 * A_FLOATS + buf * B_FLOATS; };
+    auto Ds = [&](int buf, int n) -> float& {
+        if constexpr (M16) return lds_tiles[2 * A_FLOATS + buf * B_FLOATS + n * LD + 32];
+        else return lds_tiles[2 * (A_FLOATS + B_FLOATS) + buf * BN + n];
+    };
 
     // Tile coordinates: a 2-D grid (x = weight-row tiles, y = A-row tiles), or
     // a 1-D grid over gx * gy tiles (Policy::kLinearGrid) remapped so that
@@ -221,7 +249,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
         for (int i = 0; i < A_PER_T; ++i) {
             const int idx = tid + i * NT;
             if (idx < A_VEC)
-                *reinterpret_cast<f32x4*>(&As[buf][(idx >> 3) * kGemmLd + 4 * Part::a_chunk(idx & 7)]) = a_reg[r][i];
+                *reinterpret_cast<f32x4*>(&As(buf)[(idx >> 3) * LD + 4 * Part::a_chunk(idx & 7)]) = a_reg[r][i];
         }
 #pragma unroll
         for (int p = 0; p < B_PASSES; ++p) {
@@ -229,18 +257,23 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
             if (n < BN) {
                 float vals[PER_PART];
                 Part::values(b_raw[r][p], vals);
-                if (kScaled && b_part == 0) Ds[buf][n] = Part::scale(b_raw[r][p]);
+                if constexpr (kFold) {
+                    if (b_part == 0) Ds(buf, n) = Part::scale(b_raw[r][p]);
+                } else if constexpr (kScaled) {
+                    const float d = Part::scale(b_raw[r][p]);
+#pragma unroll
+                    for (int e = 0; e < PER_PART; ++e) vals[e] *= d;  // exact
+                }
 #pragma unroll
                 for (int e = 0; e < PER_PART; e += 4) {
                     const int c = Part::column(b_part, e);
-                    *reinterpret_cast<f32x4*>(&Bs[buf][n * kGemmLd + c]) =
+                    *reinterpret_cast<f32x4*>(&Bs(buf)[n * LD + c]) =
                         f32x4{vals[e], vals[e + 1], vals[e + 2], vals[e + 3]};
                 }
             }
         }
     };
 
-    constexpr bool M16 = Mfma16<Policy>::value;
     f32x16 acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -318,22 +351,23 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
         if (kb + 1 < nblk) store_stage(buf ^ 1, r);
         if (kb + 1 + PF < nblk) load_stage(kb + 1 + PF, r);
         if (M16 && active) {
-            // Lane group g16 supplies k = 8 * g16 + s of MFMA step s (the same
-            // k order for both operands), i.e. 8 consecutive LDS columns.
+            // Lane group g16 supplies, at MFMA step s, k = 4 * g16 + s for s < 4
+            // and k = 16 + 4 * g16 + (s - 4) after (the same k order for both
+            // operands): the 16-byte chunks g16 and g16 + 4 of the row.
             f32x4 bf[TN][2][2];
 #pragma unroll
             for (int j = 0; j < TN; ++j)
 #pragma unroll
                 for (int nh = 0; nh < 2; ++nh) {
-                    const float* src = &Bs[buf][((wn * TN + j) * 32 + nh * 16 + l16) * kGemmLd + 8 * g16];
+                    const float* src = &Bs(buf)[((wn * TN + j) * 32 + nh * 16 + l16) * LD + 4 * g16];
                     bf[j][nh][0] = *reinterpret_cast<const f32x4*>(src);
-                    bf[j][nh][1] = *reinterpret_cast<const f32x4*>(src + 4);
+                    bf[j][nh][1] = *reinterpret_cast<const f32x4*>(src + 16);
                 }
-            if constexpr (kScaled) {
+            if constexpr (kFold) {
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
 #pragma unroll
-                    for (int nh = 0; nh < 2; ++nh) d16_new[j][nh] = Ds[buf][(wn * TN + j) * 32 + nh * 16 + l16];
+                    for (int nh = 0; nh < 2; ++nh) d16_new[j][nh] = Ds(buf, (wn * TN + j) * 32 + nh * 16 + l16);
                 // One active subtile: its pending block is folded before the
                 // chain reuses its accumulator.
                 if (kb > 0 && nsub == 1) fold16_pending();
@@ -341,9 +375,9 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
 #pragma unroll
             for (int q = 0; q < NSUB; ++q) {
                 if (q >= nsub) break;
-                const float* asrc = &As[buf][((wm * TM + q / 2) * 32 + (q & 1) * 16 + l16) * kGemmLd + 8 * g16];
+                const float* asrc = &As(buf)[((wm * TM + q / 2) * 32 + (q & 1) * 16 + l16) * LD + 4 * g16];
                 const f32x4 af0 = *reinterpret_cast<const f32x4*>(asrc);
-                const f32x4 af1 = *reinterpret_cast<const f32x4*>(asrc + 4);
+                const f32x4 af1 = *reinterpret_cast<const f32x4*>(asrc + 16);
 #pragma unroll
                 for (int s = 0; s < 8; ++s) {
                     const float a = s < 4 ? af0[s] : af1[s - 4];
@@ -352,19 +386,19 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
 #pragma unroll
                         for (int nh = 0; nh < 2; ++nh) {
                             const float b = bf[j][nh][s >> 2][s & 3];
-                            if constexpr (kScaled)
+                            if constexpr (kFold)
                                 blk16[q][j][nh] = __builtin_amdgcn_mfma_f32_16x16x4f32(
                                     a, b, s == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : blk16[q][j][nh], 0, 0, 0);
                             else
                                 acc16[q][j][nh] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc16[q][j][nh], 0, 0, 0);
                         }
                 }
-                if constexpr (kScaled) {
+                if constexpr (kFold) {
                     if (q == 0 && kb > 0 && nsub > 1) fold16_pending();
                     if (q > 0) fold16(q - 1, d16_new);
                 }
             }
-            if constexpr (kScaled) {
+            if constexpr (kFold) {
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -374,19 +408,19 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
             f32x4 af[TM][4], bf[TN][4];
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
-                const float* src = &As[buf][((wm * TM + i) * 32 + li) * kGemmLd + 16 * kh];
+                const float* src = &As(buf)[((wm * TM + i) * 32 + li) * LD + 16 * kh];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) af[i][q] = *reinterpret_cast<const f32x4*>(src + 4 * q);
             }
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                const float* src = &Bs[buf][((wn * TN + j) * 32 + li) * kGemmLd + 16 * kh];
+                const float* src = &Bs(buf)[((wn * TN + j) * 32 + li) * LD + 16 * kh];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) bf[j][q] = *reinterpret_cast<const f32x4*>(src + 4 * q);
             }
-            if constexpr (kScaled) {
+            if constexpr (kFold) {
 #pragma unroll
-                for (int j = 0; j < TN; ++j) d_new[j] = Ds[buf][(wn * TN + j) * 32 + li];
+                for (int j = 0; j < TN; ++j) d_new[j] = Ds(buf, (wn * TN + j) * 32 + li);
                 constexpr int S = P % SETS;
 #pragma unroll
                 for (int t = 0; t < NT32; ++t) {
@@ -432,7 +466,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(Policy pol, 
         if (kb + 1 < nblk) step(kb + 1, 0, std::integral_constant<int, 1>{});  // PF 2: stage kb + 2 is in set 0
     }
     // The last stage's pending tile.
-    if (kScaled && active) {
+    if (kFold && active) {
         if constexpr (M16) {
             fold16_pending();
         } else if constexpr (SETS == 2) {

@@ -276,6 +276,10 @@ struct GroupedGemm {
     static constexpr bool kPairedColumns = false;
     static constexpr bool kPartialTiles = true;  // every expert's last tile is short
     static constexpr bool kMfma16 = true;        // skip 16-row halves past the valid pairs
+    // One MFMA chain over K with the exact d * q in the weight tile: K is the
+    // hidden size (gate_up) or the expert width (down), and the per-block
+    // fold measured 8% slower here (92.6 -> 85.2 TFLOP/s at config 4).
+    static constexpr bool kBlockFold = false;
     int tiles_x;  // weight-row tiles
     const float* A;
     int a_cols;
