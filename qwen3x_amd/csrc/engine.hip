@@ -986,14 +986,17 @@ struct SwiGLUInput {
 // eps), x = o * (g * gate), gate = norm[j] * silu(z) formed by
 // delta_step_kernel.  Every workgroup forms it on the way into LDS: each
 // thread loads its chunks of o and gate in one round trip (the first kHeld
-// stay in registers) and copies o to LDS; then 16-lane groups take the heads
-// (group G: heads G, G + groups, ...), lane i summing the squares of columns
-// i, i + 16, ... in order with FMAs and the group adding its lanes with DPP,
-// so every workgroup holds the same scales; then each thread scales its
-// chunks.  Requires VD % 4 == 0 and at most 256 heads (the scales use the
-// 1 KB work area).
+// stay in registers).  With 128-value heads and every chunk held, a head's
+// sum of squares is the 32-lane DPP sum of its 32 chunks' threads (each
+// adding its own four squares with FMAs in order), and each thread scales and
+// stores its chunks at once.  Otherwise o is copied to LDS, 16-lane groups
+// take the heads (group G: heads G, G + groups, ...), lane i summing the
+// squares of columns i, i + 16, ... in order with FMAs and the group adding
+// its lanes with DPP, then each thread scales its chunks.  Either way every
+// workgroup holds the same scales.  Requires VD % 4 == 0 and at most 256
+// heads (the scales use the 1 KB work area).
 struct GatedNormInput {
-    static constexpr int kHeld = 4;
+    static constexpr int kHeld = 6;
     const float* gate;  // [VH * VD]: norm[j] * silu(z)
     int VD;
     __device__ void stage(const float* o, uint8_t* xl, int bpr, float* work) const {
@@ -1011,6 +1014,36 @@ struct GatedNormInput {
                 orr[k] = os[ck];
                 grr[k] = gs[ck];
             }
+        }
+        if (VD == 128 && chunks <= kHeld * B) {
+            // Every chunk is held, and the 32 chunks of a 128-value head are
+            // the k-th chunks of 32 consecutive threads (B is a multiple of
+            // 64): each head's sum of squares is a 32-lane DPP sum of the
+            // threads' own four squares, with no LDS round trip.
+#pragma unroll
+            for (int k = 0; k < kHeld; ++k) {
+                const int ck = threadIdx.x + k * B;
+                const bool mine = ck < chunks;
+                float sq = 0.0f;
+                if (mine) {
+                    sq = fmaf(orr[k].x, orr[k].x, sq);
+                    sq = fmaf(orr[k].y, orr[k].y, sq);
+                    sq = fmaf(orr[k].z, orr[k].z, sq);
+                    sq = fmaf(orr[k].w, orr[k].w, sq);
+                }
+                const float total = group_sum<32>(sq);
+                if (mine) {
+                    const float g = 1.0f / sqrtf(total / static_cast<float>(VD) + kEps);
+                    f32x4 v = orr[k];
+                    v.x = v.x * (g * grr[k].x);
+                    v.y = v.y * (g * grr[k].y);
+                    v.z = v.z * (g * grr[k].z);
+                    v.w = v.w * (g * grr[k].w);
+                    *at(ck) = v;
+                }
+            }
+            __syncthreads();
+            return;
         }
 #pragma unroll
         for (int k = 0; k < kHeld; ++k) {
