@@ -130,26 +130,11 @@ def lm_head_launch_ms(torch, step, lm_set, reps):
     return e0.elapsed_time(e1) / reps
 
 
-def events_ms(torch, fn, reps, warmup=3):
-    """Mean ms per call of fn(i) over `reps` back-to-back calls between two
-    HIP events on the current stream."""
-    for i in range(warmup):
-        fn(i)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(reps):
-        fn(i)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / reps
-
-
 def launch_breakdown(torch, q3x, step, layer_sets):
-    """Each launch of the layer on its own (back-to-back launches of one kind,
-    rotating the weight copies): microseconds and algorithmic GB/s."""
+    """Each launch of the layer on its own: 4n launches of one kind (rotating
+    the n weight copies) captured in one graph and replayed, so the host's
+    per-call cost (ctypes and Python, ~8 us, more than a small launch's GPU
+    time) does not set the rate: microseconds and algorithmic GB/s."""
     n = len(layer_sets)
     o = step.out
 
@@ -168,9 +153,9 @@ def launch_breakdown(torch, q3x, step, layer_sets):
     }
     out = {}
     for name, (fn, nbytes) in kinds.items():
-        # Median of five windows of 4n calls: one slow window (a clock or
-        # power transition) does not stand for the launch.
-        ms = statistics.median(events_ms(torch, fn, 4 * n) for _ in range(5))
+        # Median of five timings (each 5 replays): one slow window (a clock
+        # or power transition) does not stand for the launch.
+        ms = statistics.median(time_graph(torch, fn, 4 * n, 5) for _ in range(5))
         out[name] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
     step.reset()
     return out
@@ -210,11 +195,11 @@ def headline(torch, q3x, wl, steps, warmup):
     step_bytes = step.step_bytes()
     per_launch = launch_breakdown(torch, q3x, step, layer_sets)
     per_launch["lm_head"] = {"us": round(lm_ms * 1e3, 2), "GBps": round(lm_alg / (lm_ms * 1e-3) / 1e9, 1)}
-    # The layer's four launches without lm_head (back to back, rotating the
-    # copies): the rate of the smaller matvecs, which the 662 MB lm_head
-    # otherwise carries in the step's figure.
+    # The layer's four launches without lm_head (rotating the copies, in one
+    # graph as above): the rate of the smaller matvecs, which the 662 MB
+    # lm_head otherwise carries in the step's figure.
     set_bytes = step_bytes - lm_alg
-    set_ms = statistics.median(events_ms(torch, lambda i: step.run_layer(layer_sets[i % n_layer]), 4 * n_layer)
+    set_ms = statistics.median(time_graph(torch, lambda i: step.run_layer(layer_sets[i % n_layer]), 4 * n_layer, 5)
                                for _ in range(5))
     step.reset()
     layer_set = {"us": round(set_ms * 1e3, 2), "bytes": set_bytes,
