@@ -38,8 +38,9 @@ constexpr int kGemmLd = 32 + kGemmPad; // LDS row pitch (floats), 32x32x2 operan
 // 16g + 15, rows 0..15) reads the 16-byte chunks g and g + 4 of its row:
 // with 40-float rows that is conflict-free (measured 112 TB/s of LDS reads
 // per GPU, as the 32x32 reads at pitch 36), where the 36-float pitch costs
-// 1.44x (70 TB/s).  The 8 pad floats of a weight row hold its block scale,
-// so two workgroups of 128 x 128 tiles still fit one CU's 160 KiB.
+// 1.44x (70 TB/s).  Two workgroups of 128 x 128 tiles fit one CU's 160 KiB;
+// a kernel that also folds per block keeps the block scale of a weight row
+// in the row's 8 pad floats rather than in an array of its own.
 constexpr int kGemmLd16 = 40;
 
 struct GemmTile {
