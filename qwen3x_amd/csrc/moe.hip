@@ -549,7 +549,7 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
         }
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
-            if (it >= groups) break;
+            if (it >= groups) continue;  // uniform: the trip count stays IT, so the loop unrolls
             // x of this lane's slot, block col.
             const int my_slot = it * G + g;
             const uint8_t* xs = lds_dyn + (my_slot < slots ? my_slot : 0) * xs_bytes;
@@ -578,7 +578,7 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
             float out = 0.0f;
 #pragma unroll
             for (int it = 0; it < IT; ++it) {
-                if (it >= groups) break;
+                if (it >= groups) continue;
                 const float total = group_sum<LPR>(acc[it]);
 #pragma unroll
                 for (int gg = 0; gg < G; ++gg) {
