@@ -24,6 +24,10 @@ CONFIGS = {
     "moe_q8_tied": dict(BASE, id=4, matrix_type=Q8_0, I=128, experts=8, top_k=3, shared_I=64, tied_embeddings=1),
     # eight query heads per KV head (the 35B-A3B's grouping) and four value heads per key head
     "gqa8_q8": dict(BASE, id=5, matrix_type=Q8_0, AH=8, KVH=1, KH=1, VH=4),
+    # narrow recurrent heads (KD = 64, VD = 96, three value heads per key head):
+    # zero-padded key and value slots in the scans, the gated norm over heads
+    # that are not 128 wide, an output projection 288 columns wide
+    "narrow_q4": dict(BASE, id=6, matrix_type=Q4_0, KD=64, VD=96, KH=1, VH=3),
 }
 
 

@@ -48,7 +48,7 @@ def test_engine_logits_match_the_reference_forward(name):
 
 @pytest.mark.parametrize("name,prompt,chunk", [("dense_q8", 40, 0), ("dense_q4", 530, 256), ("moe_q4", 300, 0),
                                                ("moe_q8_tied", 64, 48), ("gqa8_q8", 100, 0), ("dense_q8", 333, 100),
-                                               ("gqa8_q8", 2100, 0)])
+                                               ("gqa8_q8", 2100, 0), ("narrow_q4", 300, 128)])
 def test_prefill_then_decode_match_the_reference_forward(name, prompt, chunk):
     # A forward of many tokens runs them as prefill chunks (GEMMs, the
     # recurrences token by token inside one launch, attention on the matrix
