@@ -15,6 +15,7 @@ constexpr int kQ8Bytes = 34;      // uint16 scale + int8[32]   (q8.h:10-15)
 constexpr int kQ4Bytes = 18;      // uint16 scale + uint8[16]  (q4.h:12-15)
 constexpr int kBF16Bytes = 64;    // 32 BF16 values (a block column of a BF16 matrix)
 constexpr int kWave = 64;         // CDNA wavefront
+constexpr int kCUs = 256;          // MI355X compute units
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));

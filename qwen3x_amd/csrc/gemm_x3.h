@@ -1,0 +1,348 @@
+// gemm_x3.h -- FP32 GEMM with exact products on the bf16 matrix cores.
+//
+// Y[m, n] = sum over blocks b of d[n, b] * (sum over the block's 32 k of
+// A[m, k] q[n, k]): the reference's per-block factorisation of a quantized
+// dot (arch/cpu.cpp:64-73, 91-106), for A in FP32 and q the block's integers
+// (Q8_0: int8, Q4_0: nibble - 8), or for BF16 weights a plain sum over K
+// (engine.cpp:181-185).
+//
+// Every weight value q is exact in bf16 (at most 8 significant bits), and an
+// FP32 activation splits exactly into three bf16 values, a = a1 + a2 + a3:
+// a1 is a truncated to its upper 16 bits, a2 the remainder truncated the
+// same way, a3 what is left (at most 8 significant bits; both subtractions
+// are exact by Sterbenz's lemma).  So
+//   sum_k a q = sum_k a3 q + sum_k a2 q + sum_k a1 q,
+// three v_mfma_f32_16x16x32_bf16 per 16x16 output block and weight block,
+// each product exact and every sum in FP32 -- where the FP32 matrix
+// instruction (v_mfma_f32_16x16x4_f32) needs eight instructions of twice the
+// cycles for the same block.  The split is exact for |a| >= 2^-110; below,
+// the lowest part loses bits under 2^-133 (bf16 has 8 significant bits in
+// FP32's subnormal range), an absolute error far below the FP32 rounding of
+// any sum it enters.
+//
+// Tile: WM x WN waves, each SM x SN output blocks of 16x16 (wave tile
+// 16 SM x 16 SN); BM = 16 SM WM A rows, BN = 16 SN WN weight rows.  A K
+// stage is one weight block (32 columns).  Per stage the workgroup stages,
+// in LDS, the three bf16 planes of its A rows (split once per tile) and its
+// weight rows as bf16, 64 bytes a row, the 16-byte chunks of row r at
+// position chunk ^ ((r >> 1) & 3), so the operand reads (lane l: row l % 16,
+// chunk l / 16) of each eight consecutive rows fall on distinct banks.  Per
+// stage kb: stage kb + 1 goes from registers to the other LDS buffer (the
+// previous barrier freed it), the loads of stage kb + 1 + PF are issued
+// into the registers just emptied, the matrix instructions of stage kb run,
+// then one barrier.  At the LDS write the only loads in flight are the ones
+// it consumes, so the wait is exact, and the new loads overlap a stage.
+//
+// A policy supplies the tiles and the operand rows: tile(ty, BM, tile)
+// (false: no such tile), a_row(tile, m) (an FP32 A row), b_row(tile, n) (a
+// weight row), store(tile, m, n, v) or, with kPairedColumns,
+// store_pair(tile, m, n, v, v16) for columns n and n + 16; kLinearGrid (a
+// 1-D grid of tiles_x weight-row tiles per A tile, remapped so that each
+// XCD takes a contiguous run: workgroups that share an A tile share an L2;
+// optionally linear_total()); kPartialTiles (A tiles often short).  With
+// kPartialTiles the wave's subtile rows are the tile's rows 16 (i WM + wm)
+// + [0, 16), so the valid rows of a short tile spread over the wave rows,
+// and a wave skips the subtile rows past the valid ones.
+#pragma once
+
+#include "gemm.h"
+
+namespace q3x {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// LDS byte offset of 16-byte chunk c (0..3) of row r in a 64-byte-row tile.
+__device__ __forceinline__ int x3_offset(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 1) & 3)); }
+
+// The upper halves of two words as one word of two bf16: lo from x, hi from y.
+__device__ __forceinline__ uint32_t bf16_pair(uint32_t x, uint32_t y) {
+    return __builtin_amdgcn_perm(y, x, 0x07060302u);
+}
+
+// a = a1 + a2 + a3 exactly (|a| >= 2^-110): each part's word has its low
+// half zero, i.e. is a bf16 value in the upper half.
+__device__ __forceinline__ void split3(float a, uint32_t& h1, uint32_t& h2, uint32_t& h3) {
+    h1 = __float_as_uint(a) & 0xffff0000u;
+    const float r = a - __uint_as_float(h1);
+    h2 = __float_as_uint(r) & 0xffff0000u;
+    h3 = __float_as_uint(r - __uint_as_float(h2));
+}
+
+template <uint32_t QT, int WM, int WN, int SM, int SN, class Policy, int PF = 1>
+__global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, int rows, int cols) {
+    static_assert(PF == 1 || PF == 2, "one or two stages in flight");
+    static_assert(!Policy::kPairedColumns || SN % 2 == 0, "paired columns need column blocks in pairs");
+    constexpr int NT = WM * WN * kWave;
+    constexpr int BM = WM * SM * 16;
+    constexpr int BN = WN * SN * 16;
+    constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : QT == Q3X_HIP_MATRIX_Q4_0 ? kQ4Bytes : kBF16Bytes;
+    constexpr bool kScaled = QT != Q3X_HIP_MATRIX_BF16;
+    // A: BM rows x 8 float4 per stage.
+    constexpr int A_VEC = BM * 8;
+    constexpr int A_PER_T = (A_VEC + NT - 1) / NT;
+    // Weights: BN rows, PARTS threads per row.
+    constexpr int PARTS = NT / BN >= 2 ? 2 : 1;
+    constexpr int B_ROWS_PER_PASS = NT / PARTS;
+    constexpr int B_PASSES = (BN + B_ROWS_PER_PASS - 1) / B_ROWS_PER_PASS;
+    constexpr int PER_PART = 32 / PARTS;
+    static_assert(PARTS * B_ROWS_PER_PASS == NT, "thread split");
+    using Part = BlockPart<QT, PARTS>;
+
+    // One LDS buffer: the A planes (a1, a2, a3), the weight rows, the scales.
+    constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64, D_BYTES = kScaled ? BN * 4 : 0;
+    constexpr int BUF = 3 * A_BYTES + B_BYTES + D_BYTES;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * BUF];
+    auto plane = [&](int buf, int p) { return lds + buf * BUF + p * A_BYTES; };
+    auto wtile = [&](int buf) { return lds + buf * BUF + 3 * A_BYTES; };
+    auto scales = [&](int buf) { return reinterpret_cast<float*>(lds + buf * BUF + 3 * A_BYTES + B_BYTES); };
+    // The weight values' chunk order (BlockPart's columns: for Q4_0 with two
+    // parts, elements 0-7 | 16-23 | 8-15 | 24-31); A's elements take the
+    // same chunks, so the products pair up unchanged.
+    auto a_chunk = [](int c) {
+        if constexpr (QT == Q3X_HIP_MATRIX_Q4_0 && PARTS == 2) return c == 1 ? 2 : c == 2 ? 1 : c;
+        else return c;
+    };
+
+    int bx = blockIdx.x, by = blockIdx.y;
+    if constexpr (Policy::kLinearGrid) {
+        const int total = LinearTotal<Policy>::get(pol, gridDim.x), L = blockIdx.x;
+        if (L >= total) return;
+        const int q = total / kXcds, r = total % kXcds, xcd = L % kXcds, k = L / kXcds;
+        const int t = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + k;
+        bx = t % pol.tiles_x;
+        by = t / pol.tiles_x;
+    }
+    GemmTile tile;
+    if (!pol.tile(by, BM, tile)) return;
+    const int n0 = bx * BN;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int wm = wave / WN, wn = wave % WN;
+    const int l16 = lane & 15, g16 = lane >> 4;
+
+    // Source pointers, fixed over K.  Every thread loads every stage with no
+    // branch (rows past the valid A rows or past the matrix read a valid row
+    // instead; their outputs are never stored).
+    const float* a_src[A_PER_T];
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+        const int idx = min(tid + i * NT, A_VEC - 1);
+        a_src[i] = pol.a_row(tile, min(idx >> 3, tile.mcount - 1)) + 4 * (idx & 7);
+    }
+    const uint8_t* b_src[B_PASSES];
+    const int b_part = tid % PARTS;
+#pragma unroll
+    for (int p = 0; p < B_PASSES; ++p) {
+        const int n = min(tid / PARTS + p * B_ROWS_PER_PASS, BN - 1);
+        b_src[p] = pol.b_row(tile, min(n0 + n, rows - 1));
+    }
+
+    f32x4 a_reg[PF][A_PER_T];
+    uint32_t b_raw[PF][B_PASSES][1 + Part::WORDS];
+    auto load_stage = [&](int kb, int r) {
+#pragma unroll
+        for (int i = 0; i < A_PER_T; ++i) a_reg[r][i] = *reinterpret_cast<const f32x4*>(a_src[i] + 32 * kb);
+#pragma unroll
+        for (int p = 0; p < B_PASSES; ++p) Part::load(b_src[p] + static_cast<size_t>(kb) * BB, b_part, b_raw[r][p]);
+    };
+    auto store_stage = [&](int buf, int r) {
+#pragma unroll
+        for (int i = 0; i < A_PER_T; ++i) {
+            const int idx = tid + i * NT;
+            if (A_VEC % NT == 0 || idx < A_VEC) {
+                const int row = idx >> 3, q4 = idx & 7;
+                const int off = x3_offset(row, a_chunk(q4 >> 1)) + 8 * (q4 & 1);
+                uint32_t h[3][4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) split3(a_reg[r][i][e], h[0][e], h[1][e], h[2][e]);
+#pragma unroll
+                for (int p = 0; p < 3; ++p)
+                    *reinterpret_cast<uint2*>(plane(buf, p) + off) =
+                        uint2{bf16_pair(h[p][0], h[p][1]), bf16_pair(h[p][2], h[p][3])};
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < B_PASSES; ++p) {
+            const int n = tid / PARTS + p * B_ROWS_PER_PASS;
+            if (BN % B_ROWS_PER_PASS == 0 || n < BN) {
+                uint32_t w[PER_PART / 2];
+                if constexpr (kScaled) {
+                    float vals[PER_PART];
+                    Part::values(b_raw[r][p], vals);
+#pragma unroll
+                    for (int e = 0; e < PER_PART / 2; ++e)
+                        w[e] = bf16_pair(__float_as_uint(vals[2 * e]), __float_as_uint(vals[2 * e + 1]));
+                    if (b_part == 0) scales(buf)[n] = Part::scale(b_raw[r][p]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < PER_PART / 2; ++e) w[e] = b_raw[r][p][1 + e];  // two bf16 a word already
+                }
+#pragma unroll
+                for (int c = 0; c < PER_PART / 8; ++c)
+                    *reinterpret_cast<u32x4*>(wtile(buf) + x3_offset(n, (b_part * PER_PART) / 8 + c)) =
+                        u32x4{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
+            }
+        }
+    };
+
+    // acc[i][j]: output block (subtile row i, column block j); lane l holds
+    // rows 4 (l / 16) + r, column l % 16.
+    f32x4 acc[SM][SN];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto sub_row = [&](int i) { return 16 * (i * WM + wm); };
+    const int s16 = (tile.mcount + 15) / 16;
+    const int nsub = Policy::kPartialTiles ? max(0, min(SM, (s16 - wm + WM - 1) / WM)) : SM;
+    const bool active = nsub > 0;
+    const int nblk = cols / kBlock;
+
+    auto step = [&](int kb, int r) {
+        const int buf = kb & 1;
+        if (kb + 1 < nblk) store_stage(buf ^ 1, r);
+        if (kb + 1 + PF < nblk) load_stage(kb + 1 + PF, r);
+        if (active) {
+            bf16x8 bf[SN];
+            float d[SN];
+#pragma unroll
+            for (int j = 0; j < SN; ++j) {
+                const int n = (wn * SN + j) * 16 + l16;
+                bf[j] = *reinterpret_cast<const bf16x8*>(wtile(buf) + x3_offset(n, g16));
+                if constexpr (kScaled) d[j] = scales(buf)[n];
+            }
+#pragma unroll
+            for (int i = 0; i < SM; ++i) {
+                if (i >= nsub) break;
+                const int m = sub_row(i) + l16;
+                const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(plane(buf, 0) + x3_offset(m, g16));
+                const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(plane(buf, 1) + x3_offset(m, g16));
+                const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(plane(buf, 2) + x3_offset(m, g16));
+#pragma unroll
+                for (int j = 0; j < SN; ++j) {
+                    if constexpr (kScaled) {
+                        // The block's sum from zero, smallest parts first,
+                        // then acc = fma(d, sum, acc).
+                        f32x4 s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, bf[j], f32x4{0.0f, 0.0f, 0.0f, 0.0f},
+                                                                          0, 0, 0);
+                        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bf[j], s, 0, 0, 0);
+                        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bf[j], s, 0, 0, 0);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(d[j], s[e], acc[i][j][e]);
+                    } else {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, bf[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bf[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bf[j], acc[i][j], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    };
+    // Prologue: stage 0 into LDS buffer 0, stages 1..PF into registers.
+    load_stage(0, 0);
+    store_stage(0, 0);
+#pragma unroll
+    for (int q = 1; q <= PF; ++q)
+        if (q < nblk) load_stage(q, q % PF);
+    __syncthreads();
+    // Stage s + 1 is in register set (s + 1) % PF when stage s runs.
+    for (int kb = 0; kb < nblk; kb += 2) {
+        step(kb, PF == 1 ? 0 : 1);
+        if (kb + 1 < nblk) step(kb + 1, 0);
+    }
+
+#pragma unroll
+    for (int i = 0; i < SM; ++i) {
+        if (i >= nsub) break;
+#pragma unroll
+        for (int j = 0; j < SN; ++j) {
+            const int n = n0 + (wn * SN + j) * 16 + l16;
+            if constexpr (Policy::kPairedColumns) {
+                // Column blocks 2s and 2s + 1 hold columns q and q + 16 of a
+                // 32-column group (e.g. gate and up of one output feature).
+                if (j % 2 == 1) continue;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = sub_row(i) + 4 * g16 + e;
+                    if (m < tile.mcount && n < rows) pol.store_pair(tile, m, n, acc[i][j][e], acc[i][j + 1][e]);
+                }
+            } else {
+                if (n >= rows) continue;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = sub_row(i) + 4 * g16 + e;
+                    if (m < tile.mcount) pol.store(tile, m, n, acc[i][j][e]);
+                }
+            }
+        }
+    }
+}
+
+// Tile shapes of the launches: 128 A rows x 256 weight rows on 8 waves of
+// 64x64 (one workgroup per CU: 198 registers), 128 x 128 on 8 waves of
+// 64x32 (two), 64 x 128 on 8 waves of 32x32 (three), 64 x 64 on 4 waves of
+// 32x32 (four).  A launch takes the shape of least estimated time: the
+// busiest CU takes ceil(tiles / CUs) tiles, resident up to the occupancy at
+// a time, and a CU holding k of them runs at the shape's measured rate for
+// k (TFLOP/s over the chip, MI355X, dense Q8_0/Q4_0).  Measured, e.g.: 4096
+// tokens x 12288 rows x 4096 columns 370 TFLOP/s on 128 x 256; 512 x 4096
+// x 12288 (64 tiles of 128 x 256) 208 on 64 x 128; 512 x 17408 x 5120 253
+// on 64 x 128 (272 tiles of 128 x 256 would leave 16 CUs a second one).
+enum class X3Shape { k128x256, k128x128, k64x128, k64x64 };
+
+inline double x3_estimate(long long tiles, int area, int occupancy, const double* rate) {
+    long long left = (tiles + kCUs - 1) / kCUs;
+    double t = 0.0;
+    while (left > 0) {
+        const int k = static_cast<int>(left < occupancy ? left : occupancy);
+        t += k * static_cast<double>(area) / rate[k - 1];
+        left -= k;
+    }
+    return t;
+}
+
+// rows = weight rows (outputs per A row), count = A rows.
+inline X3Shape x3_shape(int rows, int count) {
+    auto tiles = [&](int bm, int bn) {
+        return static_cast<long long>((rows + bn - 1) / bn) * ((count + bm - 1) / bm);
+    };
+    static constexpr double r256[] = {370.0};
+    static constexpr double r128[] = {200.0, 330.0};
+    static constexpr double r64x128[] = {210.0, 240.0, 260.0};
+    static constexpr double r64[] = {150.0, 190.0, 215.0, 230.0};
+    const double e[4] = {x3_estimate(tiles(128, 256), 128 * 256, 1, r256),
+                         x3_estimate(tiles(128, 128), 128 * 128, 2, r128),
+                         x3_estimate(tiles(64, 128), 64 * 128, 3, r64x128),
+                         x3_estimate(tiles(64, 64), 64 * 64, 4, r64)};
+    int best = 0;
+    for (int i = 1; i < 4; ++i)
+        if (e[i] < e[best]) best = i;
+    return static_cast<X3Shape>(best);
+}
+
+// One launch of gemm_x3_kernel over count A rows (pol.count) and `rows`
+// weight rows, on a 1-D grid (Policy::kLinearGrid) of all tiles.
+template <uint32_t QT, int WM, int WN, int SM, int SN, class P>
+int launch_x3_tiles(P pol, int rows, int count, int cols, hipStream_t stream) {
+    constexpr int BM = WM * SM * 16, BN = WN * SN * 16;
+    pol.tiles_x = (rows + BN - 1) / BN;
+    const long long tiles = static_cast<long long>(pol.tiles_x) * ((count + BM - 1) / BM);
+    if (tiles > 0x7fffffffLL) return Q3X_HIP_EINVAL;
+    hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, P>), dim3(static_cast<unsigned>(tiles)),
+                       dim3(WM * WN * kWave), 0, stream, pol, rows, cols);
+    return launch_status();
+}
+
+template <uint32_t QT, class P>
+int launch_x3(const P& pol, int rows, int count, int cols, hipStream_t stream) {
+    switch (x3_shape(rows, count)) {
+        case X3Shape::k128x256: return launch_x3_tiles<QT, 2, 4, 4, 4>(pol, rows, count, cols, stream);
+        case X3Shape::k128x128: return launch_x3_tiles<QT, 2, 4, 4, 2>(pol, rows, count, cols, stream);
+        case X3Shape::k64x128: return launch_x3_tiles<QT, 2, 4, 2, 2>(pol, rows, count, cols, stream);
+        default: return launch_x3_tiles<QT, 2, 2, 2, 2>(pol, rows, count, cols, stream);
+    }
+}
+
+}  // namespace q3x

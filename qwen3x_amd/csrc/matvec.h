@@ -486,7 +486,6 @@ __global__ __launch_bounds__(kMvWaves * kWave) void mv_generic_kernel(Rows rows,
 
 // ---- launch helpers shared with the MoE decode path ----
 
-constexpr int kCUs = 256;
 constexpr size_t kLdsPerCU = 160 * 1024;
 
 // Streaming launch: persistent grid sized to what is resident at once on 256

@@ -22,6 +22,7 @@
 #include "moe.h"
 
 #include "gemm.h"
+#include "gemm_x3.h"
 #include "libm_expf.h"
 #include "matvec.h"
 
@@ -31,17 +32,9 @@ constexpr int kRouterMaxExperts = 1024;
 constexpr int kRouterMaxTopK = 8;          // q3x_model::MAX_TOP_K (model_config.h:14)
 constexpr int kGroupThreads = 1024;
 constexpr int kChunk = 1024;               // pairs per grouping chunk
-// Grouped GEMM: 2 x 4 waves of one 32x32 tile -> 64 pairs x 128 weight rows,
-// or of two 32x32 tiles each -> 128 pairs (moe_grouped picks).  64 pairs was
-// measured ahead of 32-pair tiles, which waste fewer rows of an expert's last
-// tile but stream the weights twice as often per pair.  kGrpBM, the smaller
-// tile, bounds the tile count.
-constexpr int kGrpWM = 2, kGrpWN = 4, kGrpTM = 1, kGrpTN = 1;
-constexpr int kGrpBM = kGrpWM * kGrpTM * 32;
-// Register sets for the stages ahead in the 64 x 128 tile GEMMs (measured).
-template <uint32_t QT>
-constexpr int kTilePF = QT == Q3X_HIP_MATRIX_Q8_0 ? 2 : 1;
-constexpr int kGrpBN = kGrpWN * kGrpTN * 32;
+// Grouped GEMM tiles (gemm_x3_kernel): at least kGrpBM pairs, which bounds
+// the tile count the workspace holds.
+constexpr int kGrpBM = 64;
 
 // ---------------------------------------------------------------- router ----
 
@@ -663,11 +656,13 @@ int moe_decode(const uint8_t* gate_up, const uint8_t* down, int experts, int H, 
     return Q3X_HIP_ENOTSUP;
 }
 
-template <uint32_t QT, int WM, int TM>
+template <uint32_t QT, int WM, int WN, int SM, int SN>
 int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
                 int tokens, const int* ids, const float* weights, int top_k, float* Y, int accumulate,
                 uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
     constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
+    constexpr int BM = WM * SM * 16, BN = WN * SN * 16, NT = WM * WN * kWave;
+    static_assert(BM >= kGrpBM, "the workspace bounds the tile count for kGrpBM-pair tiles");
     const int P = tokens * top_k;
     int* ntiles = reinterpret_cast<int*>(ws + L.ntiles);
     int* nvalid = reinterpret_cast<int*>(ws + L.nvalid);
@@ -686,7 +681,7 @@ int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, 
     int status = launch_status();
     if (status != Q3X_HIP_OK) return status;
     hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(kGroupThreads), 0, stream,
-                       static_cast<const int*>(chunk_counts), L.chunks, experts, WM * TM * 32, chunk_base, tile_expert,
+                       static_cast<const int*>(chunk_counts), L.chunks, experts, BM, chunk_base, tile_expert,
                        tile_start, tile_count, ntiles, nvalid);
     if ((status = launch_status()) != Q3X_HIP_OK) return status;
     hipLaunchKernelGGL(moe_scatter_kernel, dim3(L.chunks), dim3(kChunk), 0, stream, ids, P, top_k, experts,
@@ -699,20 +694,20 @@ int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, 
     if (I % 64 == 0) {
         // SwiGLU in the gate_up epilogue: h directly.
         GroupedGateUp g1{};
-        const int nx = 2 * I / kGrpBN;
+        const int nx = (2 * I + BN - 1) / BN;
         static_cast<GroupedGemm&>(g1) = GroupedGemm{nx, X, H, src_token, gate_up, gu_row * 2 * I, gu_row,
                                                     tile_expert, tile_start, tile_count, ntiles, nullptr, 0};
         g1.I = I;
         g1.h = h;
-        hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, kGrpWN, TM, kGrpTN, GroupedGateUp, kTilePF<QT>>),
-                           dim3(nx * tiles_bound), dim3(WM * kGrpWN * kWave), 0, stream, g1, 2 * I, H);
+        hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, GroupedGateUp>), dim3(nx * tiles_bound), dim3(NT), 0,
+                           stream, g1, 2 * I, H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
     } else {
-        const int nx = (2 * I + kGrpBN - 1) / kGrpBN;
+        const int nx = (2 * I + BN - 1) / BN;
         GroupedGemm g1{nx, X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
                        ntiles, gu, 2 * I};
-        hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, kGrpWN, TM, kGrpTN, GroupedGemm, kTilePF<QT>>),
-                           dim3(nx * tiles_bound), dim3(WM * kGrpWN * kWave), 0, stream, g1, 2 * I, H);
+        hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, GroupedGemm>), dim3(nx * tiles_bound), dim3(NT), 0,
+                           stream, g1, 2 * I, H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
         const size_t sw = static_cast<size_t>(P) * I;
         const int sw_blocks = static_cast<int>(std::min<size_t>((sw + 255) / 256, 65536));
@@ -720,11 +715,11 @@ int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, 
                            static_cast<const int*>(nvalid));
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
     }
-    const int nx2 = (H + kGrpBN - 1) / kGrpBN;
+    const int nx2 = (H + BN - 1) / BN;
     GroupedGemm g2{nx2, h, I, nullptr, down, down_row * H, down_row, tile_expert, tile_start, tile_count,
                    ntiles, d, H};
-    hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, kGrpWN, TM, kGrpTN, GroupedGemm, kTilePF<QT>>),
-                       dim3(nx2 * tiles_bound), dim3(WM * kGrpWN * kWave), 0, stream, g2, H, I);
+    hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, GroupedGemm>), dim3(nx2 * tiles_bound), dim3(NT), 0,
+                       stream, g2, H, I);
     if ((status = launch_status()) != Q3X_HIP_OK) return status;
     const size_t outs = static_cast<size_t>(tokens) * H;
     if (H % 4 == 0 && aligned(Y, 16)) {
@@ -741,17 +736,13 @@ template <uint32_t QT>
 int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
                 int tokens, const int* ids, const float* weights, int top_k, float* Y, int accumulate,
                 uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
-    // 128-pair tiles (two 32-pair tiles per wave) once an expert averages 32
-    // or more pairs: a routed expert's group is rarely a whole number of
-    // tiles, and every tile streams the expert's weights and pays its stages'
-    // loads and barriers whatever its valid pairs.  At 2048 tokens x top 8 of
-    // 256 experts (64 pairs per expert on average) 128-pair tiles measured
-    // 1.21 ms against 1.32 ms for 64-pair ones (96-pair: 1.24 ms).
-    if (static_cast<long long>(tokens) * top_k >= 32LL * experts)
-        return moe_grouped_tiles<QT, 2, 2>(gate_up, down, experts, H, I, X, tokens, ids, weights, top_k, Y,
-                                           accumulate, ws, L, stream);
-    return moe_grouped_tiles<QT, 2, 1>(gate_up, down, experts, H, I, X, tokens, ids, weights, top_k, Y,
-                                       accumulate, ws, L, stream);
+    // 64 pairs x 128 weight rows on 8 waves of 32x32.  At 2048 tokens x top
+    // 8 of 256 experts (64 pairs per expert on average) 64 x 128, 128 x 128
+    // and 128 x 256 tiles measured within 2% (0.587-0.597 ms for the routed
+    // GEMMs and combine), 64 x 64 0.72 ms; the smallest of the three wastes
+    // the least on an expert's short last tile.
+    return moe_grouped_tiles<QT, 2, 4, 2, 2>(gate_up, down, experts, H, I, X, tokens, ids, weights, top_k, Y,
+                                             accumulate, ws, L, stream);
 }
 
 // ------------------------------------------------------------ MoE layer ----
@@ -909,15 +900,9 @@ struct SharedDownAdd : TokenTiles {
     }
 };
 
-template <uint32_t QT, int WM, int WN, int TM, int TN, class P>
-int launch_token_gemm(P pol, int rows, hipStream_t stream) {
-    constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
-    pol.tiles_x = (rows + BN - 1) / BN;
-    const long long tiles = static_cast<long long>(pol.tiles_x) * ((pol.count + BM - 1) / BM);
-    if (tiles > 0x7fffffffLL) return Q3X_HIP_EINVAL;
-    hipLaunchKernelGGL((gemm_mfma_kernel<QT, WM, WN, TM, TN, P, kTilePF<QT>>), dim3(static_cast<unsigned>(tiles)),
-                       dim3(WM * WN * kWave), 0, stream, pol, rows, pol.cols);
-    return launch_status();
+template <uint32_t QT, class P>
+int launch_token_gemm(const P& pol, int rows, hipStream_t stream) {
+    return launch_x3<QT>(pol, rows, pol.count, pol.cols, stream);
 }
 
 inline int launch_router_topk(const float* logits, int tokens, int experts, int top_k, int* ids, float* weights,
@@ -988,7 +973,7 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
         g.X = X; g.cols = H; g.count = tokens;
         g.router = router; g.gate_row = gate_row; g.row_bytes = static_cast<size_t>(H) * 2; g.experts = E;
         g.logits = logits; g.gate_logit = gate;
-        status = launch_token_gemm<Q3X_HIP_MATRIX_BF16, 2, 4, 1, 1>(g, E + 1, stream);
+        status = launch_token_gemm<Q3X_HIP_MATRIX_BF16>(g, E + 1, stream);
     }
     if (status != Q3X_HIP_OK) return status;
     if ((status = launch_router_topk(logits, tokens, E, K, sel, wts, stream)) != Q3X_HIP_OK) return status;
@@ -1011,7 +996,7 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
         PairedGateUpGemm g{};
         g.X = X; g.cols = H; g.count = tokens;
         g.gate = sg; g.up = su; g.row_bytes = gu_row; g.I = SI; g.h = h_s;
-        status = launch_token_gemm<QT, 2, 4, 1, 1>(g, 2 * SI, stream);
+        status = launch_token_gemm<QT>(g, 2 * SI, stream);
         if (status != Q3X_HIP_OK) return status;
     } else {
         float* gu_s = reinterpret_cast<float*>(ws + L.gu_s);
@@ -1019,9 +1004,9 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
         g.X = X; g.cols = H; g.count = tokens;
         g.row_bytes = gu_row; g.out = gu_s; g.out_stride = 2 * SI;
         g.w = sg; g.col0 = 0;
-        if ((status = launch_token_gemm<QT, 2, 4, 1, 1>(g, SI, stream)) != Q3X_HIP_OK) return status;
+        if ((status = launch_token_gemm<QT>(g, SI, stream)) != Q3X_HIP_OK) return status;
         g.w = su; g.col0 = SI;
-        if ((status = launch_token_gemm<QT, 2, 4, 1, 1>(g, SI, stream)) != Q3X_HIP_OK) return status;
+        if ((status = launch_token_gemm<QT>(g, SI, stream)) != Q3X_HIP_OK) return status;
         const size_t n = static_cast<size_t>(tokens) * SI;
         hipLaunchKernelGGL(swiglu_kernel, dim3(static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 65536))),
                            dim3(256), 0, stream, gu_s, h_s, SI, tokens, nullptr);
@@ -1030,7 +1015,7 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
     SharedDownAdd g{};
     g.X = h_s; g.cols = SI; g.count = tokens;
     g.w = sd; g.row_bytes = sd_row; g.Y = Y; g.H = H; g.gate_logit = gate;
-    return launch_token_gemm<QT, 2, 4, 1, 1>(g, H, stream);
+    return launch_token_gemm<QT>(g, H, stream);
 }
 
 }  // namespace q3x
