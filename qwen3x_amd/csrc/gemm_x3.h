@@ -30,8 +30,14 @@
 // stage kb: stage kb + 1 goes from registers to the other LDS buffer (the
 // previous barrier freed it), the loads of stage kb + 1 + PF are issued
 // into the registers just emptied, the matrix instructions of stage kb run,
-// then one barrier.  At the LDS write the only loads in flight are the ones
-// it consumes, so the wait is exact, and the new loads overlap a stage.
+// then one barrier; at the LDS write the only loads in flight are the ones
+// it consumes, so the wait is exact.  Past the last block the store and the
+// loads repeat the last block (into a buffer no stage reads), so a step has
+// no branch.  CF ("compute first") issues stage kb's matrix instructions
+// before stage kb + 1's conversion instead, so the scheduler places the
+// split and the weight conversion in the matrix instructions' shadow: 3-13%
+// faster with 64x64 wave tiles, slower with smaller ones (the registers the
+// overlap holds cost them a wave of occupancy).
 //
 // A policy supplies the tiles and the operand rows: tile(ty, BM, tile)
 // (false: no such tile), a_row(tile, m) (an FP32 A row), b_row(tile, n) (a
@@ -68,7 +74,7 @@ __device__ __forceinline__ void split3(float a, uint32_t& h1, uint32_t& h2, uint
     h3 = __float_as_uint(r - __uint_as_float(h2));
 }
 
-template <uint32_t QT, int WM, int WN, int SM, int SN, class Policy, int PF = 1>
+template <uint32_t QT, int WM, int WN, int SM, int SN, class Policy, int PF = 1, bool CF = false>
 __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, int rows, int cols) {
     static_assert(PF == 1 || PF == 2, "one or two stages in flight");
     static_assert(!Policy::kPairedColumns || SN % 2 == 0, "paired columns need column blocks in pairs");
@@ -173,7 +179,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
 #pragma unroll
                     for (int e = 0; e < PER_PART / 2; ++e)
                         w[e] = bf16_pair(__float_as_uint(vals[2 * e]), __float_as_uint(vals[2 * e + 1]));
-                    if (b_part == 0) scales(buf)[n] = Part::scale(b_raw[r][p]);
+                    scales(buf)[n] = Part::scale(b_raw[r][p]);  // the row's parts write the same value
                 } else {
 #pragma unroll
                     for (int e = 0; e < PER_PART / 2; ++e) w[e] = b_raw[r][p][1 + e];  // two bf16 a word already
@@ -201,8 +207,10 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
 
     auto step = [&](int kb, int r) {
         const int buf = kb & 1;
-        if (kb + 1 < nblk) store_stage(buf ^ 1, r);
-        if (kb + 1 + PF < nblk) load_stage(kb + 1 + PF, r);
+        if constexpr (!CF) {
+            store_stage(buf ^ 1, r);
+            load_stage(min(kb + 1 + PF, nblk - 1), r);
+        }
         if (active) {
             bf16x8 bf[SN];
             float d[SN];
@@ -238,14 +246,17 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
                 }
             }
         }
+        if constexpr (CF) {
+            store_stage(buf ^ 1, r);
+            load_stage(min(kb + 1 + PF, nblk - 1), r);
+        }
         __syncthreads();
     };
     // Prologue: stage 0 into LDS buffer 0, stages 1..PF into registers.
     load_stage(0, 0);
     store_stage(0, 0);
 #pragma unroll
-    for (int q = 1; q <= PF; ++q)
-        if (q < nblk) load_stage(q, q % PF);
+    for (int q = 1; q <= PF; ++q) load_stage(min(q, nblk - 1), q % PF);
     __syncthreads();
     // Stage s + 1 is in register set (s + 1) % PF when stage s runs.
     for (int kb = 0; kb < nblk; kb += 2) {
@@ -324,24 +335,30 @@ inline X3Shape x3_shape(int rows, int count) {
 
 // One launch of gemm_x3_kernel over count A rows (pol.count) and `rows`
 // weight rows, on a 1-D grid (Policy::kLinearGrid) of all tiles.
-template <uint32_t QT, int WM, int WN, int SM, int SN, class P>
+template <uint32_t QT, int WM, int WN, int SM, int SN, int PF, bool CF, class P>
 int launch_x3_tiles(P pol, int rows, int count, int cols, hipStream_t stream) {
     constexpr int BM = WM * SM * 16, BN = WN * SN * 16;
     pol.tiles_x = (rows + BN - 1) / BN;
     const long long tiles = static_cast<long long>(pol.tiles_x) * ((count + BM - 1) / BM);
     if (tiles > 0x7fffffffLL) return Q3X_HIP_EINVAL;
-    hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, P>), dim3(static_cast<unsigned>(tiles)),
+    hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, P, PF, CF>), dim3(static_cast<unsigned>(tiles)),
                        dim3(WM * WN * kWave), 0, stream, pol, rows, cols);
     return launch_status();
 }
 
+// Two stages of loads ahead for the 64 x 128 tiles over long K (5-10% on
+// 512 tokens x 12288- and 17408-column matrices, a few % slower on short K).
+constexpr int kX3LongK = 8192;
+
 template <uint32_t QT, class P>
 int launch_x3(const P& pol, int rows, int count, int cols, hipStream_t stream) {
     switch (x3_shape(rows, count)) {
-        case X3Shape::k128x256: return launch_x3_tiles<QT, 2, 4, 4, 4>(pol, rows, count, cols, stream);
-        case X3Shape::k128x128: return launch_x3_tiles<QT, 2, 4, 4, 2>(pol, rows, count, cols, stream);
-        case X3Shape::k64x128: return launch_x3_tiles<QT, 2, 4, 2, 2>(pol, rows, count, cols, stream);
-        default: return launch_x3_tiles<QT, 2, 2, 2, 2>(pol, rows, count, cols, stream);
+        case X3Shape::k128x256: return launch_x3_tiles<QT, 2, 4, 4, 4, 1, true>(pol, rows, count, cols, stream);
+        case X3Shape::k128x128: return launch_x3_tiles<QT, 2, 4, 4, 2, 1, false>(pol, rows, count, cols, stream);
+        case X3Shape::k64x128:
+            if (cols >= kX3LongK) return launch_x3_tiles<QT, 2, 4, 2, 2, 2, false>(pol, rows, count, cols, stream);
+            return launch_x3_tiles<QT, 2, 4, 2, 2, 1, false>(pol, rows, count, cols, stream);
+        default: return launch_x3_tiles<QT, 2, 2, 2, 2, 1, false>(pol, rows, count, cols, stream);
     }
 }
 
