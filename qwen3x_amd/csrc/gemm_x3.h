@@ -292,16 +292,17 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
 }
 
 // Tile shapes of the launches: 128 A rows x 256 weight rows on 8 waves of
-// 64x64 (one workgroup per CU: 198 registers), 128 x 128 on 8 waves of
-// 64x32 (two), 64 x 128 on 8 waves of 32x32 (three), 64 x 64 on 4 waves of
-// 32x32 (four).  A launch takes the shape of least estimated time: the
+// 64x64 (one workgroup per CU: 209 registers), 64 x 128 on 8 waves of 32x32
+// (three), 64 x 64 on 4 waves of 32x32 (four).  (128 x 128 on 8 waves of
+// 64x32, two per CU, measured 200 / 330 TFLOP/s at one / two resident and
+// never beat these three on the config and engine shapes.)  A launch takes the shape of least estimated time: the
 // busiest CU takes ceil(tiles / CUs) tiles, resident up to the occupancy at
 // a time, and a CU holding k of them runs at the shape's measured rate for
 // k (TFLOP/s over the chip, MI355X, dense Q8_0/Q4_0).  Measured, e.g.: 4096
 // tokens x 12288 rows x 4096 columns 370 TFLOP/s on 128 x 256; 512 x 4096
 // x 12288 (64 tiles of 128 x 256) 208 on 64 x 128; 512 x 17408 x 5120 253
 // on 64 x 128 (272 tiles of 128 x 256 would leave 16 CUs a second one).
-enum class X3Shape { k128x256, k128x128, k64x128, k64x64 };
+enum class X3Shape { k128x256, k64x128, k64x64 };
 
 inline double x3_estimate(long long tiles, int area, int occupancy, const double* rate) {
     long long left = (tiles + kCUs - 1) / kCUs;
@@ -314,21 +315,24 @@ inline double x3_estimate(long long tiles, int area, int occupancy, const double
     return t;
 }
 
-// rows = weight rows (outputs per A row), count = A rows.
-inline X3Shape x3_shape(int rows, int count) {
+// Two stages of loads ahead for the 64 x 128 tiles over long K (5-10% on
+// 512 tokens x 12288- and 17408-column matrices, a few % slower on short K).
+constexpr int kX3LongK = 8192;
+
+// rows = weight rows (outputs per A row), count = A rows, cols = K.
+inline X3Shape x3_shape(int rows, int count, int cols) {
     auto tiles = [&](int bm, int bn) {
         return static_cast<long long>((rows + bn - 1) / bn) * ((count + bm - 1) / bm);
     };
     static constexpr double r256[] = {370.0};
-    static constexpr double r128[] = {200.0, 330.0};
     static constexpr double r64x128[] = {210.0, 240.0, 260.0};
+    static constexpr double r64x128_long[] = {215.0, 290.0, 300.0};  // two stages ahead, K >= kX3LongK
     static constexpr double r64[] = {150.0, 190.0, 215.0, 230.0};
-    const double e[4] = {x3_estimate(tiles(128, 256), 128 * 256, 1, r256),
-                         x3_estimate(tiles(128, 128), 128 * 128, 2, r128),
-                         x3_estimate(tiles(64, 128), 64 * 128, 3, r64x128),
+    const double e[3] = {x3_estimate(tiles(128, 256), 128 * 256, 1, r256),
+                         x3_estimate(tiles(64, 128), 64 * 128, 3, cols >= kX3LongK ? r64x128_long : r64x128),
                          x3_estimate(tiles(64, 64), 64 * 64, 4, r64)};
     int best = 0;
-    for (int i = 1; i < 4; ++i)
+    for (int i = 1; i < 3; ++i)
         if (e[i] < e[best]) best = i;
     return static_cast<X3Shape>(best);
 }
@@ -346,15 +350,10 @@ int launch_x3_tiles(P pol, int rows, int count, int cols, hipStream_t stream) {
     return launch_status();
 }
 
-// Two stages of loads ahead for the 64 x 128 tiles over long K (5-10% on
-// 512 tokens x 12288- and 17408-column matrices, a few % slower on short K).
-constexpr int kX3LongK = 8192;
-
 template <uint32_t QT, class P>
 int launch_x3(const P& pol, int rows, int count, int cols, hipStream_t stream) {
-    switch (x3_shape(rows, count)) {
+    switch (x3_shape(rows, count, cols)) {
         case X3Shape::k128x256: return launch_x3_tiles<QT, 2, 4, 4, 4, 1, true>(pol, rows, count, cols, stream);
-        case X3Shape::k128x128: return launch_x3_tiles<QT, 2, 4, 4, 2, 1, false>(pol, rows, count, cols, stream);
         case X3Shape::k64x128:
             if (cols >= kX3LongK) return launch_x3_tiles<QT, 2, 4, 2, 2, 2, false>(pol, rows, count, cols, stream);
             return launch_x3_tiles<QT, 2, 4, 2, 2, 1, false>(pol, rows, count, cols, stream);

@@ -14,7 +14,7 @@ import pytest
 
 import oracle
 import qwen3x_amd as q3x
-from tests.helpers import Q4_0, Q8_0, bits, dequant_numpy, q4_blocks, random_blocks, row_bound
+from tests.helpers import Q4_0, Q8_0, bits, dequant_numpy, q4_blocks, q8_blocks, random_blocks, row_bound
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -341,6 +341,67 @@ def test_gemm_parity(type_, rows, cols, count):
     check_bound(got, want, wd, X, f"gemm {rows}x{cols}x{count}")
     q3x.batch_mv(lin, dev(X), Y, count, add=True)
     check_bound(host(Y), 2 * want, wd, 2 * X, "gemm add")
+
+
+# One nonzero weight per row: every block sum is a single product q * x, so
+# the GEMM must return fl(d * fl(q * x)) up to the matrix cores' own
+# rounding (the reference's loop, arch/cpu.cpp:64-73 / 91-101, computes
+# exactly that: inner = q * x, then sum = d * inner from zero).  The prefill
+# kernel splits x into three bf16 parts and sums q * a3 + q * a2 + q * a1;
+# the products and the first partial sum are exact, and the matrix cores'
+# FP32 accumulation is not rounded like IEEE round-to-nearest (measured: one
+# ulp off in about 14% of single-product sums), so the bar is 2 ulp -- where a
+# dropped split part errs by 2^8 ulp or more, and a mispaired activation and
+# weight chunk or a misplaced tile by an unrelated value.  x spans 2^-90 ..
+# 2^90.  The shapes take each tile shape of the launch (128 x 256, 64 x 128
+# with one and two stages ahead, 64 x 64) and partial tiles.
+ONE_PRODUCT_CASES = [(Q8_0, 4096, 256, 2048), (Q4_0, 4096, 320, 2048), (Q8_0, 4096, 8192, 512),
+                     (Q4_0, 2048, 1024, 1024), (Q8_0, 257, 512, 300), (Q4_0, 100, 96, 7)]
+
+
+def _one_product_matrix(rng, type_, rows, cols):
+    nbr = cols // 32
+    scales = rng.normal(0.0, 0.05, rows * nbr).astype(np.float16)
+    scales[scales == 0] = np.float16(0.01)
+    col = rng.integers(0, cols, rows)
+    if type_ == Q8_0:
+        q = rng.integers(1, 128, rows) * rng.choice([-1, 1], rows)
+        values = np.zeros((rows, cols), np.int64)
+        values[np.arange(rows), col] = q
+        w = q8_blocks(scales.view(np.uint16), values.reshape(-1, 32))
+    else:
+        nib = rng.integers(0, 15, rows)
+        nib[nib >= 8] += 1  # 0..15 without 8
+        q = nib - 8
+        full = np.full((rows, cols), 8, np.uint8)
+        full[np.arange(rows), col] = nib
+        blocks = full.reshape(-1, 32)
+        w = q4_blocks(scales.view(np.uint16), blocks[:, :16] | (blocks[:, 16:] << 4))
+    d = scales.reshape(rows, nbr)[np.arange(rows), col // 32].astype(np.float32)
+    return w, col, q.astype(np.float32), d
+
+
+@pytest.mark.parametrize("type_,rows,cols,count", ONE_PRODUCT_CASES)
+def test_gemm_one_product_per_row(type_, rows, cols, count):
+    torch = _torch()
+    rng = np.random.default_rng(rows * 7 + cols + count + type_)
+    w, col, q, d = _one_product_matrix(rng, type_, rows, cols)
+    mant = rng.uniform(1.0, 2.0, (count, cols)) * rng.choice([-1.0, 1.0], (count, cols))
+    X = np.ldexp(mant, rng.integers(-90, 91, (count, cols))).astype(np.float32)
+    want = d[None, :] * (q[None, :] * X[:, col])  # float32: rounded after each product
+    toks = np.array([0, count // 2, count - 1])
+    assert np.array_equal(bits(oracle.gemm(w, type_, rows, cols, X[toks])), bits(want[toks]))
+    lin = q3x.Linear(dev(w), rows, cols, type_)
+    Y = torch.full((count, rows), float("nan"), dtype=torch.float32, device="cuda:0")
+    say(f"gemm one product per row: type={type_} {rows}x{cols} count={count}")
+    q3x.batch_mv(lin, dev(X), Y, count)
+    got = host(Y)
+    assert np.all(np.sign(got) == np.sign(want))
+    ulps = np.abs(bits(got).astype(np.int64) - bits(want).astype(np.int64))
+    say(f"  exact {np.mean(ulps == 0):.3f}, worst {ulps.max()} ulp")
+    assert ulps.max() <= 2, f"{np.count_nonzero(ulps > 2)} outputs beyond 2 ulp; first at {np.argwhere(ulps > 2)[0]}"
+    q3x.batch_mv(lin, dev(X), Y, count, add=True)  # the same sums again, added: exactly twice
+    assert np.array_equal(bits(host(Y)), bits(got + got))
 
 
 # ---------------------------------------------------------------- router ----
