@@ -433,8 +433,8 @@ def extra_configs(torch, q3x, wl, only=None, cpu=False):
                               device="cuda")
 
             def run_moe(i):
-                q3x.router_top_k(logits, T, moe.experts, k, ids, wts)
-                q3x.moe_routed(moe.gate_up_linear, moe.down_linear, X, T, ids, wts, k, Y, workspace=wsb)
+                q3x.moe_routed_logits(moe.gate_up_linear, moe.down_linear, X, T, logits, k, ids, wts, Y,
+                                      workspace=wsb)
             ms = time_graph(torch, run_moe, 20 if T == 1 else 1, 10 if T == 1 else 5)
             router_ms = time_graph(torch, lambda i: q3x.router_top_k(logits, T, moe.experts, k, ids, wts), 20, 5)
             if T == 1:
@@ -451,17 +451,24 @@ def extra_configs(torch, q3x, wl, only=None, cpu=False):
 
                 def run_moe_rot(i):
                     j = i % R
+                    q3x.moe_routed_logits(moe.gate_up_linear, moe.down_linear, X_r[j:j + 1], 1, logits_r[j:j + 1],
+                                          k, ids_r[j], wts_r[j], Y, workspace=wsb)
+
+                def run_two_calls(i):
+                    j = i % R
                     q3x.router_top_k(logits_r[j:j + 1], 1, moe.experts, k, ids_r[j], wts_r[j])
                     q3x.moe_routed(moe.gate_up_linear, moe.down_linear, X_r[j:j + 1], 1, ids_r[j], wts_r[j], k, Y,
                                    workspace=wsb)
                 ms_rot = time_graph(torch, run_moe_rot, R, 10)
+                ms_two = time_graph(torch, run_two_calls, R, 10)
                 distinct = int(torch.unique(ids_r).numel())
                 out["cfg4_q4_moe_decode"] = {
                     "GBps": alg / (ms_rot * 1e-3) / 1e9, "us": ms_rot * 1e3, "bytes": alg,
-                    "router_us": router_ms * 1e3, "us_same_token": ms * 1e3,
-                    "note": f"router + 8 experts per call, 64 distinct tokens in turn ({distinct} of 256 experts "
-                            "read per rotation); us_same_token repeats one token, whose 14 MB the Infinity "
-                            "Cache then serves"}
+                    "router_us": router_ms * 1e3, "us_same_token": ms * 1e3, "us_two_calls": ms_two * 1e3,
+                    "note": f"q3x_hip_moe_routed_logits (router inside the gate_up launch, then down: 2 launches) "
+                            f"per call, 64 distinct tokens in turn ({distinct} of 256 experts read per rotation); "
+                            "us_same_token repeats one token, whose 14 MB the Infinity Cache then serves; "
+                            "us_two_calls: q3x_hip_router_topk then q3x_hip_moe_routed (3 launches)"}
                 if ref_cpu:
                     import numpy as np
                     gu_h = np.ascontiguousarray(moe.gate_up.cpu().numpy())
@@ -523,8 +530,8 @@ def extra_configs(torch, q3x, wl, only=None, cpu=False):
                 alg = 2 * (E + 1) * H + k * per_expert + shared_bytes
                 out["cfg4_q4_moe_layer_decode"] = {
                     "GBps": alg / (ms * 1e-3) / 1e9, "us": ms * 1e3, "bytes": alg,
-                    "note": "router GEMV (BF16 256x2048) + shared-expert gate + top-8 + 8 routed experts + "
-                            "shared expert (Q4_0 512): 4 launches"}
+                    "note": "router GEMV (BF16 256x2048) + shared-expert gate, then top-8 inside the 8 routed + "
+                            "shared experts' gate/up launch, then their down launch: 3 launches"}
             else:
                 flops = 2.0 * T * ((E + 1) * H + k * 3 * I * H + 3 * SI * H)
                 out["cfg4_q4_moe_layer_prefill_T2048"] = {

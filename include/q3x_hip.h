@@ -134,6 +134,21 @@ int q3x_hip_moe_routed(const void* gate_up, const void* down, uint32_t type,
                        int accumulate, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
 
+/* Router and routed experts in one call: ids / weights ([tokens, top_k],
+ * device, written) = q3x_hip_router_topk(logits [tokens, experts]), then
+ * q3x_hip_moe_routed with them -- the reference's decode sequence
+ * router_top_k_kernel + expert kernels (engine.cu:1153-1250, 1711-1726).
+ * top_k <= 8.  One token takes two launches: the gate/up matvec routes the
+ * token itself (every workgroup runs the router on the logits, workgroup 0
+ * stores ids / weights) and stores h = silu(g) * u, then the down launch
+ * combines the slots; results equal the two calls' bit for bit.  Same
+ * workspace as q3x_hip_moe_routed. */
+int q3x_hip_moe_routed_logits(const void* gate_up, const void* down, uint32_t type,
+                              int experts, int H, int I, const float* X, int tokens,
+                              const float* logits, int top_k, int* ids, float* weights,
+                              float* Y, int accumulate, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+
 /* Size of the library's static per-device scratch that
  * q3x_hip_moe_routed_noalloc runs on: 32 MiB holds the workspace of 256
  * tokens at the 35B-A3B expert shape (H 2048, I 512, top 8), the reference's

@@ -59,6 +59,7 @@ SIGNATURES = {
     "q3x_hip_moe_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),
     "q3x_hip_moe_routed": (_I, [_P, _P, _U, _I, _I, _I, _P, _I, _P, _P, _I, _P, _I, _P, _S, _P]),
     "q3x_hip_moe_routed_noalloc": (_I, [_P, _P, _U, _I, _I, _I, _P, _I, _P, _P, _I, _P, _I, _P]),
+    "q3x_hip_moe_routed_logits": (_I, [_P, _P, _U, _I, _I, _I, _P, _I, _P, _I, _P, _P, _P, _I, _P, _S, _P]),
     "q3x_hip_quantize": (_I, [_U, _P, _I, _I, _P, _P]),
     "q3x_hip_moe_layer_workspace_bytes": (_S, [_P, _I]),
     "q3x_hip_moe_layer": (_I, [_P, _P, _I, _P, _P, _P, _P, _S, _P]),
@@ -305,6 +306,23 @@ def moe_routed(gate_up: ExpertLinear, down: ExpertLinear, X, tokens: int, ids, w
            lib().q3x_hip_moe_routed(_ptr(gate_up.weight), _ptr(down.weight), gate_up.type, gate_up.experts, H, I,
                                     _ptr(X), tokens, _ptr(ids), _ptr(weights), top_k, _ptr(Y), int(accumulate),
                                     _ptr(workspace), workspace.numel(), _stream(stream)))
+    return Y
+
+
+def moe_routed_logits(gate_up: ExpertLinear, down: ExpertLinear, X, tokens: int, logits, top_k: int, ids,
+                      weights, Y, accumulate: bool = False, workspace=None, stream=None):
+    """Router top-k on logits, then the routed experts (ids / weights are written)."""
+    torch = _torch()
+    _need_device(gate_up.weight, down.weight, X, logits, ids, weights, Y)
+    H, I = gate_up.columns, down.columns
+    need = moe_workspace_bytes(tokens, gate_up.experts, top_k, H, I)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=X.device)
+    _check("q3x_hip_moe_routed_logits",
+           lib().q3x_hip_moe_routed_logits(_ptr(gate_up.weight), _ptr(down.weight), gate_up.type, gate_up.experts,
+                                           H, I, _ptr(X), tokens, _ptr(logits), top_k, _ptr(ids), _ptr(weights),
+                                           _ptr(Y), int(accumulate), _ptr(workspace), workspace.numel(),
+                                           _stream(stream)))
     return Y
 
 

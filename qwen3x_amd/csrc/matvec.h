@@ -28,10 +28,38 @@
 // are deterministic.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 #include "rows.h"
 
 namespace q3x {
+
+// Row maps that choose their rows inside the launch (kRouteLds: the LDS
+// bytes their route() needs after the waves' slices): route() runs first,
+// with every thread of the workgroup, and returns what for_wave reads.
+template <class R, class = void>
+struct rows_route {
+    static constexpr bool value = false;
+    static constexpr uint32_t lds = 0;
+};
+template <class R>
+struct rows_route<R, std::void_t<decltype(R::kRouteLds)>> {
+    static constexpr bool value = true;
+    static constexpr uint32_t lds = R::kRouteLds;
+};
+
+// A wave's rows: for_wave, after route() for row maps that route.
+template <class Rows, bool = rows_route<Rows>::value>
+struct WaveRows {
+    __device__ static auto get(const Rows& r, int& gw, int& GW, int& nrows, uint8_t*) { return r.for_wave(gw, GW, nrows); }
+};
+template <class Rows>
+struct WaveRows<Rows, true> {
+    __device__ static auto get(const Rows& r, int& gw, int& GW, int& nrows, uint8_t* lds) {
+        return r.for_wave(gw, GW, nrows, r.route(lds));
+    }
+};
 
 constexpr int kMvWaves = 4;  // wavefronts per workgroup
 
@@ -326,7 +354,7 @@ __global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int n
     int gw = blockIdx.x * wpb + wave;
     int GW = gridDim.x * wpb;
     // The wave's matrix (multi-matrix launches); gw, GW, nrows become its own.
-    const auto rows = all_rows.for_wave(gw, GW, nrows);
+    const auto rows = WaveRows<Rows>::get(all_rows, gw, GW, nrows, lds_dyn + pipe_x_bytes(QT, bpr) + wpb * S::WAVE_LDS);
     const int g = lane / LPR;
     const int li = lane % LPR;
     uint8_t* const xl = lds_dyn;
@@ -564,10 +592,11 @@ inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_
     static const bool lds_ready =
         hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(kLdsPerCU)) == hipSuccess;
-    size_t lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb) * S::WAVE_LDS;
+    constexpr size_t tail = rows_route<Rows>::lds;
+    size_t lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb) * S::WAVE_LDS + tail;
     while (lds > kLdsPerCU && wpb > 4) {
         wpb -= 4;
-        lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb) * S::WAVE_LDS;
+        lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb) * S::WAVE_LDS + tail;
     }
     if (lds > kLdsPerCU) return Q3X_HIP_ENOTSUP;  // x too long for LDS
     if (lds > 64 * 1024 && !lds_ready) return Q3X_HIP_ERUNTIME;
@@ -579,7 +608,7 @@ inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_
         std::max<long long>((nrows + batches * rs - 1) / (batches * rs), rows.matrices());
     const int wpb_used = static_cast<int>(std::min<long long>(wpb, (waves + kCUs * per_cu - 1) / (kCUs * per_cu)));
     const int grid = static_cast<int>((waves + wpb_used - 1) / wpb_used);
-    lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb_used) * S::WAVE_LDS;
+    lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb_used) * S::WAVE_LDS + tail;
     Rows planned = rows;
     planned.plan_waves(grid * wpb_used);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWave * wpb_used), lds, stream, planned, nrows, bpr, in);

@@ -38,11 +38,11 @@ constexpr int kGrpBM = 64;
 
 // ---------------------------------------------------------------- router ----
 
-// One wavefront per token; lane l holds experts [PER*l, PER*l + PER), so lane
-// order is expert order.  The softmax is the reference's operation for
-// operation (engine.cpp:380-387): the maximum (exact in any order), p = exp(l -
-// max) with libm's expf arithmetic (libm_expf.h), the total added in expert
-// order from zero, and p / total correctly rounded.  The total's order is
+// One token's routing in one wavefront; lane l holds experts [PER*l, PER*l +
+// PER), so lane order is expert order.  The softmax is the reference's
+// operation for operation (engine.cpp:380-387): the maximum (exact in any
+// order), p = exp(l - max) with libm's expf arithmetic (libm_expf.h), the
+// total added in expert order from zero, and p / total correctly rounded.  The total's order is
 // sequential, so the wave writes p to LDS and every lane runs the same chain
 // of adds over it (broadcast reads).  Then top_k argmax passes, each over
 // keys (0 for an expert already chosen or past the end, else the
@@ -51,17 +51,12 @@ constexpr int kGrpBM = 64;
 // the wave's largest key is found with DPP and readlanes, and the lowest lane
 // holding it wins, i.e. the lowest expert index among equal probabilities, as
 // the reference's strict '>' scan picks.  Weights = p / (sum of the selected
-// p, added in slot order), correctly rounded (engine.cpp:388-404).
+// p, added in slot order), correctly rounded (engine.cpp:388-404).  Lane s <
+// top_k returns slot s's expert and weight.  mine_p: LDS for 64 * PER floats.
 template <int PER>
-__global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int tokens,
-                                                          int experts, int top_k, int* __restrict__ ids,
-                                                          float* __restrict__ weights) {
-    __shared__ __attribute__((aligned(16))) float probs[4][kRouterMaxExperts];
+__device__ __forceinline__ void router_topk_wave(const float* __restrict__ row, int experts, int top_k,
+                                                 float* __restrict__ mine_p, int& out_id, float& out_weight) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int token = blockIdx.x * 4 + wave;
-    if (token >= tokens) return;  // whole waves leave together; no block barrier below
-    const float* row = logits + static_cast<size_t>(token) * experts;
     const int first = PER * lane;
     float p[PER];
 #pragma unroll
@@ -70,7 +65,6 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
 #pragma unroll
     for (int j = 0; j < PER; ++j) local_max = local_max < p[j] ? p[j] : local_max;
     const float maximum = wave_max_f32(local_max);
-    float* mine_p = probs[wave];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         p[j] = first + j < experts ? libm_expf(p[j] - maximum) : 0.0f;
@@ -124,11 +118,66 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
 #pragma unroll
     for (int slot = 0; slot < kRouterMaxTopK; ++slot)
         if (slot == lane) { mine = chosen[slot]; mine_id = chosen_id[slot]; }
+    out_id = mine_id;
+    out_weight = __fdiv_rn(mine, selected_total);
+}
+
+// One wavefront per token (router_topk_wave); lane s < top_k writes slot s.
+template <int PER>
+__global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int tokens,
+                                                          int experts, int top_k, int* __restrict__ ids,
+                                                          float* __restrict__ weights) {
+    __shared__ __attribute__((aligned(16))) float probs[4][kRouterMaxExperts];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int token = blockIdx.x * 4 + wave;
+    if (token >= tokens) return;  // whole waves leave together; no block barrier below
+    int id;
+    float weight;
+    router_topk_wave<PER>(logits + static_cast<size_t>(token) * experts, experts, top_k, probs[wave], id, weight);
     if (lane < top_k) {
-        ids[static_cast<size_t>(token) * top_k + lane] = mine_id;
-        weights[static_cast<size_t>(token) * top_k + lane] = __fdiv_rn(mine, selected_total);
+        ids[static_cast<size_t>(token) * top_k + lane] = id;
+        weights[static_cast<size_t>(token) * top_k + lane] = weight;
     }
 }
+
+// The decode gate_up rows of ExpertGateUpRows, the experts chosen inside the
+// launch: route() runs the reference router (router_topk_wave) on the
+// token's logits in wave 0 of every workgroup -- a workgroup needs only the
+// selection, and computing it where it is used spares the router its own
+// launch -- and keeps ids and weights in LDS for for_wave; workgroup 0 also
+// stores them to ids_out / weights_out for the down-and-combine launch and
+// the caller.  Every workgroup computes the same selection bit for bit.
+struct RoutedGateUpRows : ExpertGateUpRows {
+    static constexpr uint32_t kRouteLds = 64 + 4 * kRouterMaxExperts;  // ids, weights, probabilities
+    const float* logits;
+    int top_k;
+    int* ids_out;
+    float* weights_out;
+    __device__ const int* route(uint8_t* lds) const {
+        int* chosen = reinterpret_cast<int*>(lds);
+        float* chosen_w = reinterpret_cast<float*>(lds + 32);
+        float* probs = reinterpret_cast<float*>(lds + 64);
+        if (threadIdx.x < kWave) {
+            const int lane = threadIdx.x;
+            int id;
+            float w;
+            if (experts <= 4 * kWave) router_topk_wave<4>(logits, experts, top_k, probs, id, w);
+            else if (experts <= 8 * kWave) router_topk_wave<8>(logits, experts, top_k, probs, id, w);
+            else router_topk_wave<16>(logits, experts, top_k, probs, id, w);
+            if (lane < top_k) {
+                chosen[lane] = id;
+                chosen_w[lane] = w;
+                if (blockIdx.x == 0) {
+                    ids_out[lane] = id;
+                    weights_out[lane] = w;
+                }
+            }
+        }
+        __syncthreads();
+        return chosen;
+    }
+};
 
 // ------------------------------------------------------------ workspace ----
 
@@ -613,11 +662,15 @@ int launch_moe_down(const uint8_t* down, int experts, int H, int I, const int* i
     return launch_status();
 }
 
+// Decode (one token).  With `logits`, the gate_up launch routes the token
+// itself (RoutedGateUpRows) and writes ids / weights, which the down launch
+// then reads: two launches for router and experts.
 template <uint32_t QT>
 int moe_decode(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
                const int* ids, const float* weights, int top_k, float* Y, int accumulate,
                uint8_t* ws, const MoeLayout& L, const SharedExpert& shared, hipStream_t stream,
-               const uint16_t* norm_w = nullptr) {
+               const uint16_t* norm_w = nullptr, const float* logits = nullptr, int* ids_out = nullptr,
+               float* weights_out = nullptr) {
     constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
     float* h = reinterpret_cast<float*>(ws + L.gu);  // [top_k (+1), I]
     const size_t gu_row = static_cast<size_t>(H / kBlock) * BB;
@@ -637,9 +690,24 @@ int moe_decode(const uint8_t* gate_up, const uint8_t* down, int experts, int H, 
         gate.shared_I = shared.I;
         // One 64-lane row group, two row iterations (gate, up) per step.
         // With norm_w, X is the raw residual, normalised in the staging.
-        int status = norm_w ? launch_pipe<QT, 64, 2, ExpertGateUpRows, 1, 4, NormInput>(
+        int status;
+        if (logits) {
+            RoutedGateUpRows routed{};
+            static_cast<ExpertGateUpRows&>(routed) = gate;
+            routed.logits = logits;
+            routed.top_k = top_k;
+            routed.ids_out = ids_out;
+            routed.weights_out = weights_out;
+            ids = ids_out;
+            weights = weights_out;
+            status = norm_w ? launch_pipe<QT, 64, 2, RoutedGateUpRows, 1, 4, NormInput>(
+                                  routed, slots * 2 * I, H / kBlock, 16, stream, 2, NormInput{norm_w})
+                            : launch_pipe<QT, 64, 2, RoutedGateUpRows>(routed, slots * 2 * I, H / kBlock, 16, stream, 2);
+        } else {
+            status = norm_w ? launch_pipe<QT, 64, 2, ExpertGateUpRows, 1, 4, NormInput>(
                                   gate, slots * 2 * I, H / kBlock, 16, stream, 2, NormInput{norm_w})
                             : launch_pipe<QT, 64, 2>(gate, slots * 2 * I, H / kBlock, 16, stream, 2);
+        }
         if (status == Q3X_HIP_OK) {
             const int bpr = I / kBlock;
             status = bpr <= 16   ? launch_moe_down<QT, 16>(down, experts, H, I, ids, weights, top_k, h, Y,
@@ -976,15 +1044,16 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
         status = launch_token_gemm<Q3X_HIP_MATRIX_BF16>(g, E + 1, stream);
     }
     if (status != Q3X_HIP_OK) return status;
-    if ((status = launch_router_topk(logits, tokens, E, K, sel, wts, stream)) != Q3X_HIP_OK) return status;
 
-    // Decode: routed and shared experts in two launches.
+    // Decode: routing, routed and shared experts in two launches (the gate_up
+    // launch routes the token from the logits).
     if (tokens == 1) {
         const SharedExpert shared{sg, su, sd, SI, gate};
         status = moe_decode<QT>(gate_up, down, E, H, I, X, sel, wts, K, Y, accumulate ? 1 : 0, rws, L.R, shared,
-                                stream, norm_w);
+                                stream, norm_w, logits, sel, wts);
         if (status != Q3X_HIP_ENOTSUP || accumulate) return status;
     }
+    if ((status = launch_router_topk(logits, tokens, E, K, sel, wts, stream)) != Q3X_HIP_OK) return status;
     // Prefill (or an unaligned decode): the grouped routed experts write Y,
     // then the shared expert's GEMMs add to it.
     status = moe_grouped<QT>(gate_up, down, E, H, I, X, tokens, sel, wts, K, Y, 0, rws, L.R, stream);
@@ -1077,6 +1146,39 @@ extern "C" int q3x_hip_moe_routed(const void* gate_up, const void* down, uint32_
                                                   accumulate, ws, L, stream);
 }
 
+extern "C" int q3x_hip_moe_routed_logits(const void* gate_up, const void* down, uint32_t type, int experts, int H,
+                                         int I, const float* X, int tokens, const float* logits, int top_k,
+                                         int* ids, float* weights, float* Y, int accumulate, void* workspace,
+                                         size_t workspace_bytes, hipStream_t stream) {
+    if (type == Q3X_HIP_MATRIX_BF16) return Q3X_HIP_ENOTSUP;
+    if (!gate_up || !down || !X || !logits || !ids || !weights || !Y || !workspace || !is_quant_type(type) ||
+        !moe_shape_ok(type, experts, H, I, tokens, top_k) || top_k > kRouterMaxTopK)
+        return Q3X_HIP_EINVAL;
+    const MoeLayout L = moe_layout(tokens, experts, top_k, H, I);
+    if (workspace_bytes < L.total || !aligned(workspace, 256)) return Q3X_HIP_EINVAL;
+    if (!aligned(gate_up, 2) || !aligned(down, 2) || !aligned(X, 16)) return Q3X_HIP_EINVAL;
+    const uint8_t* gu = static_cast<const uint8_t*>(gate_up);
+    const uint8_t* dn = static_cast<const uint8_t*>(down);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    if (tokens == 1) {
+        const int status = type == Q3X_HIP_MATRIX_Q8_0
+                               ? moe_decode<Q3X_HIP_MATRIX_Q8_0>(gu, dn, experts, H, I, X, ids, weights, top_k, Y,
+                                                                 accumulate, ws, L, SharedExpert{}, stream, nullptr,
+                                                                 logits, ids, weights)
+                               : moe_decode<Q3X_HIP_MATRIX_Q4_0>(gu, dn, experts, H, I, X, ids, weights, top_k, Y,
+                                                                 accumulate, ws, L, SharedExpert{}, stream, nullptr,
+                                                                 logits, ids, weights);
+        if (status != Q3X_HIP_ENOTSUP) return status;
+    }
+    const int status = launch_router_topk(logits, tokens, experts, top_k, ids, weights, stream);
+    if (status != Q3X_HIP_OK) return status;
+    return type == Q3X_HIP_MATRIX_Q8_0
+               ? moe_grouped<Q3X_HIP_MATRIX_Q8_0>(gu, dn, experts, H, I, X, tokens, ids, weights, top_k, Y,
+                                                  accumulate, ws, L, stream)
+               : moe_grouped<Q3X_HIP_MATRIX_Q4_0>(gu, dn, experts, H, I, X, tokens, ids, weights, top_k, Y,
+                                                  accumulate, ws, L, stream);
+}
+
 static bool moe_layer_ok(const q3x_hip_moe_layer_weights* w, int tokens) {
     if (!w || !w->router || !w->gate_up || !w->down || !w->shared_gate || !w->shared_up || !w->shared_down ||
         !w->shared_scale || !is_quant_type(w->type))
@@ -1126,3 +1228,4 @@ int q3x::moe_layer_decode_add(const q3x_hip_moe_layer_weights& layer, const floa
     if (norm_w && !aligned(norm_w, 8)) return Q3X_HIP_ENOTSUP;
     return moe_layer_checked(&layer, X, 1, Y, nullptr, nullptr, workspace, workspace_bytes, stream, true, norm_w);
 }
+

@@ -180,11 +180,13 @@ struct ExpertRows {
         GW = last - first;
         return s;
     }
-    // Expert matrix of slot s (null when its id is out of range).
-    __device__ const uint8_t* expert_of_slot(int s) const {
-        const int e = __builtin_amdgcn_readfirstlane(ids[s]);
+    // Expert matrix of slot s (null when its id is out of range), the ids
+    // read from `src` (ids, or a launch's own routing in LDS).
+    __device__ const uint8_t* expert_of_slot(int s, const int* src) const {
+        const int e = __builtin_amdgcn_readfirstlane(src[s]);
         return e >= 0 && e < experts ? pool + static_cast<size_t>(e) * expert_bytes : nullptr;
     }
+    __device__ const uint8_t* expert_of_slot(int s) const { return expert_of_slot(s, ids); }
     __device__ OneMatrix for_wave(int& gw, int& GW, int& nrows) const {
         const int s = slot_of_wave(gw, GW);
         nrows = rows_per_expert;
@@ -238,7 +240,8 @@ struct ExpertGateUpRows : ExpertRows {
     const uint8_t* shared_gate;
     const uint8_t* shared_up;
     int shared_I;
-    __device__ GateUpPairs for_wave(int& gw, int& GW, int& nrows) const {
+    __device__ GateUpPairs for_wave(int& gw, int& GW, int& nrows) const { return for_wave(gw, GW, nrows, ids); }
+    __device__ GateUpPairs for_wave(int& gw, int& GW, int& nrows, const int* src) const {
         const int s = slot_of_wave(gw, GW);
         const bool shared = shared_gate && s == slots - 1;
         const int rows = shared ? shared_I : I;
@@ -246,7 +249,7 @@ struct ExpertGateUpRows : ExpertRows {
         nrows = 2 * GW * ((rows + GW - 1) / GW);
         float* h = y + static_cast<size_t>(s) * I;
         if (shared) return GateUpPairs{shared_gate, shared_up, row_bytes, x, h, rows, GW, pool};
-        const uint8_t* w = expert_of_slot(s);
+        const uint8_t* w = expert_of_slot(s, src);
         const uint8_t* up = w ? w + static_cast<size_t>(I) * row_bytes : nullptr;
         return GateUpPairs{w, up, row_bytes, x, h, rows, GW, pool};
     }

@@ -80,6 +80,14 @@ def test_invalid_arguments_are_rejected_without_device_work():
     assert lib.q3x_hip_moe_routed(P, P, 2, 256, 2048, 500, P, 2048, P, P, 8, P, 0, P, ws, N) == q3x.EINVAL
     assert lib.q3x_hip_moe_routed(P, P, 2, 4, 2048, 512, P, 1, P, P, 5, P, 0, P, ws, N) == q3x.EINVAL
     assert lib.q3x_hip_moe_routed(P, P, 0, 4, 2048, 512, P, 1, P, P, 2, P, 0, P, ws, N) == q3x.ENOTSUP
+    rl = lib.q3x_hip_moe_routed_logits
+    ws1 = lib.q3x_hip_moe_workspace_bytes(1, 256, 8, 2048, 512)
+    assert rl(P, P, 2, 256, 2048, 512, P, 1, P, 8, P, P, P, 0, P, ws1 - 1, N) == q3x.EINVAL  # short workspace
+    assert rl(P, P, 2, 256, 2048, 512, P, 1, N, 8, P, P, P, 0, P, ws, N) == q3x.EINVAL      # no logits
+    assert rl(P, P, 2, 256, 2048, 512, P, 1, P, 8, N, P, P, 0, P, ws, N) == q3x.EINVAL      # no ids output
+    assert rl(P, P, 2, 256, 2048, 512, P, 1, P, 9, P, P, P, 0, P, ws, N) == q3x.EINVAL      # top_k > 8
+    assert rl(P, P, 2, 2048, 2048, 512, P, 1, P, 8, P, P, P, 0, P, ws, N) == q3x.EINVAL     # experts > 1024
+    assert rl(P, P, 0, 256, 2048, 512, P, 1, P, 8, P, P, P, 0, P, ws, N) == q3x.ENOTSUP
     item = q3x.MvItem(0x1000, 4, 0x1000, 0)
     items = (q3x.MvItem * 9)(*([item] * 9))
     ip = ctypes.cast(items, ctypes.c_void_p)

@@ -1,0 +1,81 @@
+"""q3x_hip_moe_routed_logits: router top-k and routed experts in one call.
+At one token the gate/up launch routes the token itself; its ids, weights and
+output must equal the two calls it replaces (q3x_hip_router_topk, then
+q3x_hip_moe_routed) bit for bit, and the ids the oracle's restatement of
+engine.cpp:377-405 exactly."""
+import numpy as np
+import pytest
+
+import oracle
+import qwen3x_amd as q3x
+from tests.helpers import Q4_0, Q8_0, random_blocks
+from tests.test_gpu_parity import _torch, dev, host, moe_bound, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("type_,E,H,I,k,tokens", [
+    (Q4_0, 256, 2048, 512, 8, 1),     # config 4 decode
+    (Q4_0, 256, 2048, 512, 8, 33),    # prefill: router kernel, then the grouped GEMMs
+    (Q8_0, 8, 512, 256, 2, 1),
+    (Q4_0, 600, 256, 256, 4, 1),      # more experts than 256: eight per lane in the router
+    (Q4_0, 16, 256, 64, 4, 1),        # unaligned down rows: the grouped path at one token
+])
+def test_routed_logits_equals_router_then_routed(type_, E, H, I, k, tokens):
+    torch = _torch()
+    rng = np.random.default_rng(E + H + I + k + tokens)
+    gu = dev(random_blocks(rng, type_, E * 2 * I, H))
+    dn = dev(random_blocks(rng, type_, E * H, I))
+    logits_h = rng.normal(0, 1, (tokens, E)).astype(np.float32)
+    logits_h[0, :4] = logits_h[0, 4]      # ties: the lowest expert index wins
+    X = dev(rng.normal(0, 1, (tokens, H)).astype(np.float32))
+    logits = dev(logits_h)
+    gul, dnl = q3x.ExpertLinear(gu, E, 2 * I, H, type_), q3x.ExpertLinear(dn, E, H, I, type_)
+    ids0 = torch.empty((tokens, k), dtype=torch.int32, device="cuda:0")
+    w0 = torch.empty((tokens, k), dtype=torch.float32, device="cuda:0")
+    Y0 = torch.empty((tokens, H), dtype=torch.float32, device="cuda:0")
+    say(f"routed_logits type={type_} E={E} H={H} I={I} k={k} tokens={tokens}")
+    q3x.router_top_k(logits, tokens, E, k, ids0, w0)
+    q3x.moe_routed(gul, dnl, X, tokens, ids0, w0, k, Y0)
+    ids1 = torch.full((tokens, k), -5, dtype=torch.int32, device="cuda:0")
+    w1 = torch.full((tokens, k), float("nan"), dtype=torch.float32, device="cuda:0")
+    Y1 = torch.full((tokens, H), float("nan"), dtype=torch.float32, device="cuda:0")
+    q3x.moe_routed_logits(gul, dnl, X, tokens, logits, k, ids1, w1, Y1)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(ids1), host(ids0))
+    assert np.array_equal(host(w1).view(np.uint32), host(w0).view(np.uint32))
+    assert np.array_equal(host(Y1).view(np.uint32), host(Y0).view(np.uint32))
+    ids_o, w_o, _ = oracle.router_top_k(logits_h, k)
+    assert np.array_equal(host(ids1), ids_o)
+    assert np.array_equal(host(w1).view(np.uint32), w_o.view(np.uint32))
+    # accumulate: Y += the same routed sum
+    q3x.moe_routed_logits(gul, dnl, X, tokens, logits, k, ids1, w1, Y1, accumulate=True)
+    q3x.moe_routed(gul, dnl, X, tokens, ids0, w0, k, Y0, accumulate=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(Y1).view(np.uint32), host(Y0).view(np.uint32))
+
+
+def test_routed_logits_config4_against_the_oracle():
+    """Config 4 decode over several tokens in turn (different experts each
+    call, one workspace): every output within the routed bound of the oracle."""
+    torch = _torch()
+    type_, E, H, I, k = Q4_0, 256, 2048, 512, 8
+    rng = np.random.default_rng(404)
+    gu_h, dn_h = random_blocks(rng, type_, E * 2 * I, H), random_blocks(rng, type_, E * H, I)
+    gul = q3x.ExpertLinear(dev(gu_h), E, 2 * I, H, type_)
+    dnl = q3x.ExpertLinear(dev(dn_h), E, H, I, type_)
+    ws = torch.empty(q3x.moe_workspace_bytes(1, E, k, H, I), dtype=torch.uint8, device="cuda:0")
+    for t in range(4):
+        logits_h = rng.normal(0, 1, (1, E)).astype(np.float32)
+        X_h = rng.normal(0, 1, (1, H)).astype(np.float32)
+        ids = torch.empty((1, k), dtype=torch.int32, device="cuda:0")
+        w = torch.empty((1, k), dtype=torch.float32, device="cuda:0")
+        Y = torch.empty((1, H), dtype=torch.float32, device="cuda:0")
+        say(f"routed_logits config 4 token {t}")
+        q3x.moe_routed_logits(gul, dnl, dev(X_h), 1, dev(logits_h), k, ids, w, Y, workspace=ws)
+        torch.cuda.synchronize()
+        ids_o, w_o, _ = oracle.router_top_k(logits_h, k)
+        assert np.array_equal(host(ids), ids_o)
+        want = oracle.moe_routed(gu_h, dn_h, type_, E, H, I, X_h, ids_o, w_o)
+        bound = moe_bound(gu_h, dn_h, type_, E, H, I, X_h, ids_o, w_o)
+        assert np.all(np.abs(host(Y).astype(np.float64) - want) <= bound)
