@@ -41,37 +41,50 @@ constexpr int kGrpBM = 64;
 // One token's routing in one wavefront; lane l holds experts [PER*l, PER*l +
 // PER), so lane order is expert order.  The softmax is the reference's
 // operation for operation (engine.cpp:380-387): the maximum (exact in any
-// order), p = exp(l - max) with libm's expf arithmetic (libm_expf.h), the
-// total added in expert order from zero, and p / total correctly rounded.  The total's order is
-// sequential, so the wave writes p to LDS and every lane runs the same chain
-// of adds over it (broadcast reads).  Then top_k argmax passes, each over
-// keys (0 for an expert already chosen or past the end, else the
-// probability's bits + 1: probabilities are >= 0, so their bits order like
-// the values).  A lane keeps its best key (lowest index among equal ones);
-// the wave's largest key is found with DPP and readlanes, and the lowest lane
-// holding it wins, i.e. the lowest expert index among equal probabilities, as
-// the reference's strict '>' scan picks.  Weights = p / (sum of the selected
-// p, added in slot order), correctly rounded (engine.cpp:388-404).  Lane s <
-// top_k returns slot s's expert and weight.  mine_p: LDS for 64 * PER floats.
+// order), e = exp(l - max) with libm's expf arithmetic (libm_expf.h), the
+// total added in expert order from zero, and p = e / total correctly
+// rounded.  The total's order is sequential, so the wave writes e to LDS and
+// every lane runs the same chain of adds over it (broadcast reads).  Then
+// top_k argmax passes, each over keys (0 for an expert already chosen or
+// past the end, else the probability's bits + 1: probabilities are >= 0, so
+// their bits order like the values).  A lane keeps its best key (lowest
+// index among equal ones); the wave's largest key is found with DPP and
+// readlanes, and the lowest lane holding it wins, i.e. the lowest expert
+// index among equal probabilities, as the reference's strict '>' scan picks.
+// Weights = p / (sum of the selected p, added in slot order), correctly
+// rounded (engine.cpp:388-404).  The phases below are shared by the two
+// routers: router_topk_wave (ids and weights) and router_select_by_exp (ids
+// alone, without the total when that is provably safe).
+
+// The token's logits, PER per lane (-inf past the end).
 template <int PER>
-__device__ __forceinline__ void router_topk_wave(const float* __restrict__ row, int experts, int top_k,
-                                                 float* __restrict__ mine_p, int& out_id, float& out_weight) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int first = PER * lane;
-    float p[PER];
+__device__ __forceinline__ void router_load(const float* __restrict__ row, int experts, float (&l)[PER]) {
+    const int first = PER * (threadIdx.x & (kWave - 1));
 #pragma unroll
-    for (int j = 0; j < PER; ++j) p[j] = first + j < experts ? row[first + j] : -INFINITY;
+    for (int j = 0; j < PER; ++j) l[j] = first + j < experts ? row[first + j] : -INFINITY;
+}
+
+// e = exp(l - max) in registers and in mine_p (LDS, 64 * PER floats; zeros
+// past the end pad the last group of four).
+template <int PER>
+__device__ __forceinline__ void router_exps(const float (&l)[PER], int experts, float* __restrict__ mine_p,
+                                            float (&e)[PER]) {
+    const int first = PER * (threadIdx.x & (kWave - 1));
     float local_max = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) local_max = local_max < p[j] ? p[j] : local_max;
+    for (int j = 0; j < PER; ++j) local_max = local_max < l[j] ? l[j] : local_max;
     const float maximum = wave_max_f32(local_max);
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-        p[j] = first + j < experts ? libm_expf(p[j] - maximum) : 0.0f;
-        mine_p[first + j] = p[j];  // zeros past the end pad the last group of four
+        e[j] = first + j < experts ? libm_expf(l[j] - maximum) : 0.0f;
+        mine_p[first + j] = e[j];
     }
     wave_lds_sync();
-    // The padding zeros add nothing: total + 0 == total for total >= +0.
+}
+
+// The softmax total, added in expert order from zero (every lane the same).
+// The padding zeros add nothing: total + 0 == total for total >= +0.
+__device__ __forceinline__ float router_total(const float* __restrict__ mine_p, int experts) {
     float total = 0.0f;
     const int groups4 = (experts + 3) / 4;
 #pragma unroll 4
@@ -82,17 +95,20 @@ __device__ __forceinline__ void router_topk_wave(const float* __restrict__ row, 
         total += v.z;
         total += v.w;
     }
-    uint32_t key[PER];
-#pragma unroll
-    for (int j = 0; j < PER; ++j) key[j] = first + j < experts ? __float_as_uint(__fdiv_rn(p[j], total)) + 1u : 0u;
+    return total;
+}
 
-    float chosen[kRouterMaxTopK];
-    int chosen_id[kRouterMaxTopK];
+// `passes` argmax passes over the keys (see above): chosen[s] = the value of
+// the s-th key, chosen_id[s] its expert (uniform).
+template <int PER>
+__device__ __forceinline__ void router_passes(uint32_t (&key)[PER], int passes, float (&chosen)[kRouterMaxTopK + 1],
+                                              int (&chosen_id)[kRouterMaxTopK + 1]) {
+    const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
-    for (int slot = 0; slot < kRouterMaxTopK; ++slot) {
+    for (int slot = 0; slot < kRouterMaxTopK + 1; ++slot) {
         chosen[slot] = 0.0f;
         chosen_id[slot] = 0;
-        if (slot >= top_k) continue;
+        if (slot >= passes) continue;
         uint32_t best = 0;
         int best_j = 0;
 #pragma unroll
@@ -109,17 +125,88 @@ __device__ __forceinline__ void router_topk_wave(const float* __restrict__ row, 
                 if (j == best_j) key[j] = 0u;
         }
     }
+}
+
+// Weights of the selected probabilities: p_s / (sum of p in slot order),
+// correctly rounded; lane s < top_k returns slot s's.
+__device__ __forceinline__ float router_slot_weight(const float (&chosen)[kRouterMaxTopK + 1], int top_k) {
+    const int lane = threadIdx.x & (kWave - 1);
     float selected_total = 0.0f;
 #pragma unroll
     for (int slot = 0; slot < kRouterMaxTopK; ++slot)
         if (slot < top_k) selected_total += chosen[slot];
     float mine = 0.0f;
-    int mine_id = 0;
 #pragma unroll
     for (int slot = 0; slot < kRouterMaxTopK; ++slot)
-        if (slot == lane) { mine = chosen[slot]; mine_id = chosen_id[slot]; }
-    out_id = mine_id;
-    out_weight = __fdiv_rn(mine, selected_total);
+        if (slot == lane) mine = chosen[slot];
+    return __fdiv_rn(mine, selected_total);
+}
+
+__device__ __forceinline__ int lane_slot_id(const int (&chosen_id)[kRouterMaxTopK + 1]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    int mine = 0;
+#pragma unroll
+    for (int slot = 0; slot < kRouterMaxTopK; ++slot)
+        if (slot == lane) mine = chosen_id[slot];
+    return mine;
+}
+
+// The full router: lane s < top_k returns slot s's expert and weight.
+template <int PER>
+__device__ __forceinline__ void router_topk_wave(const float* __restrict__ row, int experts, int top_k,
+                                                 float* __restrict__ mine_p, int& out_id, float& out_weight) {
+    const int first = PER * (threadIdx.x & (kWave - 1));
+    float l[PER], e[PER];
+    router_load<PER>(row, experts, l);
+    router_exps<PER>(l, experts, mine_p, e);
+    const float total = router_total(mine_p, experts);
+    uint32_t key[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) key[j] = first + j < experts ? __float_as_uint(__fdiv_rn(e[j], total)) + 1u : 0u;
+    float chosen[kRouterMaxTopK + 1];
+    int chosen_id[kRouterMaxTopK + 1];
+    router_passes<PER>(key, top_k, chosen, chosen_id);
+    out_id = lane_slot_id(chosen_id);
+    out_weight = router_slot_weight(chosen, top_k);
+}
+
+// The experts alone, ordered by e instead of p = e / total where that order
+// is provably p's: dividing by the same total is monotone, equal e give
+// equal p (ties keep the lowest index in either order), and two e more than
+// 2^-21 apart (relative) stay strictly ordered after the division's rounding
+// (each rounding moves a normal quotient by at most 2^-24 of it).  So when
+// every two neighbours of the top_k + 1 largest e are equal or that far
+// apart, and the smallest of them is at least 2^-100 (its quotient by a total
+// of at most 1024 stays normal), the e order's first top_k are the
+// reference's ids in the reference's order; the total's 256-add chain is
+// then skipped.  Returns false (and no ids) otherwise.
+template <int PER>
+__device__ __forceinline__ bool router_select_by_exp(const float* __restrict__ row, int experts, int top_k,
+                                                     float* __restrict__ mine_p, int& out_id) {
+    const int first = PER * (threadIdx.x & (kWave - 1));
+    float l[PER], e[PER];
+    router_load<PER>(row, experts, l);
+    router_exps<PER>(l, experts, mine_p, e);
+    uint32_t key[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) key[j] = first + j < experts ? __float_as_uint(e[j]) + 1u : 0u;
+    const int passes = min(top_k + 1, experts);
+    float chosen[kRouterMaxTopK + 1];
+    int chosen_id[kRouterMaxTopK + 1];
+    router_passes<PER>(key, passes, chosen, chosen_id);
+    bool apart = true;
+#pragma unroll
+    for (int s = 0; s + 1 < kRouterMaxTopK + 1; ++s)
+        if (s + 1 < passes) {
+            const double a = chosen[s], b = chosen[s + 1];
+            apart = apart && (a == b || a >= b * (1.0 + 0x1p-21));
+        }
+    float smallest = chosen[0];
+#pragma unroll
+    for (int s = 1; s < kRouterMaxTopK + 1; ++s)
+        if (s < passes) smallest = chosen[s];
+    out_id = lane_slot_id(chosen_id);
+    return apart && smallest >= 0x1p-100f;
 }
 
 // One wavefront per token (router_topk_wave); lane s < top_k writes slot s.
@@ -142,12 +229,15 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
 }
 
 // The decode gate_up rows of ExpertGateUpRows, the experts chosen inside the
-// launch: route() runs the reference router (router_topk_wave) on the
-// token's logits in wave 0 of every workgroup -- a workgroup needs only the
-// selection, and computing it where it is used spares the router its own
-// launch -- and keeps ids and weights in LDS for for_wave; workgroup 0 also
-// stores them to ids_out / weights_out for the down-and-combine launch and
-// the caller.  Every workgroup computes the same selection bit for bit.
+// launch: route() selects the token's experts from its logits in wave 0 of
+// every workgroup -- a workgroup needs only the selection, and computing it
+// where it is used spares the router its own launch -- and keeps the ids in
+// LDS for for_wave.  Workgroup 0 runs the full router (router_topk_wave) and
+// stores ids and weights to ids_out / weights_out for the down-and-combine
+// launch and the caller; the others take router_select_by_exp's ids where it
+// applies (no total: the 256-add chain off their critical path), else the
+// full router's.  Every workgroup selects the same ids in the same order.
+// Workgroup 0 starts first, so its longer routing rarely delays the launch.
 struct RoutedGateUpRows : ExpertGateUpRows {
     static constexpr uint32_t kRouteLds = 64 + 4 * kRouterMaxExperts;  // ids, weights, probabilities
     const float* logits;
@@ -160,11 +250,16 @@ struct RoutedGateUpRows : ExpertGateUpRows {
         float* probs = reinterpret_cast<float*>(lds + 64);
         if (threadIdx.x < kWave) {
             const int lane = threadIdx.x;
-            int id;
-            float w;
-            if (experts <= 4 * kWave) router_topk_wave<4>(logits, experts, top_k, probs, id, w);
-            else if (experts <= 8 * kWave) router_topk_wave<8>(logits, experts, top_k, probs, id, w);
-            else router_topk_wave<16>(logits, experts, top_k, probs, id, w);
+            int id = 0;
+            float w = 0.0f;
+            // Workgroup 0 needs the weights too; the others only the ids.
+            const bool by_exp = blockIdx.x != 0 && experts <= 4 * kWave &&
+                                router_select_by_exp<4>(logits, experts, top_k, probs, id);
+            if (!by_exp) {
+                if (experts <= 4 * kWave) router_topk_wave<4>(logits, experts, top_k, probs, id, w);
+                else if (experts <= 8 * kWave) router_topk_wave<8>(logits, experts, top_k, probs, id, w);
+                else router_topk_wave<16>(logits, experts, top_k, probs, id, w);
+            }
             if (lane < top_k) {
                 chosen[lane] = id;
                 chosen_w[lane] = w;

@@ -79,3 +79,47 @@ def test_routed_logits_config4_against_the_oracle():
         want = oracle.moe_routed(gu_h, dn_h, type_, E, H, I, X_h, ids_o, w_o)
         bound = moe_bound(gu_h, dn_h, type_, E, H, I, X_h, ids_o, w_o)
         assert np.all(np.abs(host(Y).astype(np.float64) - want) <= bound)
+
+
+@pytest.mark.parametrize("case", ["ulp_top", "ulp_boundary", "tie_boundary", "wide"])
+def test_routed_logits_decode_near_ties(case):
+    """One-token routing inside the gate_up launch with logits one ulp apart
+    at the top or at the top-8 boundary (workgroups other than the first
+    cannot order those by exp alone and take the full router), exact ties at
+    the boundary, and a wide spread (tiny exp values): the ids every
+    workgroup used -- seen through the output -- and the ids and weights
+    returned equal the two-call path and the oracle."""
+    torch = _torch()
+    type_, E, H, I, k = Q4_0, 256, 2048, 512, 8
+    rng = np.random.default_rng(77)
+    gu = dev(random_blocks(rng, type_, E * 2 * I, H))
+    dn = dev(random_blocks(rng, type_, E * H, I))
+    gul, dnl = q3x.ExpertLinear(gu, E, 2 * I, H, type_), q3x.ExpertLinear(dn, E, H, I, type_)
+    lg = rng.normal(0, 1, (1, E)).astype(np.float32)
+    order = np.argsort(-lg[0], kind="stable")
+    down = np.float32(-np.inf)
+    if case == "ulp_top":
+        lg[0, order[1]] = np.nextafter(lg[0, order[0]], down)
+    elif case == "ulp_boundary":
+        lg[0, order[k]] = np.nextafter(lg[0, order[k - 1]], down)
+    elif case == "tie_boundary":
+        lg[0, order[k]] = lg[0, order[k - 1]]
+    else:
+        lg *= np.float32(40)
+    X = dev(rng.normal(0, 1, (1, H)).astype(np.float32))
+    logits = dev(lg)
+    ids0 = torch.empty((1, k), dtype=torch.int32, device="cuda:0")
+    w0 = torch.empty((1, k), dtype=torch.float32, device="cuda:0")
+    Y0 = torch.empty((1, H), dtype=torch.float32, device="cuda:0")
+    say(f"routed_logits near ties case={case}")
+    q3x.router_top_k(logits, 1, E, k, ids0, w0)
+    q3x.moe_routed(gul, dnl, X, 1, ids0, w0, k, Y0)
+    ids1 = torch.empty((1, k), dtype=torch.int32, device="cuda:0")
+    w1 = torch.empty((1, k), dtype=torch.float32, device="cuda:0")
+    Y1 = torch.empty((1, H), dtype=torch.float32, device="cuda:0")
+    q3x.moe_routed_logits(gul, dnl, X, 1, logits, k, ids1, w1, Y1)
+    torch.cuda.synchronize()
+    ids_o, w_o, _ = oracle.router_top_k(lg, k)
+    assert np.array_equal(host(ids1), ids_o) and np.array_equal(host(ids0), ids_o)
+    assert np.array_equal(host(w1).view(np.uint32), w_o.view(np.uint32))
+    assert np.array_equal(host(Y1).view(np.uint32), host(Y0).view(np.uint32))
