@@ -225,6 +225,47 @@ __device__ __forceinline__ float conv_token(float x, const float* hist, const ui
     return silu_ref(sum);
 }
 
+// conv_token in two halves, so that a decode step can request every input
+// before it knows the position: conv_fetch loads the channel's input, both
+// history copies and the weights; conv_apply picks the copy by position
+// parity and runs conv_token's arithmetic in the same order.
+struct ConvInputs {
+    float x;
+    float past[2][kMaxConv - 1];
+    float w[kMaxConv];
+};
+__device__ __forceinline__ void conv_fetch(ConvInputs& in, float x, const float* history, size_t copy,
+                                           const uint16_t* w, int ci, int CK) {
+    in.x = x;
+    const float* h0 = history + static_cast<size_t>(ci) * (CK - 1);
+#pragma unroll
+    for (int i = 0; i < kMaxConv - 1; ++i) {
+        in.past[0][i] = i < CK - 1 ? h0[i] : 0.0f;
+        in.past[1][i] = i < CK - 1 ? h0[copy + i] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxConv; ++i) in.w[i] = i < CK ? bf16_value(w[static_cast<size_t>(ci) * CK + i]) : 0.0f;
+}
+__device__ __forceinline__ float conv_apply(const ConvInputs& in, int parity, int CK, float* hist_out) {
+    float past[kMaxConv - 1];
+#pragma unroll
+    for (int i = 0; i < kMaxConv - 1; ++i) past[i] = parity ? in.past[1][i] : in.past[0][i];
+    float last = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxConv; ++i)
+        if (i == CK - 1) last = in.w[i];
+    float sum = in.x * last;
+#pragma unroll
+    for (int i = 0; i < kMaxConv - 1; ++i)
+        if (i < CK - 1) sum = fmaf(past[i], in.w[i], sum);
+    if (hist_out) {
+#pragma unroll
+        for (int i = 0; i < kMaxConv - 1; ++i)
+            if (i < CK - 1) hist_out[i] = i + 1 < CK - 1 ? past[i + 1] : in.x;
+    }
+    return silu_ref(sum);
+}
+
 // The DeltaNet memory S of a value head is stored column by column,
 // S[c * KD + k] (value column c, key k), so a thread's run of consecutive
 // keys of one column is contiguous: 16-byte accesses when KD % 4 == 0.
@@ -443,32 +484,37 @@ __global__ __launch_bounds__(kScanThreads) void delta_step_kernel(
     const int c = slice * kScanCols + cl, k0 = (lane % kScanGroups) * kScanKeys;
     const bool col = c < VD;
     float* S = memory + (static_cast<size_t>(head) * VD + (col ? c : 0)) * KD;  // column c
+    // Every input is requested before any is used -- the memory columns,
+    // the head's gate parameters, the conv inputs with both history copies
+    // (the position only picks one), the output gate's norm and z -- so the
+    // step waits for one round trip to memory instead of four.
     float s[kScanKeys];
     load_keys<kScanKeys>(S, k0, KD, col, s);
-    const float a_in = a[head], b_in = b[head];
     const int pos = *position;
+    const float a_in = a[head], b_in = b[head];
+    const float alog_h = alog[head];
+    const uint16_t dt_h = dt[head];
+    const bool writer = lane % kScanGroups == 0 && col;
+    const size_t at = static_cast<size_t>(head) * VD + c;
+    const float norm_c = writer ? norm[c] : 0.0f;
+    const float z_at = writer ? z[at] : 0.0f;
     const size_t copy = static_cast<size_t>(DQKV) * (CK - 1);
-    const float* hin = history + (pos & 1) * copy;
-    float* hout = history + ((pos + 1) & 1) * copy;
     const bool qk_writer = head % per == 0 && slice == 0;
-    // q | k channel of this thread (t < 128: q, else k), convolved.
+    // q | k channel of this thread (t < 128: q, else k).
     const int ch = t & 127;
+    const int ci_qk = (t < 128 ? 0 : DQK) + kh * KD + ch;
+    ConvInputs in_qk{}, in_v{};
+    if (ch < KD) conv_fetch(in_qk, qkv[ci_qk], history, copy, conv_w, ci_qk, CK);
+    const int cv = slice * kScanCols + t;
+    const int ci_v = 2 * DQK + head * VD + cv;  // each v channel belongs to one slice
+    const bool has_v = t < kScanCols && cv < VD;
+    if (has_v) conv_fetch(in_v, qkv[ci_v], history, copy, conv_w, ci_v, CK);
+    const int parity = pos & 1;
+    float* hout = history + static_cast<size_t>(parity ^ 1) * copy;
     float x = 0.0f;
-    if (ch < KD) {
-        const int ci = (t < 128 ? 0 : DQK) + kh * KD + ch;
-        x = conv_token(qkv[ci], hin + static_cast<size_t>(ci) * (CK - 1), conv_w + static_cast<size_t>(ci) * CK, CK,
-                       qk_writer ? hout + static_cast<size_t>(ci) * (CK - 1) : nullptr);
-    }
-    if (t < kScanCols) {
-        const int cv = slice * kScanCols + t;
-        float v = 0.0f;
-        if (cv < VD) {
-            const int ci = 2 * DQK + head * VD + cv;  // each v channel belongs to one slice
-            v = conv_token(qkv[ci], hin + static_cast<size_t>(ci) * (CK - 1), conv_w + static_cast<size_t>(ci) * CK,
-                           CK, hout + static_cast<size_t>(ci) * (CK - 1));
-        }
-        vs[t] = v;
-    }
+    if (ch < KD)
+        x = conv_apply(in_qk, parity, CK, qk_writer ? hout + static_cast<size_t>(ci_qk) * (CK - 1) : nullptr);
+    if (t < kScanCols) vs[t] = has_v ? conv_apply(in_v, parity, CK, hout + static_cast<size_t>(ci_v) * (CK - 1)) : 0.0f;
     // L2 norms: waves 0, 1 hold q, waves 2, 3 hold k.
     const float sq = wave_sum_f32(x * x);
     if (lane == 0) squares[wave] = sq;
@@ -477,7 +523,7 @@ __global__ __launch_bounds__(kScanThreads) void delta_step_kernel(
     else qk[t] = x * (1.0f / sqrtf(squares[2] + squares[3] + kEps));
     __syncthreads();
     const float bb = sigmoid_ref(b_in);
-    const float sc = expf(-expf(alog[head]) * softplus_ref(a_in + bf16_value(dt[head])));
+    const float sc = expf(-expf(alog_h) * softplus_ref(a_in + bf16_value(dt_h)));
     const f32x4* kp = reinterpret_cast<const f32x4*>(qk + 128 + k0);
     const f32x4* qp = reinterpret_cast<const f32x4*>(qk + k0);
     float p0 = 0.0f, p1 = 0.0f;
@@ -511,10 +557,9 @@ __global__ __launch_bounds__(kScanThreads) void delta_step_kernel(
     o += dpp_f32<0xB1>(o);
     o += dpp_f32<0x4E>(o);
     o += dpp_f32<0x141>(o);
-    if (lane % kScanGroups == 0 && col) {
-        const size_t at = static_cast<size_t>(head) * VD + c;
+    if (writer) {
         out[at] = o;
-        gate[at] = norm[c] * silu_ref(z[at]);
+        gate[at] = norm_c * silu_ref(z_at);
     }
     store_keys<kScanKeys>(S, k0, KD, col, s);
 }
