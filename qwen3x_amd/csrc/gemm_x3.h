@@ -292,8 +292,14 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
 }
 
 // Tile shapes of the launches: 128 A rows x 256 weight rows on 8 waves of
-// 64x64 (one workgroup per CU: 209 registers), 64 x 128 on 8 waves of 32x32
-// (three), 64 x 64 on 4 waves of 32x32 (four).  (128 x 128 on 8 waves of
+// 64x64 (one workgroup per CU: 209 registers), 128 x 192 on 8 waves of
+// 64x48 (one per CU; paired-column policies excluded: SN is odd), 64 x 128
+// on 8 waves of 32x32 (three), 64 x 64 on 4 waves of 32x32 (four).  128 x 192
+// exists for row counts that 256 leaves uneven over the CUs: 512 tokens x
+// 12288 rows x 4096 columns is 256 tiles of it, one per CU, at 306 TFLOP/s
+// (Q8_0; 260 on 128 x 256, whose 192 tiles leave 64 CUs idle), and 512 x
+// 17408 x 5120 runs at 257 (238 on 64 x 128); with many tiles per CU it
+// runs at ~340, below 128 x 256's ~383.  (128 x 128 on 8 waves of
 // 64x32, two per CU, measured 200 / 330 TFLOP/s at one / two resident and
 // never beat these three on the config and engine shapes.)  A launch takes the shape of least estimated time: the
 // busiest CU takes ceil(tiles / CUs) tiles, resident up to the occupancy at
@@ -302,7 +308,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
 // tokens x 12288 rows x 4096 columns 370 TFLOP/s on 128 x 256; 512 x 4096
 // x 12288 (64 tiles of 128 x 256) 208 on 64 x 128; 512 x 17408 x 5120 253
 // on 64 x 128 (272 tiles of 128 x 256 would leave 16 CUs a second one).
-enum class X3Shape { k128x256, k64x128, k64x64 };
+enum class X3Shape { k128x256, k64x128, k64x64, k128x192 };
 
 inline double x3_estimate(long long tiles, int area, int occupancy, const double* rate) {
     long long left = (tiles + kCUs - 1) / kCUs;
@@ -320,7 +326,7 @@ inline double x3_estimate(long long tiles, int area, int occupancy, const double
 constexpr int kX3LongK = 8192;
 
 // rows = weight rows (outputs per A row), count = A rows, cols = K.
-inline X3Shape x3_shape(int rows, int count, int cols) {
+inline X3Shape x3_shape(int rows, int count, int cols, bool paired = false) {
     auto tiles = [&](int bm, int bn) {
         return static_cast<long long>((rows + bn - 1) / bn) * ((count + bm - 1) / bm);
     };
@@ -328,11 +334,13 @@ inline X3Shape x3_shape(int rows, int count, int cols) {
     static constexpr double r64x128[] = {210.0, 240.0, 260.0};
     static constexpr double r64x128_long[] = {215.0, 290.0, 300.0};  // two stages ahead, K >= kX3LongK
     static constexpr double r64[] = {150.0, 190.0, 215.0, 230.0};
-    const double e[3] = {x3_estimate(tiles(128, 256), 128 * 256, 1, r256),
+    static constexpr double r192[] = {330.0};
+    const double e[4] = {x3_estimate(tiles(128, 256), 128 * 256, 1, r256),
                          x3_estimate(tiles(64, 128), 64 * 128, 3, cols >= kX3LongK ? r64x128_long : r64x128),
-                         x3_estimate(tiles(64, 64), 64 * 64, 4, r64)};
+                         x3_estimate(tiles(64, 64), 64 * 64, 4, r64),
+                         paired ? 1e300 : x3_estimate(tiles(128, 192), 128 * 192, 1, r192)};
     int best = 0;
-    for (int i = 1; i < 3; ++i)
+    for (int i = 1; i < 4; ++i)
         if (e[i] < e[best]) best = i;
     return static_cast<X3Shape>(best);
 }
@@ -352,8 +360,13 @@ int launch_x3_tiles(P pol, int rows, int count, int cols, hipStream_t stream) {
 
 template <uint32_t QT, class P>
 int launch_x3(const P& pol, int rows, int count, int cols, hipStream_t stream) {
-    switch (x3_shape(rows, count, cols)) {
+    switch (x3_shape(rows, count, cols, P::kPairedColumns)) {
         case X3Shape::k128x256: return launch_x3_tiles<QT, 2, 4, 4, 4, 1, true>(pol, rows, count, cols, stream);
+        case X3Shape::k128x192:
+            if constexpr (!P::kPairedColumns)
+                return launch_x3_tiles<QT, 2, 4, 4, 3, 1, false>(pol, rows, count, cols, stream);
+            else
+                return launch_x3_tiles<QT, 2, 4, 4, 4, 1, true>(pol, rows, count, cols, stream);
         case X3Shape::k64x128:
             if (cols >= kX3LongK) return launch_x3_tiles<QT, 2, 4, 2, 2, 2, false>(pol, rows, count, cols, stream);
             return launch_x3_tiles<QT, 2, 4, 2, 2, 1, false>(pol, rows, count, cols, stream);
