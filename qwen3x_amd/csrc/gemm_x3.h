@@ -20,6 +20,11 @@
 // FP32's subnormal range), an absolute error far below the FP32 rounding of
 // any sum it enters.
 //
+// KS = 2 runs the tile on two groups of WM x WN waves, each over half of the
+// K blocks (the first half the first ceil(blocks / 2)) with its own LDS
+// buffers; the second group's sums then pass through LDS and the first adds
+// them, acc = first + second, a fixed order.
+//
 // Tile: WM x WN waves, each SM x SN output blocks of 16x16 (wave tile
 // 16 SM x 16 SN); BM = 16 SM WM A rows, BN = 16 SN WN weight rows.  A K
 // stage is one weight block (32 columns).  Per stage the workgroup stages,
@@ -74,11 +79,12 @@ __device__ __forceinline__ void split3(float a, uint32_t& h1, uint32_t& h2, uint
     h3 = __float_as_uint(r - __uint_as_float(h2));
 }
 
-template <uint32_t QT, int WM, int WN, int SM, int SN, class Policy, int PF = 1, bool CF = false>
-__global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, int rows, int cols) {
+template <uint32_t QT, int WM, int WN, int SM, int SN, class Policy, int PF = 1, bool CF = false, int KS = 1>
+__global__ __launch_bounds__(KS * WM * WN * kWave) void gemm_x3_kernel(Policy pol, int rows, int cols) {
     static_assert(PF == 1 || PF == 2, "one or two stages in flight");
+    static_assert(KS == 1 || KS == 2, "the K blocks in one or two halves");
     static_assert(!Policy::kPairedColumns || SN % 2 == 0, "paired columns need column blocks in pairs");
-    constexpr int NT = WM * WN * kWave;
+    constexpr int NT = WM * WN * kWave;  // threads of one K half
     constexpr int BM = WM * SM * 16;
     constexpr int BN = WN * SN * 16;
     constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : QT == Q3X_HIP_MATRIX_Q4_0 ? kQ4Bytes : kBF16Bytes;
@@ -97,7 +103,11 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
     // One LDS buffer: the A planes (a1, a2, a3), the weight rows, the scales.
     constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64, D_BYTES = kScaled ? BN * 4 : 0;
     constexpr int BUF = 3 * A_BYTES + B_BYTES + D_BYTES;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * BUF];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_all[KS * 2 * BUF];
+    // With KS = 2 the second half's partial sums come back through LDS.
+    static_assert(KS == 1 || SM * SN * 4 * 4 * NT <= 2 * BUF, "partials fit a half's buffers");
+    const int half = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / NT);
+    uint8_t* const lds = lds_all + half * 2 * BUF;
     auto plane = [&](int buf, int p) { return lds + buf * BUF + p * A_BYTES; };
     auto wtile = [&](int buf) { return lds + buf * BUF + 3 * A_BYTES; };
     auto scales = [&](int buf) { return reinterpret_cast<float*>(lds + buf * BUF + 3 * A_BYTES + B_BYTES); };
@@ -121,7 +131,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
     GemmTile tile;
     if (!pol.tile(by, BM, tile)) return;
     const int n0 = bx * BN;
-    const int tid = threadIdx.x;
+    const int tid = static_cast<int>(threadIdx.x) % NT;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
     const int wm = wave / WN, wn = wave % WN;
@@ -144,13 +154,21 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
         b_src[p] = pol.b_row(tile, min(n0 + n, rows - 1));
     }
 
+    // The K blocks of this half: [kbeg, kbeg + kcnt); both halves run
+    // kmax stages (the same barriers), a half past its own count computes
+    // nothing.
+    const int nblk_all = cols / kBlock;
+    const int kmax = (nblk_all + KS - 1) / KS;
+    const int kbeg = half * kmax;
+    const int kcnt = KS == 1 ? nblk_all : min(kmax, nblk_all - kbeg);
     f32x4 a_reg[PF][A_PER_T];
     uint32_t b_raw[PF][B_PASSES][1 + Part::WORDS];
     auto load_stage = [&](int kb, int r) {
+        const int k = min(kbeg + max(kb, 0), nblk_all - 1);
 #pragma unroll
-        for (int i = 0; i < A_PER_T; ++i) a_reg[r][i] = *reinterpret_cast<const f32x4*>(a_src[i] + 32 * kb);
+        for (int i = 0; i < A_PER_T; ++i) a_reg[r][i] = *reinterpret_cast<const f32x4*>(a_src[i] + 32 * k);
 #pragma unroll
-        for (int p = 0; p < B_PASSES; ++p) Part::load(b_src[p] + static_cast<size_t>(kb) * BB, b_part, b_raw[r][p]);
+        for (int p = 0; p < B_PASSES; ++p) Part::load(b_src[p] + static_cast<size_t>(k) * BB, b_part, b_raw[r][p]);
     };
     auto store_stage = [&](int buf, int r) {
 #pragma unroll
@@ -203,7 +221,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
     const int s16 = (tile.mcount + 15) / 16;
     const int nsub = Policy::kPartialTiles ? max(0, min(SM, (s16 - wm + WM - 1) / WM)) : SM;
     const bool active = nsub > 0;
-    const int nblk = cols / kBlock;
+    const int nblk = kcnt;
 
     auto step = [&](int kb, int r) {
         const int buf = kb & 1;
@@ -211,7 +229,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
             store_stage(buf ^ 1, r);
             load_stage(min(kb + 1 + PF, nblk - 1), r);
         }
-        if (active) {
+        if (active && (KS == 1 || kb < nblk)) {
             bf16x8 bf[SN];
             float d[SN];
 #pragma unroll
@@ -259,9 +277,31 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
     for (int q = 1; q <= PF; ++q) load_stage(min(q, nblk - 1), q % PF);
     __syncthreads();
     // Stage s + 1 is in register set (s + 1) % PF when stage s runs.
-    for (int kb = 0; kb < nblk; kb += 2) {
+    const int nsteps = KS == 1 ? nblk : kmax;
+    for (int kb = 0; kb < nsteps; kb += 2) {
         step(kb, PF == 1 ? 0 : 1);
-        if (kb + 1 < nblk) step(kb + 1, 0);
+        if (kb + 1 < nsteps) step(kb + 1, 0);
+    }
+    if constexpr (KS == 2) {
+        // The second half's sums to LDS (its own buffers, free after the
+        // last barrier), then the first half adds them: acc = first + second.
+        float* part = reinterpret_cast<float*>(lds_all + 2 * BUF);
+        if (half == 1) {
+#pragma unroll
+            for (int i = 0; i < SM; ++i)
+#pragma unroll
+                for (int j = 0; j < SN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) part[((i * SN + j) * 4 + e) * NT + tid] = acc[i][j][e];
+        }
+        __syncthreads();
+        if (half == 1) return;
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+#pragma unroll
+            for (int j = 0; j < SN; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[i][j][e] += part[((i * SN + j) * 4 + e) * NT + tid];
     }
 
 #pragma unroll
@@ -299,7 +339,13 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
 // 12288 rows x 4096 columns is 256 tiles of it, one per CU, at 306 TFLOP/s
 // (Q8_0; 260 on 128 x 256, whose 192 tiles leave 64 CUs idle), and 512 x
 // 17408 x 5120 runs at 257 (238 on 64 x 128); with many tiles per CU it
-// runs at ~340, below 128 x 256's ~383.  (128 x 128 on 8 waves of
+// runs at ~340, below 128 x 256's ~383.  Over long K (>= kX3LongK) a
+// 64 x 128 tile can also run on two halves of 8 waves, each over half the
+// K blocks with its own LDS buffers, the second half's sums added to the
+// first's at the end (KS = 2; one 1024-thread workgroup per CU): 512 x 4096
+// x 12288 is 256 such tiles, one per CU, at 233 (Q8_0) / 260 (Q4_0) TFLOP/s
+// against 178 / 212 with 8 waves over the whole K; with more tiles than CUs
+// it loses to the 8-wave tile (three resident).  (128 x 128 on 8 waves of
 // 64x32, two per CU, measured 200 / 330 TFLOP/s at one / two resident and
 // never beat these three on the config and engine shapes.)  A launch takes the shape of least estimated time: the
 // busiest CU takes ceil(tiles / CUs) tiles, resident up to the occupancy at
@@ -308,7 +354,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_kernel(Policy pol, in
 // tokens x 12288 rows x 4096 columns 370 TFLOP/s on 128 x 256; 512 x 4096
 // x 12288 (64 tiles of 128 x 256) 208 on 64 x 128; 512 x 17408 x 5120 253
 // on 64 x 128 (272 tiles of 128 x 256 would leave 16 CUs a second one).
-enum class X3Shape { k128x256, k64x128, k64x64, k128x192 };
+enum class X3Shape { k128x256, k64x128, k64x64, k128x192, k64x128_split };
 
 inline double x3_estimate(long long tiles, int area, int occupancy, const double* rate) {
     long long left = (tiles + kCUs - 1) / kCUs;
@@ -335,26 +381,28 @@ inline X3Shape x3_shape(int rows, int count, int cols, bool paired = false) {
     static constexpr double r64x128_long[] = {215.0, 290.0, 300.0};  // two stages ahead, K >= kX3LongK
     static constexpr double r64[] = {150.0, 190.0, 215.0, 230.0};
     static constexpr double r192[] = {330.0};
-    const double e[4] = {x3_estimate(tiles(128, 256), 128 * 256, 1, r256),
+    static constexpr double r64x128_split[] = {240.0};  // K halves on 16 waves, one workgroup per CU
+    const double e[5] = {x3_estimate(tiles(128, 256), 128 * 256, 1, r256),
                          x3_estimate(tiles(64, 128), 64 * 128, 3, cols >= kX3LongK ? r64x128_long : r64x128),
                          x3_estimate(tiles(64, 64), 64 * 64, 4, r64),
-                         paired ? 1e300 : x3_estimate(tiles(128, 192), 128 * 192, 1, r192)};
+                         paired ? 1e300 : x3_estimate(tiles(128, 192), 128 * 192, 1, r192),
+                         cols >= kX3LongK ? x3_estimate(tiles(64, 128), 64 * 128, 1, r64x128_split) : 1e300};
     int best = 0;
-    for (int i = 1; i < 4; ++i)
+    for (int i = 1; i < 5; ++i)
         if (e[i] < e[best]) best = i;
     return static_cast<X3Shape>(best);
 }
 
 // One launch of gemm_x3_kernel over count A rows (pol.count) and `rows`
 // weight rows, on a 1-D grid (Policy::kLinearGrid) of all tiles.
-template <uint32_t QT, int WM, int WN, int SM, int SN, int PF, bool CF, class P>
+template <uint32_t QT, int WM, int WN, int SM, int SN, int PF, bool CF, class P, int KS = 1>
 int launch_x3_tiles(P pol, int rows, int count, int cols, hipStream_t stream) {
     constexpr int BM = WM * SM * 16, BN = WN * SN * 16;
     pol.tiles_x = (rows + BN - 1) / BN;
     const long long tiles = static_cast<long long>(pol.tiles_x) * ((count + BM - 1) / BM);
     if (tiles > 0x7fffffffLL) return Q3X_HIP_EINVAL;
-    hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, P, PF, CF>), dim3(static_cast<unsigned>(tiles)),
-                       dim3(WM * WN * kWave), 0, stream, pol, rows, cols);
+    hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, P, PF, CF, KS>), dim3(static_cast<unsigned>(tiles)),
+                       dim3(KS * WM * WN * kWave), 0, stream, pol, rows, cols);
     return launch_status();
 }
 
@@ -367,6 +415,8 @@ int launch_x3(const P& pol, int rows, int count, int cols, hipStream_t stream) {
                 return launch_x3_tiles<QT, 2, 4, 4, 3, 1, false>(pol, rows, count, cols, stream);
             else
                 return launch_x3_tiles<QT, 2, 4, 4, 4, 1, true>(pol, rows, count, cols, stream);
+        case X3Shape::k64x128_split:
+            return launch_x3_tiles<QT, 2, 4, 2, 2, 1, false, P, 2>(pol, rows, count, cols, stream);
         case X3Shape::k64x128:
             if (cols >= kX3LongK) return launch_x3_tiles<QT, 2, 4, 2, 2, 2, false>(pol, rows, count, cols, stream);
             return launch_x3_tiles<QT, 2, 4, 2, 2, 1, false>(pol, rows, count, cols, stream);

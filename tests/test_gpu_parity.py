@@ -324,7 +324,9 @@ GEMM_CASES = [(Q8_0, 64, 128, 1), (Q8_0, 130, 256, 5), (Q8_0, 300, 512, 129), (Q
               # 128x128-tile path (>= 512 workgroups), partial tiles on both edges
               (Q8_0, 4096, 512, 2048), (Q4_0, 4000, 256, 2100),
               # 128x192 tiles (one per CU), whole and partial on both edges
-              (Q8_0, 12288, 256, 512), (Q4_0, 12000, 128, 500)]
+              (Q8_0, 12288, 256, 512), (Q4_0, 12000, 128, 500),
+              # 64x128 tiles with the K blocks in two halves (long K, <= 256 tiles), odd block count
+              (Q8_0, 3300, 8224, 300)]
 
 
 @pytest.mark.parametrize("type_,rows,cols,count", GEMM_CASES)
@@ -356,10 +358,12 @@ def test_gemm_parity(type_, rows, cols, count):
 # dropped split part errs by 2^8 ulp or more, and a mispaired activation and
 # weight chunk or a misplaced tile by an unrelated value.  x spans 2^-90 ..
 # 2^90.  The shapes take each tile shape of the launch (128 x 256, 128 x 192,
-# 64 x 128 with one and two stages ahead, 64 x 64) and partial tiles.
+# 64 x 128 with one and two stages ahead and with the K blocks in two
+# halves -- an even and an odd block count -- and 64 x 64) and partial tiles.
 ONE_PRODUCT_CASES = [(Q8_0, 4096, 256, 2048), (Q4_0, 4096, 320, 2048), (Q8_0, 4096, 8192, 512),
                      (Q4_0, 2048, 1024, 1024), (Q8_0, 257, 512, 300), (Q4_0, 100, 96, 7),
-                     (Q8_0, 12288, 128, 512), (Q4_0, 11999, 96, 500)]
+                     (Q8_0, 12288, 128, 512), (Q4_0, 11999, 96, 500), (Q4_0, 4096, 8192, 1024),
+                     (Q4_0, 4096, 8224, 500)]
 
 
 def _one_product_matrix(rng, type_, rows, cols):
