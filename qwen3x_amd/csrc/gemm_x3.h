@@ -380,7 +380,7 @@ inline X3Shape x3_shape(int rows, int count, int cols, bool paired = false) {
     static constexpr double r64x128[] = {210.0, 240.0, 260.0};
     static constexpr double r64x128_long[] = {215.0, 290.0, 300.0};  // two stages ahead, K >= kX3LongK
     static constexpr double r64[] = {150.0, 190.0, 215.0, 230.0};
-    static constexpr double r192[] = {330.0};
+    static constexpr double r192[] = {300.0};
     static constexpr double r64x128_split[] = {240.0};  // K halves on 16 waves, one workgroup per CU
     const double e[5] = {x3_estimate(tiles(128, 256), 128 * 256, 1, r256),
                          x3_estimate(tiles(64, 128), 64 * 128, 3, cols >= kX3LongK ? r64x128_long : r64x128),
