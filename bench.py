@@ -206,9 +206,17 @@ def headline(torch, q3x, wl, steps, warmup):
     set_ms = statistics.median(time_graph(torch, lambda i: step.run_layer(layer_sets[i % n_layer]), 4 * n_layer, 5)
                                for _ in range(5))
     step.reset()
+    # The same launches as plain reads of the same weight bytes (q|k|v,
+    # o, gate|up, down): what the box reaches at these sizes with no work.
+    by = {m.name: m.nbytes for m in layer}
+    read_us = plain_read_us(torch, q3x, [by["q"] + by["k"] + by["v"], by["o"], by["gate"] + by["up"], by["down"]],
+                            n_layer, graph=True)
     layer_set = {"us": round(set_ms * 1e3, 2), "bytes": set_bytes,
                  "GBps": round(set_bytes / (set_ms * 1e-3) / 1e9, 1),
-                 "frac_of_hbm_peak": round(set_bytes / (set_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                 "frac_of_hbm_peak": round(set_bytes / (set_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                 "plain_read_us": round(read_us, 2),
+                 "note": "plain_read_us: the four launches' weight bytes read by q3x_hip_read_probe "
+                         "(no work on the data), replayed the same way"}
     return {
         "layer_set": layer_set,
         "per_launch": per_launch,
@@ -265,6 +273,36 @@ def time_graph(torch, fn, calls, replays, warmup=2):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / (replays * calls)
+
+
+def plain_read_us(torch, q3x, sizes, copies, graph):
+    """Microseconds per round of plain streaming reads (q3x_hip_read_probe:
+    every byte once, no work on the data) of buffers of the given byte
+    sizes, one launch per size, over `copies` rotating sets -- the read rate
+    this box reaches at the matvecs' sizes.  graph: replayed from a graph
+    like the matvec it stands beside, else back to back on the stream."""
+    sizes = [(b + 15) // 16 * 16 for b in sizes]
+    bufs = [[torch.empty(b, dtype=torch.uint8, device="cuda") for b in sizes] for _ in range(copies)]
+    sink = torch.zeros(4, dtype=torch.uint8, device="cuda")
+
+    def run(i):
+        for b in bufs[i % copies]:
+            q3x.read_probe(b, sink)
+    if graph:
+        ms = statistics.median(time_graph(torch, run, 4 * copies, 5) for _ in range(3))
+    else:
+        for i in range(2 * copies):
+            run(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(8 * copies):
+            run(i)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / (8 * copies)
+    del bufs
+    return ms * 1e3
 
 
 def cpu_median(fn, seconds, max_reps=25):
@@ -329,7 +367,8 @@ def extra_configs(torch, q3x, wl, only=None, cpu=False):
         x = wl.activations(0, 1, 4096)[0].contiguous()
         y = torch.empty(4096, dtype=torch.float32, device="cuda")
         ms = time_graph(torch, lambda i: q3x.mv(q3x.Linear(ws[i % n], 4096, 4096, m.type), x, y), 4 * n, 20)
-        out["cfg0_q8_mv_4096"] = {"GBps": mv_bytes(m) / (ms * 1e-3) / 1e9, "us": ms * 1e3, "copies": n}
+        out["cfg0_q8_mv_4096"] = {"GBps": mv_bytes(m) / (ms * 1e-3) / 1e9, "us": ms * 1e3, "copies": n,
+                                  "plain_read_us": plain_read_us(torch, q3x, [m.nbytes], n, graph=True)}
         if ref_cpu:
             t, reps = cpu_matvecs(ref_cpu, [m], 1.0)
             out["cfg0_q8_mv_4096"]["cpu_baseline"] = ref_cpu.entry(
@@ -393,9 +432,14 @@ def extra_configs(torch, q3x, wl, only=None, cpu=False):
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / (8 * n)
         alg = sum(mv_bytes(mm) for mm in mats) - 4 * 5120  # gate|up read x once
+        by = {mm.name: mm.nbytes for mm in mats}
+        read_us = plain_read_us(torch, q3x, [by["gate"] + by["up"], by["down"]], n, graph=False)
         out["cfg3_q4_mv_27b_ffn"] = {"GBps": alg / (ms * 1e-3) / 1e9, "us": ms * 1e3, "copies": n,
                                      "us_graph": ms_graph * 1e3,
-                                     "GBps_graph": alg / (ms_graph * 1e-3) / 1e9}
+                                     "GBps_graph": alg / (ms_graph * 1e-3) / 1e9,
+                                     "plain_read_us": read_us,
+                                     "note": "plain_read_us: gate|up and down weight bytes read by "
+                                             "q3x_hip_read_probe (no work on the data), back to back as above"}
         del sets
         X = wl.activations(3, 512, 5120)
         H = wl.activations(3, 512, 17408, salt=1)

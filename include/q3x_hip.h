@@ -229,6 +229,15 @@ int q3x_hip_quantize(uint32_t type, const float* src, int rows, int cols, void* 
 int q3x_hip_quantize_bf16(uint32_t type, const uint16_t* src, int rows, int cols, void* dst,
                           hipStream_t stream);
 
+/* A plain streaming read of bytes (16-byte aligned, a multiple of 16) of
+ * device memory, as fast as this library reads HBM without any work on the
+ * data: non-temporal 16-byte loads over 512 workgroups of 1024 threads.  No
+ * counterpart in the reference; bench.py times it over the same weight
+ * bytes as each decode matvec, so every matvec figure sits beside the read
+ * rate the box reaches at that size.  *sink (4 bytes of device memory) is
+ * written only on a 1-in-2^32 pattern of the data's XOR. */
+int q3x_hip_read_probe(const void* buffer, size_t bytes, uint32_t* sink, hipStream_t stream);
+
 /* ------------------------------------------------------------------------
  * model.bin -- the weight file the matmuls read (reference model_config.h,
  * engine.cpp:455-559, arch/cuda/engine.cu:2007-2188, written by

@@ -64,6 +64,7 @@ SIGNATURES = {
     "q3x_hip_moe_layer_workspace_bytes": (_S, [_P, _I]),
     "q3x_hip_moe_layer": (_I, [_P, _P, _I, _P, _P, _P, _P, _S, _P]),
     "q3x_hip_quantize_bf16": (_I, [_U, _P, _I, _I, _P, _P]),
+    "q3x_hip_read_probe": (_I, [_P, _S, _P, _P]),
     "q3x_hip_model_layout": (_I, [_P, _S, ctypes.c_uint64, _P, _P, _S, ctypes.POINTER(_S),
                                   ctypes.POINTER(ctypes.c_char_p)]),
     "q3x_hip_model_load": (_I, [ctypes.c_char_p, ctypes.POINTER(_P), ctypes.POINTER(ctypes.c_char_p)]),
@@ -386,6 +387,14 @@ def quantize_bf16(type_: int, src, rows: int, cols: int, dst, stream=None):
     _check("q3x_hip_quantize_bf16",
            lib().q3x_hip_quantize_bf16(type_, _ptr(src), rows, cols, _ptr(dst), _stream(stream)))
     return dst
+
+
+def read_probe(buffer, sink, stream=None):
+    """A plain streaming read of the device tensor `buffer` (no work on the
+    data); sink: a device tensor of at least 4 bytes."""
+    _need_device(buffer, sink)
+    nbytes = buffer.numel() * buffer.element_size()
+    _check("q3x_hip_read_probe", lib().q3x_hip_read_probe(_ptr(buffer), nbytes, _ptr(sink), _stream(stream)))
 
 
 # ---------------------------------------------------------------- model.bin

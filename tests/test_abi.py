@@ -71,6 +71,10 @@ def test_invalid_arguments_are_rejected_without_device_work():
     assert lib.q3x_hip_gemm(P, 0, 4, 64, P, 3, P, 0, N) == q3x.ENOTSUP
     assert lib.q3x_hip_dequant(P, 1, 64, -1, 1, P, N) == q3x.EINVAL
     assert lib.q3x_hip_dequant(P, 2, 64, 0, 0, P, N) == q3x.EINVAL
+    assert lib.q3x_hip_read_probe(N, 16, P, N) == q3x.EINVAL
+    assert lib.q3x_hip_read_probe(P, 24, P, N) == q3x.EINVAL                   # not a multiple of 16
+    assert lib.q3x_hip_read_probe(ctypes.c_void_p(0x1008), 32, P, N) == q3x.EINVAL  # not 16-byte aligned
+    assert lib.q3x_hip_read_probe(P, 0, P, N) == q3x.EINVAL
     assert lib.q3x_hip_router_topk(P, 1, 256, 9, P, P, N) == q3x.EINVAL       # top_k > 8
     assert lib.q3x_hip_router_topk(P, 1, 4, 5, P, P, N) == q3x.EINVAL         # top_k > experts
     assert lib.q3x_hip_router_topk(P, 1, 2048, 8, P, P, N) == q3x.EINVAL      # experts > 1024
