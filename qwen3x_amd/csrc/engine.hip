@@ -133,7 +133,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_kernel(float* __restrict__ h
 // before its run (the previous run's last rows, or the remembered history for
 // the first tokens); after one barrier the runs are convolved in place and
 // the thread holding the last token leaves the last CK - 1 raw inputs as the
-// new history.  The arithmetic per token is the reference's (conv_token).
+// new history.  The arithmetic per token is the reference's (conv_apply).
 // The history is kept in two copies, [2][channels][CK - 1]: a forward at
 // position p reads copy p % 2 and leaves copy (p + count) % 2, so a decode
 // step (delta_step_kernel, which convolves its own channels) can read the
@@ -203,32 +203,12 @@ __global__ __launch_bounds__(kConvThreads) void delta_conv_kernel(float* __restr
 }
 
 // One token of the causal conv of one channel, then SiLU (the arithmetic of
-// delta_conv_kernel): the CK - 1 remembered inputs from `hist`, the weights
-// w[0 .. CK - 1] (BF16); the shifted history goes to `hist_out` if not null.
-__device__ __forceinline__ float conv_token(float x, const float* hist, const uint16_t* w, int CK, float* hist_out) {
-    float past[kMaxConv - 1];
-#pragma unroll
-    for (int i = 0; i < kMaxConv - 1; ++i) past[i] = i < CK - 1 ? hist[i] : 0.0f;
-    float last = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kMaxConv; ++i)
-        if (i == CK - 1) last = bf16_value(w[i]);
-    float sum = x * last;
-#pragma unroll
-    for (int i = 0; i < kMaxConv - 1; ++i)
-        if (i < CK - 1) sum = fmaf(past[i], bf16_value(w[i]), sum);
-    if (hist_out) {
-#pragma unroll
-        for (int i = 0; i < kMaxConv - 1; ++i)
-            if (i < CK - 1) hist_out[i] = i + 1 < CK - 1 ? past[i + 1] : x;
-    }
-    return silu_ref(sum);
-}
-
-// conv_token in two halves, so that a decode step can request every input
-// before it knows the position: conv_fetch loads the channel's input, both
-// history copies and the weights; conv_apply picks the copy by position
-// parity and runs conv_token's arithmetic in the same order.
+// delta_conv_kernel: sum = x * w[CK - 1], then sum = fma(past[i], w[i], sum)
+// for the CK - 1 remembered inputs, weights BF16), in two halves so that a
+// decode step can request every input before it knows the position:
+// conv_fetch loads the channel's input, both history copies and the
+// weights; conv_apply picks the copy by position parity, convolves, and
+// leaves the shifted history in `hist_out` if not null.
 struct ConvInputs {
     float x;
     float past[2][kMaxConv - 1];
@@ -457,7 +437,7 @@ __global__ __launch_bounds__(kScanThreads) void delta_scan_kernel(const float* _
 // workgroups of 4 waves, lane l of wave w owning column 32 slice + 8 w + l / 8
 // and keys 16 (l % 8) .. + 15, the sums over keys DPP adds inside row halves,
 // and the scan's arithmetic per token (k S once scaled by e^decay, S e^decay +
-// k (beta delta), q S).  The token's causal conv runs here too (conv_token):
+// k (beta delta), q S).  The token's causal conv runs here too (conv_fetch, conv_apply):
 // thread t convolves q channel t (t < 128) or k channel t - 128 of the key
 // head and the first kScanCols threads the slice's v channels, from history
 // copy p % 2 into copy (p + 1) % 2 -- q and k only from slice 0 of the key
@@ -999,27 +979,34 @@ __global__ __launch_bounds__(256) void swiglu_kernel(float* __restrict__ gate, c
     if (i < n) gate[i] = silu_ref(gate[i]) * up[i];
 }
 
+// gate = gate * up in place, for a gate that already holds silu(gate): the
+// second half of swiglu_kernel's arithmetic.
+__global__ __launch_bounds__(256) void product_kernel(float* __restrict__ gate, const float* __restrict__ up, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) gate[i] = gate[i] * up[i];
+}
+
 // Element i of x in the matvec kernels' padded LDS copy.
 __device__ __forceinline__ float* lds_x(uint8_t* xl, int i) {
     return reinterpret_cast<float*>(xl + x_block_offset(i / kBlock) + 4 * (i % kBlock));
 }
 
 // Input staging for a decode step's down projection: x = silu(gate) * up
-// (engine.cpp:371-376; swiglu_kernel's arithmetic) formed on the way into
-// LDS from the gate|up matvec's two outputs.
+// (engine.cpp:371-376; swiglu_kernel's arithmetic), where the gate|up
+// matvec has already stored silu(gate) (MultiRows::silu_mask, once per row),
+// so each workgroup forms x with one multiply per value on the way into LDS
+// -- the same two roundings as swiglu_kernel, bit for bit.  (Evaluating silu
+// here instead, in every one of the launch's workgroups, cost ~5 us per
+// launch at the 27B shape.)
 struct SwiGLUInput {
     const float* up;
-    __device__ void stage(const float* gate, uint8_t* xl, int bpr, float* /*work*/) const {
-        const f32x4* g = reinterpret_cast<const f32x4*>(gate);
+    __device__ void stage(const float* silu_gate, uint8_t* xl, int bpr, float* /*work*/) const {
+        const f32x4* g = reinterpret_cast<const f32x4*>(silu_gate);
         const f32x4* u = reinterpret_cast<const f32x4*>(up);
         for (int c = threadIdx.x; c < bpr * 8; c += blockDim.x) {
             const f32x4 a = g[c], b = u[c];
-            f32x4 h;
-            h.x = silu_ref(a.x) * b.x;
-            h.y = silu_ref(a.y) * b.y;
-            h.z = silu_ref(a.z) * b.z;
-            h.w = silu_ref(a.w) * b.w;
-            *reinterpret_cast<f32x4*>(xl + x_block_offset(c >> 3) + 16 * (c & 7)) = h;
+            *reinterpret_cast<f32x4*>(xl + x_block_offset(c >> 3) + 16 * (c & 7)) =
+                f32x4{a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w};
         }
         __syncthreads();
     }
@@ -1277,7 +1264,7 @@ int apply_group(const Mat* m, float* const* y, int n, uint32_t type, int cols, c
 // separate kernels.
 template <class In>
 int mv_staged(const Mat* m, float* const* y, const bool* add, int n, uint32_t type, int cols, const float* x,
-              const In& in, hipStream_t s) {
+              const In& in, hipStream_t s, uint32_t silu_mask = 0) {
     const int bpr = cols / kBlock;
     const size_t row_bytes = static_cast<size_t>(bpr) * block_bytes(type);
     if (row_bytes % 16 != 0 || !aligned(x, 16) || n < 1 || n > MultiRows::kMax) return Q3X_HIP_ENOTSUP;
@@ -1285,6 +1272,7 @@ int mv_staged(const Mat* m, float* const* y, const bool* add, int n, uint32_t ty
     map.count = n;
     map.row_bytes = row_bytes;
     map.x = x;
+    map.silu_mask = silu_mask;
     int total = 0;
     for (int i = 0; i < n; ++i) {
         if (!aligned(m[i].w, 16) || m[i].cols != cols) return Q3X_HIP_ENOTSUP;
@@ -1405,9 +1393,12 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
         } else {
             const Mat gate_up[2] = {L.gate, L.up};
             float* const ffn[2] = {e.ffn_gate, e.ffn_up};
+            // A decode step stores silu(gate) (matrix 0) for the down
+            // launch's SwiGLUInput.
             rc = step && aligned(L.post_norm, 8)
-                     ? mv_staged(gate_up, ffn, no_add, 2, type, c.H, e.hidden, NormInput{L.post_norm}, s)
+                     ? mv_staged(gate_up, ffn, no_add, 2, type, c.H, e.hidden, NormInput{L.post_norm}, s, 1u)
                      : Q3X_HIP_ENOTSUP;
+            const bool silu_stored = rc == Q3X_HIP_OK;
             if (rc == Q3X_HIP_ENOTSUP) {
                 hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden, nullptr,
                                    L.post_norm, c.H, e.normalized);
@@ -1416,11 +1407,14 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
             if (rc) break;
             const bool add = true;
             float* const residual = e.hidden;
-            rc = step ? mv_staged(&L.down, &residual, &add, 1, type, c.I, e.ffn_gate, SwiGLUInput{e.ffn_up}, s)
-                      : Q3X_HIP_ENOTSUP;
+            rc = silu_stored ? mv_staged(&L.down, &residual, &add, 1, type, c.I, e.ffn_gate, SwiGLUInput{e.ffn_up}, s)
+                             : Q3X_HIP_ENOTSUP;
             if (rc == Q3X_HIP_ENOTSUP) {
                 const int n = count * c.I;
-                hipLaunchKernelGGL(swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, s, e.ffn_gate, e.ffn_up, n);
+                if (silu_stored)  // silu(gate) already: x = gate * up
+                    hipLaunchKernelGGL(product_kernel, dim3((n + 255) / 256), dim3(256), 0, s, e.ffn_gate, e.ffn_up, n);
+                else
+                    hipLaunchKernelGGL(swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, s, e.ffn_gate, e.ffn_up, n);
                 rc = apply(L.down, type, e.ffn_gate, count, e.hidden, true, s);
             }
             pending = false;

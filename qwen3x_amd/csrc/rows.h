@@ -47,11 +47,12 @@ struct OneMatrix {
     float* y;
     bool accumulate;
     const uint8_t* any_w;  // a valid address for empty buffer ranges
+    bool silu = false;     // store silu(v) (the gate half of a decode step's SwiGLU)
     __device__ const uint8_t* row(int r) const { return w ? w + static_cast<size_t>(r) * row_bytes : nullptr; }
     __device__ const uint8_t* any() const { return any_w; }
     __device__ const float* input(int) const { return x; }
     __device__ float previous(int r) const { return accumulate ? y[r] : 0.0f; }
-    __device__ void store(int r, float v) const { y[r] = v; }
+    __device__ void store(int r, float v) const { y[r] = silu ? silu_ref(v) : v; }
 };
 
 // Up to Q3X_HIP_MV_MULTI_MAX matrices of one type and width that read the
@@ -68,6 +69,11 @@ struct MultiRows {
     int wave_end[kMax];
     int count;
     uint32_t accumulate_mask;
+    // Matrices whose rows store silu(W x) instead of W x: a decode step's
+    // gate, so that the down projection's input staging forms
+    // silu(gate) * up with one multiply per value instead of every
+    // workgroup evaluating silu over the whole row (engine.cpp:371-376).
+    uint32_t silu_mask = 0;
     size_t row_bytes;
     const float* x;
 
@@ -132,7 +138,7 @@ struct MultiRows {
         gw -= first_wave;
         GW = last_wave - first_wave;
         nrows = last_row - first_row;
-        return OneMatrix{wk, row_bytes, x, yk, ((accumulate_mask >> k) & 1u) != 0, wk};
+        return OneMatrix{wk, row_bytes, x, yk, ((accumulate_mask >> k) & 1u) != 0, wk, ((silu_mask >> k) & 1u) != 0};
     }
 };
 
