@@ -686,7 +686,7 @@ __device__ __forceinline__ float bf16_value(uint16_t v) { return __uint_as_float
 struct NormInput {
     static constexpr int kHeld = 4;
     const uint16_t* w;
-    __device__ void stage(const float* x, uint8_t* xl, int bpr, float* /*work*/) const {
+    __device__ void stage(const float* x, uint8_t* xl, int bpr, float* work) const {
         const int chunks = bpr * 8;
         const int B = blockDim.x;
         const f32x4* xs = reinterpret_cast<const f32x4*>(x);
@@ -709,17 +709,25 @@ struct NormInput {
         }
         for (int c = threadIdx.x + kHeld * B; c < chunks; c += B) *at(c) = xs[c];
         __syncthreads();
-        float square = 0.0f;
-        for (int c = threadIdx.x % kWave; c < chunks; c += kWave) {
-            const f32x4 v = *at(c);
-            square = fmaf(v.x, v.x, square);
-            square = fmaf(v.y, v.y, square);
-            square = fmaf(v.z, v.z, square);
-            square = fmaf(v.w, v.w, square);
+        // Wave 0 alone sums the squares (one fixed order: lane l takes
+        // chunks l, l + 64, ... with FMAs, then the wave's DPP tree, so the
+        // scale is the same in every workgroup whatever the launch shape)
+        // and hands the scale to the other waves through LDS; it used to be
+        // every wave reading all of h, 16 times the LDS traffic.
+        if (threadIdx.x < kWave) {
+            float square = 0.0f;
+            for (int c = threadIdx.x; c < chunks; c += kWave) {
+                const f32x4 v = *at(c);
+                square = fmaf(v.x, v.x, square);
+                square = fmaf(v.y, v.y, square);
+                square = fmaf(v.z, v.z, square);
+                square = fmaf(v.w, v.w, square);
+            }
+            const float total = wave_sum_f32(square);
+            if (threadIdx.x == 0) work[0] = 1.0f / sqrtf(total / static_cast<float>(bpr * kBlock) + kEps);
         }
-        const float total = wave_sum_f32(square);
-        const float scale = 1.0f / sqrtf(total / static_cast<float>(bpr * kBlock) + kEps);
-        __syncthreads();  // every wave's reads of h precede the scaled writes
+        __syncthreads();  // the scale is in LDS; every read of h for it precedes the scaled writes
+        const float scale = work[0];
         auto put = [&](int c, f32x4 v, uint2 q) {
             v.x = v.x * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.x)));
             v.y = v.y * scale * (1.0f + bf16_value(static_cast<uint16_t>(q.x >> 16)));
