@@ -30,6 +30,7 @@
 
 #include <algorithm>
 #include <new>
+#include <type_traits>
 #include <vector>
 
 #include "common.h"
@@ -617,31 +618,74 @@ __global__ __launch_bounds__(kHeadThreads) void attention_prep_kernel(
     }
 }
 
+// Sum over the 64 lanes of each of 64 values: afterwards lane L holds the
+// total of value L.  Six exchange levels, one per lane-index bit from the top:
+// at each, a lane keeps the half of its values that its bit selects (the upper
+// half when the bit is set) and adds its partner's copy of that half, so the
+// levels move 32 + 16 + 8 + 4 + 2 + 1 values instead of 64 full reductions.
+// Bits 5 and 4 pair lanes L and L ^ 32 / L ^ 16 by the gfx950 lane swaps
+// (v_permlane32_swap, v_permlane16_swap); bits 3 .. 0 by DPP (row_mirror,
+// row_half_mirror, then the two quad permutations), whose partners differ
+// from the lane in the level's bit and agree in every bit above it.
+__device__ __forceinline__ float transpose_sum64(float (&v)[64]) {
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 32]), false, false);
+        v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 16]), false, false);
+        v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const int lane = threadIdx.x & (kWave - 1);
+    auto level = [&](auto ctrl, int half, bool upper) {
+#pragma unroll
+        for (int k = 0; k < half; ++k) {
+            const float keep = upper ? v[k + half] : v[k];
+            const float send = upper ? v[k] : v[k + half];
+            v[k] = keep + dpp_f32<decltype(ctrl)::value>(send);
+        }
+    };
+    level(std::integral_constant<int, 0x140>{}, 8, (lane & 8) != 0);
+    level(std::integral_constant<int, 0x141>{}, 4, (lane & 4) != 0);
+    level(std::integral_constant<int, 0x4E>{}, 2, (lane & 2) != 0);
+    level(std::integral_constant<int, 0xB1>{}, 1, (lane & 1) != 0);
+    return v[0];
+}
+
 // Decode attention of the query row at *position for the G = AH / KVH query
 // heads that share KV head blockIdx.x / splits (engine.cpp:344-361: scores
 // q . k / sqrt(AD), softmax, sum of weights times v), over position range
-// blockIdx.x % splits of 0 .. *position.  A range is taken in blocks of 64
-// positions, every K and V load of a block requested at once (wave w holds
-// the key rows of positions w, w + 4, ... of the block, lane l elements 4l ..
-// 4l + 3; thread i holds value element i of every position), each K and V row
-// loaded once for all G heads.  Scores leave each wave's DPP sum for LDS;
-// wave w then runs the online softmax of heads w, w + 4 with wave reductions
-// (a running maximum rescales the running sum and accumulators), so no score
-// buffer bounds the context.  Each head's range maximum, sum and accumulator
-// go to `partial` for attention_combine_kernel (empty ranges leave m = -inf,
-// l = 0).  AD <= 256 and a multiple of 4, G <= kMaxGroup.
+// blockIdx.x % splits of 0 .. *position.  A range is taken in blocks of
+// B = 4 * 64 / GP positions (GP = G rounded up to 4 or 8): wave w holds the K
+// and V rows of positions w, w + 4, ... of a block, lane l elements 4l .. 4l +
+// 3 of each, every load of a block requested at once and each row loaded once
+// for all G heads.  The lane products q_g . k_u of a wave's 64 (row, head)
+// pairs reduce together in transpose_sum64; the scores go to LDS, where wave
+// w runs the online softmax of heads w, w + 4 with wave reductions (a running
+// maximum rescales the running sum and accumulators), so no score buffer
+// bounds the context.  Each wave accumulates weight times v over its own rows
+// (four outputs per lane per head); the four waves' accumulators add in wave
+// order at the end.  Each head's range maximum, sum and accumulator go to
+// `partial` for attention_combine_kernel (empty ranges leave m = -inf, l = 0).
+// AD <= 256 and a multiple of 4, G <= kMaxGroup.
 constexpr int kAttnSplits = 128;  // ranges per KV head for a decode step
-constexpr int kAttnBlock = 64;
 constexpr int kMaxGroup = 8;
 constexpr int kChunk = 2048;     // default rows of a prefill chunk
 
+template <int GP>
 __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
     const float* __restrict__ query, const float* __restrict__ key_cache, const float* __restrict__ value_cache,
     const int* __restrict__ position, float* __restrict__ partial, int AH, int KVH, int AD, int splits) {
     constexpr int kWaves = kHeadThreads / kWave;
-    constexpr int kRows = kAttnBlock / kWaves;  // key rows per wave per block
-    __shared__ __attribute__((aligned(16))) float sc[kMaxGroup][kAttnBlock];  // scores, then weights
-    __shared__ float head_m[kMaxGroup], head_l[kMaxGroup], head_alpha[kMaxGroup];
+    static_assert(GP == 4 || GP == 8, "64 (row, head) pairs per wave");
+    constexpr int R = kWave / GP;  // rows per wave per block
+    constexpr int B = kWaves * R;  // positions per block
+    // Scores, then weights, wave-major: sc[g][w * R + u] is position u * 4 + w.
+    __shared__ __attribute__((aligned(16))) float sc[GP][B];
+    __shared__ float head_m[GP], head_l[GP], head_alpha[GP];
+    __shared__ __attribute__((aligned(16))) float red[kWaves - 1][GP][256];
     const int kv = blockIdx.x / splits, split = blockIdx.x % splits;
     const int G = AH / KVH;
     const int n = *position + 1;
@@ -649,68 +693,67 @@ __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
     const int t0 = min(n, split * per), t1 = min(n, t0 + per);
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int i = threadIdx.x;
     const size_t KVW = static_cast<size_t>(KVH) * AD;
-    const float* kbase = key_cache + static_cast<size_t>(kv) * AD;
-    const float* vbase = value_cache + static_cast<size_t>(kv) * AD;
+    const float* kbase = key_cache + static_cast<size_t>(kv) * AD + 4 * lane;
+    const float* vbase = value_cache + static_cast<size_t>(kv) * AD + 4 * lane;
     const float divisor = sqrtf(static_cast<float>(AD));
     const bool kl = 4 * lane < AD;
-    // Every K and V load of a block, requested together; the first block's
-    // go out before q is read (their addresses do not depend on it).
-    float vr[kAttnBlock];
-    f32x4 kr[kRows];
+    f32x4 kr[R], vr[R];
     auto load_block = [&](int b0) {
-        const int nb = min(kAttnBlock, t1 - b0);
+        const int nb = min(B, t1 - b0);
 #pragma unroll
-        for (int j = 0; j < kAttnBlock; ++j)
-            vr[j] = j < nb && i < AD ? vbase[static_cast<size_t>(b0 + j) * KVW + i] : 0.0f;
-#pragma unroll
-        for (int u = 0; u < kRows; ++u) {
+        for (int u = 0; u < R; ++u) {
             const int j = u * kWaves + wave;
-            kr[u] = j < nb && kl ? *reinterpret_cast<const f32x4*>(kbase + static_cast<size_t>(b0 + j) * KVW + 4 * lane)
-                                 : f32x4{0, 0, 0, 0};
+            kr[u] = j < nb && kl ? *reinterpret_cast<const f32x4*>(kbase + static_cast<size_t>(b0 + j) * KVW) : f32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+            const int j = u * kWaves + wave;
+            vr[u] = j < nb && kl ? *reinterpret_cast<const f32x4*>(vbase + static_cast<size_t>(b0 + j) * KVW) : f32x4{0, 0, 0, 0};
         }
     };
     if (t0 < t1) load_block(t0);
-    f32x4 q[kMaxGroup];
+    f32x4 q[GP];
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g)
+    for (int g = 0; g < GP; ++g)
         q[g] = g < G && kl ? *reinterpret_cast<const f32x4*>(query + (kv * G + g) * AD + 4 * lane) : f32x4{0, 0, 0, 0};
-    float acc[kMaxGroup];
+    f32x4 acc[GP];
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) acc[g] = 0.0f;
-    if (i < kMaxGroup) {
-        head_m[i] = -INFINITY;
-        head_l[i] = 0.0f;
+    for (int g = 0; g < GP; ++g) acc[g] = f32x4{0, 0, 0, 0};
+    if (threadIdx.x < GP) {
+        head_m[threadIdx.x] = -INFINITY;
+        head_l[threadIdx.x] = 0.0f;
     }
     __syncthreads();
-    for (int b0 = t0; b0 < t1; b0 += kAttnBlock) {
-        const int nb = min(kAttnBlock, t1 - b0);
+    // After transpose_sum64, lane L holds the score of row u = L / GP, head g = L % GP.
+    const int my_u = lane / GP, my_g = lane % GP;
+    for (int b0 = t0; b0 < t1; b0 += B) {
+        const int nb = min(B, t1 - b0);
         if (b0 != t0) load_block(b0);
+        float v[64];
 #pragma unroll
-        for (int u = 0; u < kRows; ++u) {
-            const int j = u * kWaves + wave;
-            if (j >= nb) break;
+        for (int u = 0; u < R; ++u) {
 #pragma unroll
-            for (int g = 0; g < kMaxGroup; ++g) {
-                if (g < G) {
-                    float x = q[g].x * kr[u].x;
-                    x = fmaf(q[g].y, kr[u].y, x);
-                    x = fmaf(q[g].z, kr[u].z, x);
-                    x = fmaf(q[g].w, kr[u].w, x);
-                    x = wave_sum_f32(x);
-                    if (lane == 0) sc[g][j] = x / divisor;
-                }
+            for (int g = 0; g < GP; ++g) {
+                float x = q[g].x * kr[u].x;
+                x = fmaf(q[g].y, kr[u].y, x);
+                x = fmaf(q[g].z, kr[u].z, x);
+                x = fmaf(q[g].w, kr[u].w, x);
+                v[u * GP + g] = x;
             }
         }
+        const float s = transpose_sum64(v);
+        sc[my_g][wave * R + my_u] = s / divisor;
         __syncthreads();
         for (int g = wave; g < G; g += kWaves) {
-            const float sj = lane < nb ? sc[g][lane] : -INFINITY;
+            // lane = w * R + u holds position u * 4 + w.
+            const bool valid = lane < B && (lane % R) * kWaves + lane / R < nb;
+            const float sj = valid ? sc[g][lane] : -INFINITY;
             const float mo = head_m[g];
             const float mn = fmaxf(mo, wave_max_f32(sj));
-            const float pj = lane < nb ? expf(sj - mn) : 0.0f;
+            const float pj = valid ? expf(sj - mn) : 0.0f;
             const float ps = wave_sum_f32(pj);
-            sc[g][lane] = pj;
+            if (lane < B) sc[g][lane] = pj;
             if (lane == 0) {
                 const float alpha = expf(mo - mn);  // 0 for the first block (mo = -inf)
                 head_alpha[g] = alpha;
@@ -719,33 +762,53 @@ __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
             }
         }
         __syncthreads();
-        if (i < AD) {
 #pragma unroll
-            for (int g = 0; g < kMaxGroup; ++g) {
-                if (g < G) {
-                    float a = acc[g] * head_alpha[g];
+        for (int g = 0; g < GP; ++g) {
+            if (g < G) {
+                const float alpha = head_alpha[g];
+                f32x4 a = {acc[g].x * alpha, acc[g].y * alpha, acc[g].z * alpha, acc[g].w * alpha};
 #pragma unroll
-                    for (int j = 0; j < kAttnBlock; j += 4) {
-                        const f32x4 w = *reinterpret_cast<const f32x4*>(&sc[g][j]);
-                        a = fmaf(w.x, vr[j + 0], a);
-                        a = fmaf(w.y, vr[j + 1], a);
-                        a = fmaf(w.z, vr[j + 2], a);
-                        a = fmaf(w.w, vr[j + 3], a);
+                for (int u0 = 0; u0 < R; u0 += 4) {
+                    const f32x4 p = *reinterpret_cast<const f32x4*>(&sc[g][wave * R + u0]);
+                    const float pw[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        a.x = fmaf(pw[d], vr[u0 + d].x, a.x);
+                        a.y = fmaf(pw[d], vr[u0 + d].y, a.y);
+                        a.z = fmaf(pw[d], vr[u0 + d].z, a.z);
+                        a.w = fmaf(pw[d], vr[u0 + d].w, a.w);
                     }
-                    acc[g] = a;
                 }
+                acc[g] = a;
             }
         }
-        __syncthreads();  // sc and the head state are rewritten by the next block
+        __syncthreads();
     }
+    // The waves' partial accumulators, summed in wave order.
+    if (wave > 0 && kl) {
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) {
-        if (g >= G) continue;
-        float* p = partial + (static_cast<size_t>(kv * G + g) * splits + split) * (AD + 2);
-        if (i < AD) p[i] = acc[g];
-        if (i == 0) {
-            p[AD] = head_m[g];
-            p[AD + 1] = head_l[g];
+        for (int g = 0; g < GP; ++g)
+            if (g < G) *reinterpret_cast<f32x4*>(&red[wave - 1][g][4 * lane]) = acc[g];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int g = 0; g < GP; ++g) {
+            if (g >= G) continue;
+            float* p = partial + (static_cast<size_t>(kv * G + g) * splits + split) * (AD + 2);
+            if (kl) {
+                f32x4 a = acc[g];
+#pragma unroll
+                for (int w = 0; w < kWaves - 1; ++w) {
+                    const f32x4 o = *reinterpret_cast<const f32x4*>(&red[w][g][4 * lane]);
+                    a.x += o.x; a.y += o.y; a.z += o.z; a.w += o.w;
+                }
+                p[4 * lane + 0] = a.x; p[4 * lane + 1] = a.y; p[4 * lane + 2] = a.z; p[4 * lane + 3] = a.w;
+            }
+            if (lane == 0) {
+                p[AD] = head_m[g];
+                p[AD + 1] = head_l[g];
+            }
         }
     }
 }
@@ -940,18 +1003,28 @@ __global__ __launch_bounds__(kFlashWaves * kWave, 1) void attention_prefill_kern
 }
 
 // out = (sum_s exp(m_s - M) acc_s) / (sum_s exp(m_s - M) l_s) * sigmoid(gate)
-// over the kAttnSplits ranges s of head blockIdx.x of row r = blockIdx.y, M
-// their largest maximum (empty ranges have m = -inf and weight 0).
+// over the kAttnSplits ranges s of head blockIdx.x of row r = blockIdx.z, M
+// their largest maximum (empty ranges have m = -inf and weight 0).  A
+// workgroup takes kCombCols output elements (blockIdx.y): thread t sums
+// ranges (t / kCombCols) * kPer .. + kPer of element t % kCombCols, every load
+// requested at once, and the groups' sums add in group order.
+constexpr int kCombCols = 32;
 __global__ __launch_bounds__(kHeadThreads) void attention_combine_kernel(const float* __restrict__ partial,
-                                                                         const float* __restrict__ gate,
-                                                                         float* __restrict__ out, int AH, int AD) {
-    static_assert(kAttnSplits % kWave == 0, "ranges in whole waves");
+                                                           const float* __restrict__ gate,
+                                                           float* __restrict__ out, int AH, int AD) {
+    constexpr int kGroups = kHeadThreads / kCombCols;
+    constexpr int kPer = kAttnSplits / kGroups;
+    static_assert(kAttnSplits % kGroups == 0 && kAttnSplits <= kHeadThreads, "whole groups of ranges");
     __shared__ float w[kAttnSplits], red[kHeadThreads / kWave];
+    __shared__ float part[kGroups][kCombCols];
     __shared__ float total;
-    const int head = blockIdx.x, r = blockIdx.y;
+    const int head = blockIdx.x, r = blockIdx.z;
     const float* p = partial + (static_cast<size_t>(r) * AH + head) * kAttnSplits * (AD + 2);
     const int t = threadIdx.x;
-    // Range weights: the maximum over all ranges, then exp(m_s - M).
+    const int e = blockIdx.y * kCombCols + t % kCombCols, grp = t / kCombCols;
+    float v[kPer];
+#pragma unroll
+    for (int s = 0; s < kPer; ++s) v[s] = e < AD ? p[(grp * kPer + s) * (AD + 2) + e] : 0.0f;
     const float m = t < kAttnSplits ? p[t * (AD + 2) + AD] : -INFINITY;
     const float M = block_max<kHeadThreads>(m, red);
     const float ws = t < kAttnSplits && m != -INFINITY ? expf(m - M) : 0.0f;
@@ -959,20 +1032,19 @@ __global__ __launch_bounds__(kHeadThreads) void attention_combine_kernel(const f
     const float L = block_sum<kHeadThreads>(t < kAttnSplits ? ws * p[t * (AD + 2) + AD + 1] : 0.0f, red);
     if (t == 0) total = L;
     __syncthreads();
-    const int AS = AH * AD;
-    for (int i = t; i < AD; i += kHeadThreads) {
-        // Every range's accumulator requested at once, then summed in order.
-        float v[kAttnSplits];
+    float acc = 0.0f;
 #pragma unroll
-        for (int s = 0; s < kAttnSplits; ++s) v[s] = p[s * (AD + 2) + i];
-        float acc = 0.0f;
+    for (int s = 0; s < kPer; ++s) acc = fmaf(w[grp * kPer + s], v[s], acc);
+    part[grp][t % kCombCols] = acc;
+    __syncthreads();
+    if (t < kCombCols && e < AD) {
+        float a = part[0][t];
 #pragma unroll
-        for (int s = 0; s < kAttnSplits; ++s) acc = fmaf(w[s], v[s], acc);
-        const size_t at = static_cast<size_t>(r) * AS + head * AD + i;
-        out[at] = acc / total * sigmoid_ref(gate[at]);
+        for (int g2 = 1; g2 < kGroups; ++g2) a += part[g2][t];
+        const size_t at = static_cast<size_t>(r) * AH * AD + head * AD + e;
+        out[at] = a / total * sigmoid_ref(gate[at]);
     }
 }
-
 // h = silu(gate) * up (engine.cpp:371-376), in place in gate.
 __global__ __launch_bounds__(256) void swiglu_kernel(float* __restrict__ gate, const float* __restrict__ up, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1364,11 +1436,12 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                                e.query_and_gate, e.key, e.value, L.qnorm, L.knorm, e.d_position, e.query, e.gate,
                                L.key_cache, L.value_cache, c.AH, c.KVH, c.AD, c.RD);
             if (count == 1) {
-                hipLaunchKernelGGL(attention_kernel, dim3(c.KVH * kAttnSplits), dim3(kHeadThreads), 0, s, e.query,
+                auto attend = c.AH / c.KVH <= 4 ? attention_kernel<4> : attention_kernel<8>;
+                hipLaunchKernelGGL(attend, dim3(c.KVH * kAttnSplits), dim3(kHeadThreads), 0, s, e.query,
                                    L.key_cache, L.value_cache, e.d_position, e.scores, c.AH, c.KVH, c.AD,
                                    kAttnSplits);
-                hipLaunchKernelGGL(attention_combine_kernel, dim3(c.AH, 1), dim3(kHeadThreads), 0, s, e.scores,
-                                   e.gate, e.attn_out, c.AH, c.AD);
+                hipLaunchKernelGGL(attention_combine_kernel, dim3(c.AH, (c.AD + kCombCols - 1) / kCombCols, 1),
+                                   dim3(kHeadThreads), 0, s, e.scores, e.gate, e.attn_out, c.AH, c.AD);
             } else {
                 const int subs = (c.AH / c.KVH + kFlashWaves - 1) / kFlashWaves;
                 hipLaunchKernelGGL(attention_prefill_kernel, dim3(c.KVH * subs, (count + kFlashQ - 1) / kFlashQ),
