@@ -678,11 +678,11 @@ __device__ __forceinline__ float bf16_value(uint16_t v) { return __uint_as_float
 // formed by every workgroup of the matvec launch on its way into LDS.  Each
 // thread loads its 16-byte chunks of h together with their four norm
 // weights (one round trip; the first kHeld chunks stay in registers) and
-// copies h to LDS; after one barrier every wave sums the squares of all of
-// h from LDS in the same fixed order (lane l takes chunks l, l + 64, ...
-// with FMAs, then the wave's DPP tree), so every wave of every workgroup --
-// whatever the launch shape -- holds the same scale; then each thread
-// scales its own chunks.  Requires w 8-byte aligned.
+// copies h to LDS; after one barrier wave 0 sums the squares of all of h
+// from LDS in one fixed order (lane l takes chunks l, l + 64, ... with FMAs,
+// then the wave's DPP tree), so every workgroup -- whatever the launch shape
+// -- forms the same scale, and hands it to the other waves through LDS; then
+// each thread scales its own chunks.  Requires w 8-byte aligned.
 struct NormInput {
     static constexpr int kHeld = 4;
     const uint16_t* w;
@@ -709,11 +709,9 @@ struct NormInput {
         }
         for (int c = threadIdx.x + kHeld * B; c < chunks; c += B) *at(c) = xs[c];
         __syncthreads();
-        // Wave 0 alone sums the squares (one fixed order: lane l takes
-        // chunks l, l + 64, ... with FMAs, then the wave's DPP tree, so the
-        // scale is the same in every workgroup whatever the launch shape)
-        // and hands the scale to the other waves through LDS; it used to be
-        // every wave reading all of h, 16 times the LDS traffic.
+        // Wave 0 alone sums the squares and hands the scale to the other
+        // waves through LDS (a sum in every wave would read all of h from
+        // LDS 16 times over).
         if (threadIdx.x < kWave) {
             float square = 0.0f;
             for (int c = threadIdx.x; c < chunks; c += kWave) {
