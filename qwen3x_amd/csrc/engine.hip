@@ -618,25 +618,20 @@ __global__ __launch_bounds__(kHeadThreads) void attention_prep_kernel(
     }
 }
 
-// Sum over the 64 lanes of each of N = 64 or 32 values: afterwards lane L
-// holds the total of value L % N.  One exchange level per lane-index bit from
-// the top: at each, a lane keeps the half of its values that its bit selects
-// (the upper half when the bit is set) and adds its partner's copy of that
-// half, so the levels move 32 + 16 + 8 + 4 + 2 + 1 values instead of 64 full
-// reductions.  Bits 5 and 4 pair lanes L and L ^ 32 / L ^ 16 by the gfx950
-// lane swaps (v_permlane32_swap, v_permlane16_swap); bits 3 .. 0 by DPP
-// (row_mirror, row_half_mirror, then the two quad permutations), whose
-// partners differ from the lane in the level's bit and agree in every bit
-// above it.  For N = 32 the levels start at bit 4, and the two 32-lane
-// halves' totals add at the end.
-template <int N>
-__device__ __forceinline__ float transpose_sum(float (&v)[N]) {
-    if constexpr (N == 64) {
+// Sum over the 64 lanes of each of 64 values: afterwards lane L holds the
+// total of value L.  Six exchange levels, one per lane-index bit from the top:
+// at each, a lane keeps the half of its values that its bit selects (the upper
+// half when the bit is set) and adds its partner's copy of that half, so the
+// levels move 32 + 16 + 8 + 4 + 2 + 1 values instead of 64 full reductions.
+// Bits 5 and 4 pair lanes L and L ^ 32 / L ^ 16 by the gfx950 lane swaps
+// (v_permlane32_swap, v_permlane16_swap); bits 3 .. 0 by DPP (row_mirror,
+// row_half_mirror, then the two quad permutations), whose partners differ
+// from the lane in the level's bit and agree in every bit above it.
+__device__ __forceinline__ float transpose_sum64(float (&v)[64]) {
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
         const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 32]), false, false);
         v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
     }
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
@@ -656,10 +651,6 @@ __device__ __forceinline__ float transpose_sum(float (&v)[N]) {
     level(std::integral_constant<int, 0x141>{}, 4, (lane & 4) != 0);
     level(std::integral_constant<int, 0x4E>{}, 2, (lane & 2) != 0);
     level(std::integral_constant<int, 0xB1>{}, 1, (lane & 1) != 0);
-    if constexpr (N == 32) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0]), __float_as_uint(v[0]), false, false);
-        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
     return v[0];
 }
 
@@ -667,11 +658,11 @@ __device__ __forceinline__ float transpose_sum(float (&v)[N]) {
 // heads that share KV head blockIdx.x / splits (engine.cpp:344-361: scores
 // q . k / sqrt(AD), softmax, sum of weights times v), over position range
 // blockIdx.x % splits of 0 .. *position.  A range is taken in blocks of
-// B = 4 R positions: wave w holds the K and V rows of positions w, w + 4, ...
-// of a block, lane l elements 4l .. 4l + 3 of each, every load of a block
-// requested at once and each row loaded once for all G heads (GP = G rounded
-// up to 4 or 8).  The lane products q_g . k_u of a wave's R GP (row, head)
-// pairs (32 or 64) reduce together in transpose_sum; the scores go to LDS, where wave
+// B = 4 * 64 / GP positions (GP = G rounded up to 4 or 8): wave w holds the K
+// and V rows of positions w, w + 4, ... of a block, lane l elements 4l .. 4l +
+// 3 of each, every load of a block requested at once and each row loaded once
+// for all G heads.  The lane products q_g . k_u of a wave's 64 (row, head)
+// pairs reduce together in transpose_sum64; the scores go to LDS, where wave
 // w runs the online softmax of heads w, w + 4 with wave reductions (a running
 // maximum rescales the running sum and accumulators), so no score buffer
 // bounds the context.  Each wave accumulates weight times v over its own rows
@@ -683,13 +674,13 @@ constexpr int kAttnSplits = 128;  // ranges per KV head for a decode step
 constexpr int kMaxGroup = 8;
 constexpr int kChunk = 2048;     // default rows of a prefill chunk
 
-template <int GP, int R = kWave / GP>
+template <int GP>
 __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
     const float* __restrict__ query, const float* __restrict__ key_cache, const float* __restrict__ value_cache,
     const int* __restrict__ position, float* __restrict__ partial, int AH, int KVH, int AD, int splits) {
     constexpr int kWaves = kHeadThreads / kWave;
-    constexpr int NV = R * GP;
-    static_assert((NV == 32 || NV == 64) && R % 4 == 0, "32 or 64 (row, head) pairs per wave, whole weight quads");
+    static_assert(GP == 4 || GP == 8, "64 (row, head) pairs per wave");
+    constexpr int R = kWave / GP;  // rows per wave per block
     constexpr int B = kWaves * R;  // positions per block
     // Scores, then weights, wave-major: sc[g][w * R + u] is position u * 4 + w.
     __shared__ __attribute__((aligned(16))) float sc[GP][B];
@@ -734,12 +725,12 @@ __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
         head_l[threadIdx.x] = 0.0f;
     }
     __syncthreads();
-    // After transpose_sum, lane L holds the score of row u = L / GP, head g = L % GP.
+    // After transpose_sum64, lane L holds the score of row u = L / GP, head g = L % GP.
     const int my_u = lane / GP, my_g = lane % GP;
     for (int b0 = t0; b0 < t1; b0 += B) {
         const int nb = min(B, t1 - b0);
         if (b0 != t0) load_block(b0);
-        float v[NV];
+        float v[64];
 #pragma unroll
         for (int u = 0; u < R; ++u) {
 #pragma unroll
@@ -751,8 +742,8 @@ __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
                 v[u * GP + g] = x;
             }
         }
-        const float s = transpose_sum(v);
-        if (lane < NV) sc[my_g][wave * R + my_u] = s / divisor;
+        const float s = transpose_sum64(v);
+        sc[my_g][wave * R + my_u] = s / divisor;
         __syncthreads();
         for (int g = wave; g < G; g += kWaves) {
             // lane = w * R + u holds position u * 4 + w.
@@ -1445,10 +1436,7 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                                e.query_and_gate, e.key, e.value, L.qnorm, L.knorm, e.d_position, e.query, e.gate,
                                L.key_cache, L.value_cache, c.AH, c.KVH, c.AD, c.RD);
             if (count == 1) {
-                // Blocks of 32 positions: at 4K context one block per range
-                // (4 query heads per KV head: 10.4 us against 11.7 with
-                // blocks of 64; the same at 16K).
-                auto attend = c.AH / c.KVH <= 4 ? attention_kernel<4, 8> : attention_kernel<8, 8>;
+                auto attend = c.AH / c.KVH <= 4 ? attention_kernel<4> : attention_kernel<8>;
                 hipLaunchKernelGGL(attend, dim3(c.KVH * kAttnSplits), dim3(kHeadThreads), 0, s, e.query,
                                    L.key_cache, L.value_cache, e.d_position, e.scores, c.AH, c.KVH, c.AD,
                                    kAttnSplits);
