@@ -126,7 +126,8 @@ size_t q3x_hip_moe_workspace_bytes(int tokens, int experts, int top_k, int H, in
  * expert_swiglu_kernel, expert_down_weighted_q4_kernel engine.cu:1186-1250).
  * gate_up: [experts, 2I, H], down: [experts, H, I], type Q4_0 or Q8_0.
  * tokens == 1 runs fused matvecs (decode); tokens > 1 groups the (token,
- * slot) pairs by expert and runs one grouped FP32-MFMA GEMM per expert.
+ * slot) pairs by expert and runs the experts' tiles as grouped GEMMs on the
+ * bf16 matrix cores, three exact bf16 products per FP32 product (FP32 sums).
  * ids outside [0, experts) contribute nothing (as engine.cu:1198, 1235). */
 int q3x_hip_moe_routed(const void* gate_up, const void* down, uint32_t type,
                        int experts, int H, int I, const float* X, int tokens,
@@ -207,7 +208,9 @@ size_t q3x_hip_moe_layer_workspace_bytes(const q3x_hip_moe_layer_weights* layer,
  * 1024, H, I, shared_I multiples of 32, shared_I <= I (the reference reuses
  * its 2I gate_up buffer for the shared expert, engine.cpp:100-102, 422-423),
  * X 16-byte aligned.  Replaces the routed path's caller-side router matvec,
- * shared expert and scaled add (engine.cu:1711, 1728-1735). */
+ * shared expert and scaled add (engine.cu:1711, 1728-1735).  On return the
+ * workspace begins with the router logits, FP32 [tokens, experts], that the
+ * routing was computed from. */
 int q3x_hip_moe_layer(const q3x_hip_moe_layer_weights* layer, const float* X, int tokens, float* Y,
                       int* ids, float* weights, void* workspace, size_t workspace_bytes,
                       hipStream_t stream);

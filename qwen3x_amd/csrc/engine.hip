@@ -1772,8 +1772,16 @@ extern "C" int q3x_hip_engine_forward(q3x_hip_engine* e, const int* tokens, int 
     if (count == 1) {
         hipGraphExec_t& g = e->graph[compute_logits ? 1 : 0];
         if (!g) {
+            // A capture runs nothing on the device: on failure the state, the
+            // KV cache and the position are as they were (the token copy
+            // queued above is rewritten by the next forward), so the engine
+            // stays usable and the error is returned as it is.
             const int rc = capture(*e, compute_logits != 0);
-            if (rc) return forward_failed(*e, rc);
+            if (rc) {
+                (void)hipStreamSynchronize(e->stream);
+                (void)hipGetLastError();
+                return rc;
+            }
         }
         if (hipGraphLaunch(g, e->stream) != hipSuccess) return forward_failed(*e, Q3X_HIP_ERUNTIME);
     } else {

@@ -15,9 +15,11 @@
 //     combines the slots in order (moe_down_combine_kernel);
 //   prefill (tokens > 1): the (token, slot) pairs are grouped by expert with
 //     a stable counting sort (deterministic positions), each expert's group is
-//     cut into 32-token tiles, and one grouped FP32-MFMA GEMM launch (gemm.h)
-//     runs gate_up for every tile of every expert, then SwiGLU, then one for
-//     down; a combine sums the slots of each token in slot order from zero.
+//     cut into tiles of 64 or 128 pairs, and one grouped GEMM launch
+//     (gemm_x3.h: bf16 matrix cores, three exact products per FP32 product)
+//     runs gate_up for every tile of every expert with SwiGLU in its
+//     epilogue, then one runs down; a combine sums the slots of each token
+//     in slot order from zero.
 // No atomics touch any accumulated value, so results are deterministic.
 #include "moe.h"
 
@@ -174,12 +176,18 @@ __device__ __forceinline__ void router_topk_wave(const float* __restrict__ row, 
 // is provably p's: dividing by the same total is monotone, equal e give
 // equal p (ties keep the lowest index in either order), and two e more than
 // 2^-21 apart (relative) stay strictly ordered after the division's rounding
-// (each rounding moves a normal quotient by at most 2^-24 of it).  So when
-// every two neighbours of the top_k + 1 largest e are equal or that far
-// apart, and the smallest of them is at least 2^-100 (its quotient by a total
-// of at most 1024 stays normal), the e order's first top_k are the
-// reference's ids in the reference's order; the total's 256-add chain is
-// then skipped.  Returns false (and no ids) otherwise.
+// (each rounding moves a normal quotient by at most 2^-24 of it).  The e
+// order's first top_k are the reference's ids in the reference's order when
+// every class of equal e that reaches into the first top_k is that far above
+// the next smaller e, since only then can no expert from below share a p
+// with it and win by a lower index.  The passes see the top_k + 1 largest e,
+// so the rule is: neighbours among the first top_k equal or that far apart,
+// the pair at the boundary (positions top_k - 1 and top_k) that far apart and
+// never equal -- a tie there hides the next smaller e, which may sit one ulp
+// below with a lower index and round to the same p -- and the smallest of
+// them at least 2^-100 (its quotient by a total of at most 1024 stays
+// normal).  The total's 256-add chain is then skipped.  Returns false (and no
+// ids) otherwise.
 template <int PER>
 __device__ __forceinline__ bool router_select_by_exp(const float* __restrict__ row, int experts, int top_k,
                                                      float* __restrict__ mine_p, int& out_id) {
@@ -199,7 +207,8 @@ __device__ __forceinline__ bool router_select_by_exp(const float* __restrict__ r
     for (int s = 0; s + 1 < kRouterMaxTopK + 1; ++s)
         if (s + 1 < passes) {
             const double a = chosen[s], b = chosen[s + 1];
-            apart = apart && (a == b || a >= b * (1.0 + 0x1p-21));
+            const bool gap = a >= b * (1.0 + 0x1p-21);
+            apart = apart && (gap || (a == b && s + 1 < top_k));
         }
     float smallest = chosen[0];
 #pragma unroll
@@ -413,10 +422,6 @@ struct GroupedGemm {
     static constexpr bool kPairedColumns = false;
     static constexpr bool kPartialTiles = true;  // every expert's last tile is short
     static constexpr bool kMfma16 = true;        // skip 16-row halves past the valid pairs
-    // One MFMA chain over K with the exact d * q in the weight tile: K is the
-    // hidden size (gate_up) or the expert width (down), and the per-block
-    // fold measured 8% slower here (92.6 -> 85.2 TFLOP/s at config 4).
-    static constexpr bool kBlockFold = false;
     int tiles_x;  // weight-row tiles
     const float* A;
     int a_cols;

@@ -20,7 +20,7 @@ import oracle
 from oracle import model_file as mf
 import qwen3x_amd as q3x
 from tests.helpers import BLOCK_BYTES, Q4_0, Q8_0, dequant_numpy, row_bound
-from tests.test_gpu_moe_layer import bf16, check_layer
+from tests.test_gpu_moe_layer import bf16, check_layer, run_layer
 from tests.test_gpu_parity import _torch, dev, host, say
 
 pytestmark = pytest.mark.gpu
@@ -176,14 +176,10 @@ def test_moe_layer_on_a_loaded_q4_model(tokens, q4_model):
     say(f"loaded MoE layer tokens={tokens}")
     layer = model.moe_layer(7)
     assert (layer.type, layer.experts, layer.top_k, layer.H, layer.I, layer.shared_I) == (Q4_0, E, k, H, I, SI)
-    Y = torch.full((tokens, H), float("nan"), dtype=torch.float32, device="cuda:0")
-    ids = torch.empty((tokens, k), dtype=torch.int32, device="cuda:0")
-    wts = torch.empty((tokens, k), dtype=torch.float32, device="cuda:0")
-    q3x.moe_layer(layer, dev(X), tokens, Y, ids, wts)
-    got, ids_g, wts_g = host(Y), host(ids), host(wts)
+    got, ids_g, wts_g, logits_g = run_layer(layer, X, tokens, k)
     want, ids_o, wts_o = oracle.moe_layer(w["router"], w["gate_up"], w["down"], w["shared_gate"], w["shared_up"],
                                           w["shared_down"], w["shared_scale"], Q4_0, E, H, I, SI, k, X)
-    check_layer(w, Q4_0, E, H, I, SI, k, X, got, ids_g, wts_g, want, ids_o, wts_o)
+    check_layer(w, Q4_0, E, H, I, SI, k, X, got, ids_g, wts_g, want, ids_o, wts_o, logits_g)
 
 
 def test_loaded_q4_layers_bind_through_the_table(q4_model):
