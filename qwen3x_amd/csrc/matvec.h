@@ -16,9 +16,9 @@
 //  * Q8_0 bytes convert with sign-extending SDWA converts and accumulate in
 //    FP32 with FMAs: inner = sum q*x per block, then acc += f16(d) * inner,
 //    the per-block factorisation of arch/cpu.cpp:64-73;
-//  * Q4_0 nibbles become exact binary16 subnormals that v_fma_mix_f32 takes
-//    directly (block_dot_q4_mix), or signed bytes 16*(n-8) for the SDWA path
-//    (block_dot_q4);
+//  * Q4_0 nibbles become the exact binary16 values n - 8 that v_fma_mix_f32
+//    takes directly (block_dot_q4_exact), or signed bytes 16*(n-8) for the
+//    SDWA path (block_dot_q4);
 //  * the row's lane partial sums are combined with a butterfly inside the
 //    row group; lane 0 of the group writes (or adds to) y.
 // mv_pipe_kernel (x shared by all rows, held in LDS) prefetches the next
@@ -239,20 +239,32 @@ __global__ __launch_bounds__(512) void mv_stream_kernel(Rows rows, int nrows, in
     }
 }
 
-// Q4_0 block dot through binary16 subnormals: a nibble n in bits 0-3 of a
-// 16-bit half is the half n * 2^-24, in bits 4-7 it is 16n * 2^-24, and
-// v_fma_mix_f32 multiplies such a half by an FP32 activation exactly (f16 and
-// f32 denormals are enabled).  Two masks per half-pair replace the per-byte
-// converts.  With s(n) = lo + hi / 16 accumulated in a fixed order,
-// sum (n - 8) x = 2^24 * (s(n) - s(8)), where xref = s(8) is the same
-// accumulation with every nibble 8, computed once per block column; a block
-// of zero weights (all nibbles 8) therefore contributes exactly zero.
+// Q4_0 block dot with every weight exact in binary16.  A nibble n placed in
+// bits 0-3 of a half whose other bits are 0x6400 is the half 1024 + n
+// (exponent 2^10, n in the last mantissa bits); placed in bits 4-7 it is
+// 1024 + 16n.  One v_and_or per half pair builds those, one packed half add
+// of -1032 (-1152) turns them into n - 8 (16 (n - 8)) exactly, and
+// v_fma_mix_f32 multiplies such a half by an FP32 activation exactly.  So
+// the block's inner product is the reference's sum of (n - 8) x
+// (arch/cpu.cpp:91-101) with exact products and FP32 sums: elements 0..15
+// and 16..31 in two chains (the second 16 times its value), joined by one
+// FMA with 1/16.  Its rounding is relative to sum |n - 8| |x|, as the
+// reference's is, and a block of zero weights (all nibbles 8) gives 0.
 // Returns f16(d) times that.
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ half2_t as_half2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
 
-__device__ __forceinline__ float block_dot_q4_mix(const uint8_t* lds, uint32_t p, const float* xv, float xref) {
+// (a & mask) | bits in one v_and_or_b32.  A VOP3 instruction on gfx9 takes
+// no literal and one scalar operand, so the compiler would split it into an
+// AND and an OR with literals; the mask rides in a VGPR, the bits in an SGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "s"(bits));
+    return r;
+}
+
+__device__ __forceinline__ float block_dot_q4_exact(const uint8_t* lds, uint32_t p, const float* xv) {
     const uint32_t scale = *reinterpret_cast<const uint16_t*>(lds + p);
     const uint32_t start = p + 2;
     const uint32_t base = start & ~3u;
@@ -260,16 +272,18 @@ __device__ __forceinline__ float block_dot_q4_mix(const uint8_t* lds, uint32_t p
     uint32_t a[5];
 #pragma unroll
     for (int k = 0; k < 5; ++k) a[k] = *reinterpret_cast<const uint32_t*>(lds + base + 4 * k);
+    const half2_t lo_bias = as_half2(0xE408E408u);  // -1032: 1024 + n -> n - 8
+    const half2_t hi_bias = as_half2(0xE480E480u);  // -1152: 1024 + 16n -> 16 (n - 8)
     float lo = 0.0f, hi = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         // Bytes 4k..4k+3: low nibble of byte j is element j, high nibble 16 + j.
         const uint32_t u = __builtin_amdgcn_alignbyte(a[k + 1], a[k], shift);
         const uint32_t t = u >> 8;
-        const half2_t e0 = as_half2(u & 0x000F000Fu);  // elements 4k, 4k+2
-        const half2_t e1 = as_half2(u & 0x00F000F0u);  // elements 16+4k, 16+4k+2 (x16)
-        const half2_t e2 = as_half2(t & 0x000F000Fu);  // elements 4k+1, 4k+3
-        const half2_t e3 = as_half2(t & 0x00F000F0u);  // elements 16+4k+1, 16+4k+3 (x16)
+        const half2_t e0 = as_half2(and_or(u, 0x000F000Fu, 0x64006400u)) + lo_bias;  // elements 4k, 4k+2
+        const half2_t e1 = as_half2(and_or(u, 0x00F000F0u, 0x64006400u)) + hi_bias;  // 16+4k, 16+4k+2 (x16)
+        const half2_t e2 = as_half2(and_or(t, 0x000F000Fu, 0x64006400u)) + lo_bias;  // 4k+1, 4k+3
+        const half2_t e3 = as_half2(and_or(t, 0x00F000F0u, 0x64006400u)) + hi_bias;  // 16+4k+1, 16+4k+3 (x16)
         lo = fmaf(static_cast<float>(e0.x), xv[4 * k + 0], lo);
         hi = fmaf(static_cast<float>(e1.x), xv[16 + 4 * k + 0], hi);
         lo = fmaf(static_cast<float>(e2.x), xv[4 * k + 1], lo);
@@ -279,21 +293,7 @@ __device__ __forceinline__ float block_dot_q4_mix(const uint8_t* lds, uint32_t p
         lo = fmaf(static_cast<float>(e2.y), xv[4 * k + 3], lo);
         hi = fmaf(static_cast<float>(e3.y), xv[16 + 4 * k + 3], hi);
     }
-    const float inner = (fmaf(hi, 0.0625f, lo) - xref) * 16777216.0f;
-    return f16_fast(scale) * inner;
-}
-
-// s(8) of block_dot_q4_mix for one block of 32 activations: the same FMA
-// chains (elements 0..15 and 16..31 in order) with every nibble 8.
-__device__ __forceinline__ float q4_mix_reference(const float* xb) {
-    const half2_t eight = as_half2(0x00800008u);  // 8 * 2^-24 (low nibble), 128 * 2^-24 (high nibble)
-    float lo = 0.0f, hi = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        lo = fmaf(static_cast<float>(eight.x), xb[i], lo);
-        hi = fmaf(static_cast<float>(eight.y), xb[16 + i], hi);
-    }
-    return fmaf(hi, 0.0625f, lo);
+    return f16_fast(scale) * fmaf(hi, 0.0625f, lo);
 }
 
 // Software-pipelined streaming kernel for inputs shared by every row (x held
@@ -320,12 +320,8 @@ struct PipeShape {
     static constexpr int WAVE_LDS = G * SEGP;       // LDS bytes per wave
 };
 
-// LDS bytes of the shared part of a pipe launch: x (padded) and, for Q4_0,
-// the per-block references s(8) of block_dot_q4_mix.
-__host__ __device__ constexpr uint32_t pipe_x_bytes(uint32_t qt, int bpr) {
-    return ((x_lds_bytes(bpr) + 15u) & ~15u) +
-           (qt == Q3X_HIP_MATRIX_Q4_0 ? ((4u * bpr + 15u) & ~15u) : 0u);
-}
+// LDS bytes of the shared part of a pipe launch: x (padded).
+__host__ __device__ constexpr uint32_t pipe_x_bytes(int bpr) { return (x_lds_bytes(bpr) + 15u) & ~15u; }
 
 // Input staging of mv_pipe_kernel: the launch's x (bpr blocks of 32 FP32
 // values) into the workgroup's padded LDS copy, once per workgroup, with
@@ -354,12 +350,11 @@ __global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int n
     int gw = blockIdx.x * wpb + wave;
     int GW = gridDim.x * wpb;
     // The wave's matrix (multi-matrix launches); gw, GW, nrows become its own.
-    const auto rows = WaveRows<Rows>::get(all_rows, gw, GW, nrows, lds_dyn + pipe_x_bytes(QT, bpr) + wpb * S::WAVE_LDS);
+    const auto rows = WaveRows<Rows>::get(all_rows, gw, GW, nrows, lds_dyn + pipe_x_bytes(bpr) + wpb * S::WAVE_LDS);
     const int g = lane / LPR;
     const int li = lane % LPR;
     uint8_t* const xl = lds_dyn;
-    float* const sxl = reinterpret_cast<float*>(lds_dyn + ((x_lds_bytes(bpr) + 15u) & ~15u));
-    uint8_t* const wl = lds_dyn + pipe_x_bytes(QT, bpr) + wave * S::WAVE_LDS;
+    uint8_t* const wl = lds_dyn + pipe_x_bytes(bpr) + wave * S::WAVE_LDS;
     const int npass = (bpr + LPR - 1) / LPR;
     const int my_rows = gw < nrows ? (nrows - gw + GW - 1) / GW : 0;
     const int steps = (my_rows + RS - 1) / RS * npass;
@@ -400,16 +395,8 @@ __global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int n
         if (++qp == npass) { qp = 0; find_rows(++qb); }
     }
 
-    // x into LDS once per workgroup (overlaps the first weight loads), then
-    // the per-block references for Q4_0.
-    {
-        in.stage(rows.input(0), xl, bpr, reinterpret_cast<float*>(lds_dyn + pipe_x_bytes(QT, bpr)));
-        if (Q4) {
-            for (int b = threadIdx.x; b < bpr; b += blockDim.x)
-                sxl[b] = q4_mix_reference(reinterpret_cast<const float*>(xl + x_block_offset(b)));
-            __syncthreads();
-        }
-    }
+    // x into LDS once per workgroup (overlaps the first weight loads).
+    in.stage(rows.input(0), xl, bpr, reinterpret_cast<float*>(lds_dyn + pipe_x_bytes(bpr)));
 
     float acc[R];
 #pragma unroll
@@ -432,7 +419,6 @@ __global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int n
                     xv[4 * i + 0] = t.x; xv[4 * i + 1] = t.y; xv[4 * i + 2] = t.z; xv[4 * i + 3] = t.w;
                 }
             }
-            const float xref = Q4 ? sxl[col] : 0.0f;
 #pragma unroll
             for (int it = 0; it < R; ++it) {
 #pragma unroll
@@ -445,7 +431,7 @@ __global__ __launch_bounds__(1024, WPE) void mv_pipe_kernel(Rows all_rows, int n
                 wave_lds_sync();
                 if (li < nblk) {
                     const uint32_t p = g * S::SEGP + li * BB;
-                    acc[it] += Q4 ? block_dot_q4_mix(wl, p, xv, xref) : block_dot_q8(wl, p, xv);
+                    acc[it] += Q4 ? block_dot_q4_exact(wl, p, xv) : block_dot_q8(wl, p, xv);
                 }
                 wave_lds_sync();
             }
@@ -593,10 +579,10 @@ inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_
         hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(kLdsPerCU)) == hipSuccess;
     constexpr size_t tail = rows_route<Rows>::lds;
-    size_t lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb) * S::WAVE_LDS + tail;
+    size_t lds = pipe_x_bytes(bpr) + static_cast<size_t>(wpb) * S::WAVE_LDS + tail;
     while (lds > kLdsPerCU && wpb > 4) {
         wpb -= 4;
-        lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb) * S::WAVE_LDS + tail;
+        lds = pipe_x_bytes(bpr) + static_cast<size_t>(wpb) * S::WAVE_LDS + tail;
     }
     if (lds > kLdsPerCU) return Q3X_HIP_ENOTSUP;  // x too long for LDS
     if (lds > 64 * 1024 && !lds_ready) return Q3X_HIP_ERUNTIME;
@@ -608,7 +594,7 @@ inline int launch_pipe(const Rows& rows, int nrows, int bpr, int wpb, hipStream_
         std::max<long long>((nrows + batches * rs - 1) / (batches * rs), rows.matrices());
     const int wpb_used = static_cast<int>(std::min<long long>(wpb, (waves + kCUs * per_cu - 1) / (kCUs * per_cu)));
     const int grid = static_cast<int>((waves + wpb_used - 1) / wpb_used);
-    lds = pipe_x_bytes(QT, bpr) + static_cast<size_t>(wpb_used) * S::WAVE_LDS + tail;
+    lds = pipe_x_bytes(bpr) + static_cast<size_t>(wpb_used) * S::WAVE_LDS + tail;
     Rows planned = rows;
     planned.plan_waves(grid * wpb_used);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWave * wpb_used), lds, stream, planned, nrows, bpr, in);
@@ -640,9 +626,11 @@ inline int launch_pipe_for(const Rows& rows, int nrows, int bpr, hipStream_t str
     // blocks = 2.5 passes) take 32 lanes per row (two rows per pass).  The
     // lanes per row depend on the row length only, so the per-row reduction
     // order (and the result) is the same whatever the launch's row count.
-    // The two-row build needs 69 VGPRs (7 waves per SIMD), so one 16-wave
+    // The two-row build needs 70 VGPRs (7 waves per SIMD), so one 16-wave
     // workgroup per CU is resident: a grid of one per CU (each wave twice the
-    // rows) avoids a second round of workgroups (9% faster at 34816 rows).
+    // rows) avoids a second round of workgroups.  At 34816 x 160 blocks it
+    // takes 23.0 us against 24.3 us for one row per step on two workgroups
+    // per CU (60 VGPRs; interleaved A/B, medians of 9 rounds).
     if (bpr <= 256 && bpr % 64 != 0 && bpr % 32 == 0) {
         if (nrows <= 4096) return launch_pipe<QT, 32, 1, Rows, 1, 4, In>(rows, nrows, bpr, 16, stream, 1, in);
         return launch_pipe<QT, 32, 2, Rows, 1, 4, In>(rows, nrows, bpr, 16, stream, 1, in);

@@ -584,8 +584,7 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
 
     const int bpr = I / kBlock;
-    const uint32_t xs_bytes = pipe_x_bytes(QT, bpr);  // one slot's activations (+ Q4 references)
-    const uint32_t ref_off = (x_lds_bytes(bpr) + 15u) & ~15u;
+    const uint32_t xs_bytes = pipe_x_bytes(bpr);  // one slot's activations
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int wpb = blockDim.x / kWave;
@@ -639,7 +638,7 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
     };
     // h of every slot into the padded x layout: its loads go out first (they
     // return from L2), then the first step's weights, whose latency overlaps
-    // the copy and the Q4 references.
+    // the copy.
     constexpr int kHPerThread = 8;
     float hv[kHPerThread];
     const int hn = slots * I;
@@ -665,15 +664,6 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
     for (int c = threadIdx.x + kHPerThread * static_cast<int>(blockDim.x); c < hn; c += blockDim.x)
         put_h(c, h_at(c));
     __syncthreads();
-    if (Q4) {
-        for (int c = threadIdx.x; c < slots * bpr; c += blockDim.x) {
-            const int slot = c / bpr, b = c - slot * bpr;
-            uint8_t* xs = lds_dyn + slot * xs_bytes;
-            reinterpret_cast<float*>(xs + ref_off)[b] =
-                q4_mix_reference(reinterpret_cast<const float*>(xs + x_block_offset(b)));
-        }
-        __syncthreads();
-    }
 
     const float shared_weight = has_shared ? sigmoid_ref(*shared.logit) : 0.0f;
     float acc[IT];
@@ -701,7 +691,6 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
                 const f32x4 t = *reinterpret_cast<const f32x4*>(xs + x_block_offset(col) + 16 * q);
                 xv[4 * q + 0] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
             }
-            const float xref = Q4 ? reinterpret_cast<const float*>(xs + ref_off)[col] : 0.0f;
 #pragma unroll
             for (int gg = 0; gg < G; ++gg)
 #pragma unroll
@@ -711,7 +700,7 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
             wave_lds_sync();
             if (li < nblk && my_slot < slots) {
                 const uint32_t p = g * S::SEGP + li * BB;
-                acc[it] += Q4 ? block_dot_q4_mix(wl, p, xv, xref) : block_dot_q8(wl, p, xv);
+                acc[it] += Q4 ? block_dot_q4_exact(wl, p, xv) : block_dot_q8(wl, p, xv);
             }
             wave_lds_sync();
         }
@@ -745,7 +734,7 @@ int launch_moe_down(const uint8_t* down, int experts, int H, int I, const int* i
     constexpr int kWaves = 8;
     const size_t row_bytes = static_cast<size_t>(I / kBlock) * (QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes);
     const int slots = top_k + (shared.down ? 1 : 0);
-    const size_t lds = static_cast<size_t>(slots) * pipe_x_bytes(QT, I / kBlock) + kWaves * S::WAVE_LDS;
+    const size_t lds = static_cast<size_t>(slots) * pipe_x_bytes(I / kBlock) + kWaves * S::WAVE_LDS;
     if (lds > kLdsPerCU) return Q3X_HIP_ENOTSUP;
     // Slot capacity: the routed experts alone keep the smaller register set.
     auto kernel = shared.down ? moe_down_combine_kernel<QT, LPR, kRouterMaxTopK + 1>
