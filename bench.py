@@ -11,10 +11,12 @@ with all inputs resident in HBM.  Distinct weight copies are rotated so the
 reported under "configs" (matvec GB/s, GEMM TFLOP/s, MoE).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-configs] [--no-cpu] [--roofline-only]
+    python bench.py --trace-summary <rocprofv3 kernel_trace.csv>
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
 import statistics
@@ -45,6 +47,9 @@ def parse():
                     help="only the lm_head kernel (--steps launches) and a same-size copy, for counter runs")
     ap.add_argument("--only", default="",
                     help="comma list of configs (cfg0,cfg2,cfg3,cfg4,engine) to run alone, for counter runs")
+    ap.add_argument("--trace-summary", default="",
+                    help="summarise a rocprofv3 kernel trace (--kernel-trace --output-format csv) of this "
+                         "program by kernel and grid, with the roofline kernel's back-to-back block; no GPU")
     return ap.parse_args()
 
 
@@ -185,6 +190,11 @@ def headline(torch, q3x, wl, steps, warmup):
         step.run_layer(layer_sets[r])
         step.run_lm(lm_set[r % n_lm])
 
+    # The lm_head kernel's duration before the steps (the box as it comes)
+    # and after them (under the sustained load the steps put on HBM), both
+    # over the same 20 back-to-back launches: the drift of the dominant
+    # kernel within the run.
+    lm_before_ms = lm_head_launch_ms(torch, step, lm_set, 20)
     for i in range(warmup):
         run_step(i % n_layer)
     torch.cuda.synchronize()
@@ -224,7 +234,8 @@ def headline(torch, q3x, wl, steps, warmup):
         "ms_per_step": ms,
         "step_bytes": step_bytes,
         "copies": {"layer_set": n_layer, "lm_head": n_lm},
-        "lm_head": {"bytes": lm_alg, "ms": lm_ms, "GBps": lm_alg / (lm_ms * 1e-3) / 1e9},
+        "lm_head": {"bytes": lm_alg, "ms": lm_ms, "GBps": lm_alg / (lm_ms * 1e-3) / 1e9,
+                    "before_ms": lm_before_ms},
         "mats": mats,
     }
 
@@ -650,8 +661,104 @@ def cpu_baseline(mats, seconds):
                       f"({t * 1e3:.0f} ms each), single thread; host nproc={os.cpu_count()}"}
 
 
+def kernel_name(name):
+    """A demangled kernel name without its argument list (the last
+    parenthesised group; "(anonymous namespace)" inside the name stays)."""
+    name = name.strip()
+    if not name.endswith(")"):
+        return name
+    depth = 0
+    for i in range(len(name) - 1, -1, -1):
+        depth += {")": 1, "(": -1}.get(name[i], 0)
+        if depth == 0:
+            return name[:i].strip()
+    return name
+
+
+def trace_summary(path, top=40):
+    """Kernel durations from a rocprofv3 kernel trace of this program
+    (--kernel-trace --output-format csv), grouped by kernel and launch shape
+    (workgroups x workgroup size), so launches of one template at different
+    shapes (lm_head and config 0) stay apart.  The roofline kernel's
+    measurement -- the longest run of back-to-back dispatches of one kernel
+    and shape (the 20 launches timed after the steps) -- is reported with the
+    lm_head algorithmic bytes and the fraction of the HBM peak they imply, and
+    that shape's dispatches are listed over the whole run (first and last
+    five) to show the drift under sustained load."""
+    with open(path, newline="") as f:
+        rows = list(csv.DictReader(f))
+    if not rows:
+        print("empty trace")
+        return
+
+    def field(r, *names):
+        for n in names:
+            if n in r and r[n] != "":
+                return r[n]
+        raise KeyError(names)
+
+    disp = []
+    for r in rows:
+        name = field(r, "Kernel_Name", "Kernel-Name", "KernelName")
+        wg = int(field(r, "Workgroup_Size_X", "Workgroup_Size", "WorkgroupSizeX"))
+        grid = int(field(r, "Grid_Size_X", "Grid_Size", "GridSizeX"))
+        t0, t1 = int(field(r, "Start_Timestamp", "BeginNs")), int(field(r, "End_Timestamp", "EndNs"))
+        disp.append((t0, t1, kernel_name(name), grid // max(wg, 1), wg))
+    disp.sort()
+    groups = {}
+    for t0, t1, name, wgs, wg in disp:
+        groups.setdefault((name, wgs, wg), []).append((t1 - t0) / 1e3)
+    print(f"trace: {path}\n{len(disp)} dispatches\n")
+    print(f"{'calls':>6} {'mean_us':>9} {'median_us':>9} {'min_us':>8} {'max_us':>8}  workgroups x size  kernel")
+    for (name, wgs, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]:
+        print(f"{len(d):6d} {statistics.mean(d):9.2f} {statistics.median(d):9.2f} {min(d):8.2f} {max(d):8.2f}  "
+              f"{wgs:6d} x {wg:<5d}  {name[:150]}")
+    # The headline's lm_head launches (q3x_hip_mv of a Q8_0 matrix: the
+    # dense-row pipe kernel) are the shape of that kernel whose dispatches
+    # come in back-to-back blocks of 10 or more (the blocks timed before the
+    # steps and after them, the second being the roofline measurement) and
+    # last longest; config 0's launches of the same kernel come in graph
+    # replays of another shape.
+    def blocks_of(key):
+        out, run = [], []
+        for t0, t1, *k in disp + [(0, 0, None, 0, 0)]:
+            if tuple(k) == key:
+                run.append((t1 - t0) / 1e3)
+                continue
+            if len(run) >= 10:
+                out.append(run)
+            run = []
+        return out
+
+    cand = [k for k, v in groups.items() if "mv_pipe_kernel<1u" in k[0] and "DenseRows<false>" in k[0]
+            and statistics.mean(v) > 50 and blocks_of(k)]
+    if not cand:
+        return
+    key = max(cand, key=lambda k: statistics.mean(groups[k]))
+    lm_bytes = 151936 * (4096 // 32) * 34 + 4 * 4096 + 4 * 151936
+    same = groups[key]
+    print(f"\nlm_head: {key[0][:120]} ({key[1]} x {key[2]}), {len(same)} dispatches, algorithmic bytes {lm_bytes}")
+    blocks = blocks_of(key)
+    labels = ["before the steps", "after the steps (roofline)"]
+    for i, b in enumerate(blocks):
+        # The timed launches are a block's last 20 (its first are the
+        # untimed warm-up launches and, after the steps, the last step's).
+        timed = b[-20:]
+        mean = statistics.mean(timed)
+        label = labels[i] if len(blocks) == 2 else f"block {i}"
+        print(f"  back-to-back block {i} ({label}): {len(b)} dispatches; its last {len(timed)} (the timed ones) "
+              f"mean {mean:.2f} us, median {statistics.median(timed):.2f} us -> "
+              f"{lm_bytes / (mean * 1e-6) / 1e9:.1f} GB/s = {lm_bytes / (mean * 1e-6) / 1e9 / HBM_PEAK_GBS:.4f} "
+              f"of {HBM_PEAK_GBS:.0f} GB/s")
+    print(f"  all its dispatches in order: first five {', '.join(f'{v:.1f}' for v in same[:5])}; "
+          f"last five {', '.join(f'{v:.1f}' for v in same[-5:])} (us)")
+
+
 def main():
     args = parse()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the matvec/GEMM shard by output rows with an all-gather, not measured here.", file=sys.stderr)
@@ -695,6 +802,10 @@ def main():
                      "frac": round(lm["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "mv_pipe_kernel<Q8_0, 64 lanes/row, 1 row/step, 2x16 waves/CU> on lm_head 151936x4096",
                      "algorithmic_bytes_per_launch": lm["bytes"], "avg_launch_ms": round(lm["ms"], 5),
+                     "drift": {"before_steps_ms": round(lm["before_ms"], 5), "after_steps_ms": round(lm["ms"], 5),
+                               "note": "20 back-to-back lm_head launches timed by HIP events before the warm-up "
+                                       "steps and after the timed steps; avg_launch_ms is the second"},
+                     "trace": "profiles/bench_default_trace.txt",
                      "traffic_source": "profiles/pmc_traffic_lm_head_q8_0.txt" if traffic else None},
     }
     if not args.no_configs:
