@@ -19,6 +19,28 @@
 //
 // Domain: x < 88 (the router calls it on logit - max <= 0).  Below
 // ln(2^-150) the result is +0, as in libm; NaN propagates.
+//
+// The table of 2^(i/32) and the cubic's coefficients below are those of the
+// ARM Optimized Routines expf, whose upstream notice is:
+//
+//   Copyright (c) 2017-2018, Arm Limited.
+//   SPDX-License-Identifier: MIT OR Apache-2.0 WITH LLVM-exception
+//
+// Under the MIT option:  Permission is hereby granted, free of charge, to any
+// person obtaining a copy of this software and associated documentation files
+// (the "Software"), to deal in the Software without restriction, including
+// without limitation the rights to use, copy, modify, merge, publish,
+// distribute, sublicense, and/or sell copies of the Software, and to permit
+// persons to whom the Software is furnished to do so, subject to the
+// following conditions: The above copyright notice and this permission
+// notice shall be included in all copies or substantial portions of the
+// Software.  THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND,
+// EXPRESS OR IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF
+// MERCHANTABILITY, FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT.  IN
+// NO EVENT SHALL THE AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM,
+// DAMAGES OR OTHER LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR
+// OTHERWISE, ARISING FROM, OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE
+// USE OR OTHER DEALINGS IN THE SOFTWARE.
 #pragma once
 
 #include <hip/hip_runtime.h>
