@@ -709,10 +709,50 @@ def trace_summary(path, top=40):
     for t0, t1, name, wgs, wg in disp:
         groups.setdefault((name, wgs, wg), []).append((t1 - t0) / 1e3)
     print(f"trace: {path}\n{len(disp)} dispatches\n")
+    total = sum(sum(d) for d in groups.values())
+    by_name = {}
+    for (name, _, _), d in groups.items():
+        by_name.setdefault(name, []).extend(d)
+    print(f"By kernel (all shapes; share of all kernel time, {total / 1e3:.1f} ms):")
+    print(f"{'calls':>6} {'mean_us':>9} {'total_ms':>9} {'share':>6}  kernel")
+    for name, d in sorted(by_name.items(), key=lambda kv: -sum(kv[1]))[:top]:
+        print(f"{len(d):6d} {statistics.mean(d):9.2f} {sum(d) / 1e3:9.2f} {sum(d) / total:6.3f}  {name[:150]}")
+    print(f"\nBy kernel and shape:")
     print(f"{'calls':>6} {'mean_us':>9} {'median_us':>9} {'min_us':>8} {'max_us':>8}  workgroups x size  kernel")
     for (name, wgs, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]:
         print(f"{len(d):6d} {statistics.mean(d):9.2f} {statistics.median(d):9.2f} {min(d):8.2f} {max(d):8.2f}  "
               f"{wgs:6d} x {wg:<5d}  {name[:150]}")
+    # Engine decode steps: the dispatches up to and including advance_kernel
+    # (the step's last kernel), among them no prefill kernel; steps of one
+    # model have the same kernel count.
+    steps, cur = [], []
+    for t0, t1, name, wgs, wg in disp:
+        cur.append((t0, t1, name))
+        if name.endswith("advance_kernel"):
+            steps.append(cur)
+            cur = []
+    prefill = ("gemm_x3_kernel", "delta_chunk", "delta_scan", "delta_conv", "attention_prefill", "rms_kernel")
+    by_len = {}
+    for s in steps:
+        if not any(p in name for _, _, name in s for p in prefill):
+            by_len.setdefault(len(s), []).append(s)
+    for n, ss in sorted(by_len.items()):
+        if len(ss) < 16:
+            continue
+        span = statistics.median([(s[-1][1] - s[0][0]) / 1e3 for s in ss])
+        print(f"\nDecode steps of {n} kernels ({len(ss)} steps): median span {span:.1f} us; per kernel, "
+              "median us per step:")
+        per = {}
+        for s in ss:
+            acc = {}
+            for t0, t1, name in s:
+                acc.setdefault(name, [0.0, 0])
+                acc[name][0] += (t1 - t0) / 1e3
+                acc[name][1] += 1
+            for name, (us, cnt) in acc.items():
+                per.setdefault(name, []).append((us, cnt))
+        for name, v in sorted(per.items(), key=lambda kv: -statistics.median(u for u, _ in kv[1]))[:12]:
+            print(f"  x{v[0][1]:3d} {statistics.median(u for u, _ in v):8.1f}  {name[:120]}")
     # The headline's lm_head launches (q3x_hip_mv of a Q8_0 matrix: the
     # dense-row pipe kernel) are the shape of that kernel whose dispatches
     # come in back-to-back blocks of 10 or more (the blocks timed before the

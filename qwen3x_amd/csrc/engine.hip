@@ -279,7 +279,8 @@ __device__ __forceinline__ void store_keys(float* col, int k0, int KD, bool ok, 
 // recurrence itself runs token by token:
 //   delta_prep_kernel (row r, key head kh; parallel): q, k of the head
 //     L2-normalised in place (q also divided by sqrt(KD)); for the value
-//     heads of kh, b <- beta = sigmoid(b) and a <- exp(decay) in place;
+//     heads of kh, b <- beta = sigmoid(b) and a <- decay in place (the
+//     memory is scaled by exp(decay), engine.cpp:279);
 //   delta_scan_kernel (value head; sequential over the rows): the memory
 //     update of the gated delta rule (engine.cpp:262-316), writing q S
 //     unnormalised;
@@ -310,7 +311,7 @@ __global__ __launch_bounds__(128) void delta_prep_kernel(float* __restrict__ qkv
         const int head = kh * per + u;
         const size_t at = static_cast<size_t>(r) * VH + head;
         b[at] = sigmoid_ref(b[at]);
-        a[at] = expf(-expf(alog[head]) * softplus_ref(a[at] + bf16_value(dt[head])));
+        a[at] = -expf(alog[head]) * softplus_ref(a[at] + bf16_value(dt[head]));  // decay; e^decay scales S
     }
 }
 
@@ -335,7 +336,7 @@ constexpr int kScanValues = (2 * 128 + kScanCols) * kScanTile;  // staged values
 constexpr int kScanLoads = kScanValues / kScanThreads;          // per thread
 
 __global__ __launch_bounds__(kScanThreads) void delta_scan_kernel(const float* __restrict__ qkv,
-                                                                  const float* __restrict__ scale,
+                                                                  const float* __restrict__ decay,
                                                                   const float* __restrict__ beta,
                                                                   float* __restrict__ memory, float* __restrict__ out,
                                                                   int KH, int VH, int KD, int VD, int count) {
@@ -375,7 +376,7 @@ __global__ __launch_bounds__(kScanThreads) void delta_scan_kernel(const float* _
             pre[i] = x;
         }
         if (t < nt) {
-            pst = scale[static_cast<size_t>(r0 + t) * VH + head];
+            pst = expf(decay[static_cast<size_t>(r0 + t) * VH + head]);  // e^decay
             pbt = beta[static_cast<size_t>(r0 + t) * VH + head];
         }
     };
@@ -431,6 +432,322 @@ __global__ __launch_bounds__(kScanThreads) void delta_scan_kernel(const float* _
         }
     }
     store_keys<kScanKeys>(S, k0, KD, col, s);
+}
+
+// The prefill recurrence in chunks of kDeltaChunk tokens on the matrix
+// cores (the WY form of the gated delta rule).  With the memory S0 before a
+// chunk, G_t = decay_1 + ... + decay_t inside it (so the reference's
+// per-token S <- e^decay S, p = S^T k, S <- S + beta k (v - p)^T, o = S^T q,
+// engine.cpp:262-316, unrolls to S_t = e^G_t S0 + sum_{j<=t} e^(G_t - G_j)
+// k_j u_j^T), the updates u_t = beta_t (v_t - p_t) solve
+//   (I + A) U = beta (V - e^G (K S0)),  A_tj = beta_t e^(G_t - G_j) k_t.k_j (j < t),
+// so U = U0 - W S0 with U0 = (I + A)^-1 beta V and W = (I + A)^-1 beta e^G K,
+// and
+//   O = e^G (Q S0) + P U,   P_tj = e^(G_t - G_j) q_t.k_j (j <= t),
+//   S_C = e^G_C S0 + K^T (e^(G_C - G) U).
+// delta_chunk_prep_kernel forms W, U0, P, e^G, e^(G_C - G) and e^G_C of
+// every (chunk, value head) in parallel (every exponent is <= 0);
+// delta_chunk_scan_kernel then runs the chunks of a head in order with Q
+// and K read from the projections, four FP32 MFMA products per chunk.
+// Tokens past the last row are zeros in the prep (k = q = v = 0, beta = 0,
+// decay 0), so their rows of W, U0 and P are zero and they change nothing.
+// The sums run in another order than the reference's token loop (FP32
+// throughout).
+constexpr int kDeltaChunk = 32;
+constexpr int kDeltaPitch = 132;  // LDS rows of K, Q, V (16-byte aligned)
+constexpr int kDeltaTile = kDeltaChunk * 128;  // one [32][128] block
+// Per (chunk, value head): W and U0 [32][128], P [32][32], e^G [32],
+// e^(G_C - G) [32], e^G_C (padded to a multiple of 16 floats).
+constexpr int kDeltaChunkFloats = 2 * kDeltaTile + kDeltaChunk * kDeltaChunk + 80;
+constexpr int kDeltaPrepThreads = 256;
+
+// Token row of register r of a 32x32 FP32 MFMA accumulator in lane half kh.
+__device__ __forceinline__ int mfma32_row(int r, int kh) { return 8 * (r >> 2) + 4 * kh + (r & 3); }
+
+// One (chunk, value head) per workgroup of 4 waves.  K K^T and Q K^T are
+// two 32x32x128 products on the matrix cores (each wave one half of the
+// 128 keys of one of them); the triangular solve for W and U0 runs one
+// thread per column.
+__global__ __launch_bounds__(kDeltaPrepThreads) void delta_chunk_prep_kernel(
+    const float* __restrict__ qkv, const float* __restrict__ decay, const float* __restrict__ beta,
+    float* __restrict__ ws, int KH, int VH, int KD, int VD, int count) {
+    __shared__ __attribute__((aligned(16))) float kl[kDeltaChunk * kDeltaPitch];
+    __shared__ __attribute__((aligned(16))) float ql[kDeltaChunk * kDeltaPitch];
+    __shared__ __attribute__((aligned(16))) float vl[kDeltaChunk * kDeltaPitch];
+    __shared__ float dl[kDeltaChunk], gl[kDeltaChunk], bl[kDeltaChunk], eg[kDeltaChunk];
+    const int chunk = blockIdx.x, head = blockIdx.y;
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1), wave = t / kWave, li = lane & 31, kh = lane >> 5;
+    const int DQK = KH * KD, DQKV = 2 * DQK + VH * VD;
+    const int khead = head / (VH / KH);
+    const int r0 = chunk * kDeltaChunk;
+    const int n = min(kDeltaChunk, count - r0);
+    float* const W = ws + (static_cast<size_t>(chunk) * VH + head) * kDeltaChunkFloats;
+    float* const U0 = W + kDeltaTile;
+    float* const P = W + 2 * kDeltaTile;
+    float* const E = P + kDeltaChunk * kDeltaChunk;
+    float* const EC = E + kDeltaChunk;
+    float* const GC = EC + kDeltaChunk;
+    // k, q (key head khead) and v (value head) of the chunk's rows; zeros
+    // past the rows and past KD / VD.
+    const f32x4 zero{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int e = t; e < kDeltaChunk * 32; e += kDeltaPrepThreads) {
+        const int r = e / 32, c = 4 * (e % 32);
+        const float* row = qkv + static_cast<size_t>(r0 + r) * DQKV;
+        const bool in = r < n;
+        const f32x4 kv = in && c < KD ? *reinterpret_cast<const f32x4*>(row + DQK + khead * KD + c) : zero;
+        const f32x4 qv = in && c < KD ? *reinterpret_cast<const f32x4*>(row + khead * KD + c) : zero;
+        const f32x4 vv = in && c < VD ? *reinterpret_cast<const f32x4*>(row + 2 * DQK + head * VD + c) : zero;
+        *reinterpret_cast<f32x4*>(kl + r * kDeltaPitch + c) = kv;
+        *reinterpret_cast<f32x4*>(ql + r * kDeltaPitch + c) = qv;
+        *reinterpret_cast<f32x4*>(vl + r * kDeltaPitch + c) = vv;
+    }
+    if (t < kDeltaChunk) {
+        dl[t] = t < n ? decay[static_cast<size_t>(r0 + t) * VH + head] : 0.0f;
+        bl[t] = t < n ? beta[static_cast<size_t>(r0 + t) * VH + head] : 0.0f;
+    }
+    __syncthreads();
+    if (t < kDeltaChunk) {
+        // G_t and G_C, each added in token order.
+        float g = 0.0f, gc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kDeltaChunk; ++i) {
+            gc += dl[i];
+            if (i == t) g = gc;
+        }
+        gl[t] = g;
+        eg[t] = expf(g);
+        E[t] = eg[t];
+        EC[t] = expf(gc - g);
+        if (t == 0) GC[0] = expf(gc);
+    }
+    // K K^T (waves 0, 1) and Q K^T (waves 2, 3): k step s of wave w pairs
+    // key slots 64 kh + 32 (w % 2) + s of the lane halves.
+    f32x16 acc;
+    {
+        const int half = wave & 1;
+        const float* arow = (wave < 2 ? kl : ql) + li * kDeltaPitch + 64 * kh + 32 * half;
+        const float* brow = kl + li * kDeltaPitch + 64 * kh + 32 * half;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < 32; st += 4) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(arow + st);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(brow + st);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, acc, 0, 0, 0);
+        }
+    }
+    __syncthreads();  // every wave is done with ql: it holds the halves now
+    float* const part = ql;  // [wave][16][64]
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part[(wave * 16 + r) * kWave + lane] = acc[r];
+    __syncthreads();
+    // Entry (i, j) of register r: i = mfma32_row(r, kh), j = li.  Wave 0
+    // forms A (held in registers until ql is free again), wave 1 P.
+    float dots[16];
+    if (wave < 2) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            dots[r] = part[(2 * wave * 16 + r) * kWave + lane] + part[((2 * wave + 1) * 16 + r) * kWave + lane];
+    }
+    __syncthreads();
+    float* const al = ql;  // [32][33]
+    if (wave < 2) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = mfma32_row(r, kh), j = li;
+            const float d = j <= i ? expf(gl[i] - gl[j]) : 0.0f;
+            if (wave == 0) al[i * (kDeltaChunk + 1) + j] = j < i ? bl[i] * d * dots[r] : 0.0f;
+            else P[i * kDeltaChunk + j] = d * dots[r];
+        }
+    }
+    __syncthreads();
+    // Forward substitution, one thread per column: columns 0..127 of W
+    // (right side beta_t e^G_t k_t), 128..255 of U0 (beta_t v_t).
+    {
+        const bool wcol = t < 128;
+        const int c = t & 127;
+        const float* src = wcol ? kl : vl;
+        float x[kDeltaChunk];
+#pragma unroll
+        for (int i = 0; i < kDeltaChunk; ++i) {
+            float v = (wcol ? bl[i] * eg[i] : bl[i]) * src[i * kDeltaPitch + c];
+#pragma unroll
+            for (int j = 0; j < i; ++j) v = fmaf(-al[i * (kDeltaChunk + 1) + j], x[j], v);
+            x[i] = v;
+            // x_i is final before row i + 1's reads of A are issued, so one
+            // row of A is live at a time (not all 496 entries).
+            asm volatile("" : "+v"(x[i])::"memory");
+        }
+        float* dst = (wcol ? W : U0) + c;
+#pragma unroll
+        for (int i = 0; i < kDeltaChunk; ++i) dst[i * 128] = x[i];
+    }
+}
+
+// The chunks of one value head, in order: a workgroup per (value head,
+// 32 value columns), wave a holding the 32 x 32 block of keys 32 a .. of
+// the memory in the 32x32 MFMA accumulator layout (lane l: column l % 32,
+// keys 8 (r / 4) + 4 (l / 32) + r % 4 in register r).  That layout is also
+// the B operand of a k step pairing keys (8 (r / 4) + r % 4, + 4).  Per
+// chunk every wave forms its part of W S0 (wave 0 starting from -U0) and
+// of Q S0 with the memory as it stands; the W parts are added in LDS in
+// wave order to U = U0 - W S0 (the updates, in the accumulator layout: the
+// B operand of the next products), every wave adds a quarter of P U (its
+// four k steps) to e^G (Q_a S0), and writes that part of O to LDS, added in
+// wave order by wave 0 after the next chunk's barrier; each wave then
+// updates its block S = e^G_C S + K^T (e^(G_C - G) U).  The next chunk's
+// operands are loaded while the current chunk's run.  Blocks 8 apart run
+// on one XCD: the slices of a head are placed so, and share its operands
+// in that XCD's L2.
+constexpr int kDeltaScanWaves = 4;
+
+__global__ __launch_bounds__(kDeltaScanWaves * kWave) void delta_chunk_scan_kernel(
+    const float* __restrict__ qkv, const float* __restrict__ ws, float* __restrict__ memory,
+    float* __restrict__ out, int KH, int VH, int KD, int VD, int count) {
+    __shared__ __attribute__((aligned(16))) float red[2][2][kDeltaScanWaves][16][kWave];  // [parity][X|O][wave]
+    const int slices = VD / 32;
+    int blk = blockIdx.x;
+    if (VH % 8 == 0) {
+        const int x = blk % 8, j = blk / 8;
+        blk = ((j / slices) * 8 + x) * slices + j % slices;
+    }
+    const int head = blk / slices, slice = blk % slices;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int lane = threadIdx.x & (kWave - 1), li = lane & 31, kh = lane >> 5;
+    const bool active = wave < KD / 32;
+    const int DQK = KH * KD, DQKV = 2 * DQK + VH * VD, DO = VH * VD;
+    const int khead = head / (VH / KH);
+    const int col = slice * 32 + li;            // this lane's value column
+    const int key0 = 32 * (active ? wave : 0);  // first key of the wave's block
+    const float* const qrow = qkv + khead * KD + key0;
+    const float* const krow = qkv + DQK + khead * KD + key0 + li;
+    auto key_of = [&](int r) { return mfma32_row(r, kh); };
+    // The memory block: column `col`, keys key0 + key_of(r), four at a time.
+    float* const mcol = memory + (static_cast<size_t>(head) * VD + col) * KD + key0;
+    f32x16 S;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const f32x4 v = active ? *reinterpret_cast<const f32x4*>(mcol + 8 * q + 4 * kh) : f32x4{0, 0, 0, 0};
+        S[4 * q + 0] = v.x; S[4 * q + 1] = v.y; S[4 * q + 2] = v.z; S[4 * q + 3] = v.w;
+    }
+    // One chunk's operands in this lane's layouts.  Rows past the last
+    // token read the last token's q and k: their rows of P, W and U0 are
+    // zero, so those values meet only zeros.
+    struct Ops {
+        f32x16 w, q, k, u0, e, ec;
+        f32x4 p;
+        float gc;
+    };
+    auto load_ops = [&](int chunk, Ops& o) {
+        const float* W = ws + (static_cast<size_t>(chunk) * VH + head) * kDeltaChunkFloats;
+        const float* U0 = W + kDeltaTile;
+        const float* P = W + 2 * kDeltaTile;
+        const float* E = P + kDeltaChunk * kDeltaChunk;
+        const float* EC = E + kDeltaChunk;
+        const int r0 = chunk * kDeltaChunk;
+        const float* q = qrow + static_cast<size_t>(min(r0 + li, count - 1)) * DQKV;
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            // A operands of W S0 and Q S0: row li, keys key0 + key_of(4 qd ..).
+            const f32x4 w = *reinterpret_cast<const f32x4*>(W + li * 128 + key0 + 8 * qd + 4 * kh);
+            const f32x4 qq = *reinterpret_cast<const f32x4*>(q + 8 * qd + 4 * kh);
+            // Row scales: tokens key_of(4 qd ..).
+            const f32x4 e = *reinterpret_cast<const f32x4*>(E + 8 * qd + 4 * kh);
+            const f32x4 ec = *reinterpret_cast<const f32x4*>(EC + 8 * qd + 4 * kh);
+            o.w[4 * qd + 0] = w.x; o.w[4 * qd + 1] = w.y; o.w[4 * qd + 2] = w.z; o.w[4 * qd + 3] = w.w;
+            o.q[4 * qd + 0] = qq.x; o.q[4 * qd + 1] = qq.y; o.q[4 * qd + 2] = qq.z; o.q[4 * qd + 3] = qq.w;
+            o.e[4 * qd + 0] = e.x; o.e[4 * qd + 1] = e.y; o.e[4 * qd + 2] = e.z; o.e[4 * qd + 3] = e.w;
+            o.ec[4 * qd + 0] = ec.x; o.ec[4 * qd + 1] = ec.y; o.ec[4 * qd + 2] = ec.z; o.ec[4 * qd + 3] = ec.w;
+        }
+        // A operand of this wave's quarter of P U: row li, tokens key_of(4 wave ..).
+        o.p = *reinterpret_cast<const f32x4*>(P + li * kDeltaChunk + 8 * wave + 4 * kh);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            // A operand of K^T U: key key0 + li, token key_of(r).
+            o.k[r] = krow[static_cast<size_t>(min(r0 + key_of(r), count - 1)) * DQKV];
+        }
+        if (wave == 0) {
+            // U0 in the accumulator layout: token key_of(r), column col.
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o.u0[r] = U0[key_of(r) * 128 + col];
+        }
+        o.gc = EC[kDeltaChunk];
+    };
+    // O of chunk `chunk` from its parts in red[parity][1], added in wave order.
+    auto store_o = [&](int chunk, int parity) {
+        const int r0 = chunk * kDeltaChunk;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float y = red[parity][1][0][r][lane];
+#pragma unroll
+            for (int a = 1; a < kDeltaScanWaves; ++a) y += red[parity][1][a][r][lane];
+            const int row = r0 + key_of(r);
+            if (row < count) out[static_cast<size_t>(row) * DO + head * VD + col] = y;
+        }
+    };
+    const int chunks = (count + kDeltaChunk - 1) / kDeltaChunk;
+    auto step = [&](int ch, const Ops& cur, Ops& nxt) {
+        if (ch + 1 < chunks) load_ops(ch + 1, nxt);
+        const int par = ch & 1;
+        f32x16 X, Y;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            X[r] = wave == 0 ? -cur.u0[r] : 0.0f;
+            Y[r] = 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            X = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.w[r], S[r], X, 0, 0, 0);
+            Y = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.q[r], S[r], Y, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[par][0][wave][r][lane] = X[r];
+        __syncthreads();
+        if (ch > 0 && wave == 0) store_o(ch - 1, par ^ 1);
+        // U = U0 - W S0: minus the parts, added in wave order.
+        f32x16 U;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float x = red[par][0][0][r][lane];
+#pragma unroll
+            for (int a = 1; a < kDeltaScanWaves; ++a) x += red[par][0][a][r][lane];
+            U[r] = -x;
+        }
+        // This wave's part of O: e^G (Q_a S0) + P[:, tokens key_of(4 wave ..)] U.
+#pragma unroll
+        for (int r = 0; r < 16; ++r) Y[r] *= cur.e[r];
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if ((r >> 2) == wave) Y = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.p[r & 3], U[r], Y, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[par][1][wave][r][lane] = Y[r];
+        if (active) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                S[r] *= cur.gc;
+                U[r] *= cur.ec[r];
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) S = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.k[r], U[r], S, 0, 0, 0);
+        }
+    };
+    Ops a, b;
+    load_ops(0, a);
+    for (int ch = 0; ch < chunks; ch += 2) {
+        step(ch, a, b);
+        if (ch + 1 < chunks) step(ch + 1, b, a);
+    }
+    __syncthreads();
+    if (wave == 0) store_o(chunks - 1, (chunks - 1) & 1);
+    if (active) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<f32x4*>(mcol + 8 * q + 4 * kh) = f32x4{S[4 * q + 0], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]};
+    }
 }
 
 // One decode token of the gated delta rule (engine.cpp:262-316) in the
@@ -1289,6 +1606,10 @@ struct q3x_hip_engine {
     int *d_tokens = nullptr, *d_step = nullptr, *d_position = nullptr, *d_argmax = nullptr;
     void* moe_ws = nullptr;
     size_t moe_ws_bytes = 0;
+    // The chunked delta rule's per-(chunk, value head) operands for a chunk
+    // of rows (null: the token-by-token scan).
+    float* delta_ws = nullptr;
+    size_t delta_ws_floats = 0;
     int* h_tokens = nullptr;  // pinned staging of a forward's counters and tokens
     int token_capacity = 0;
     hipStream_t stream = nullptr;
@@ -1425,8 +1746,18 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                                    count);
                 hipLaunchKernelGGL(delta_prep_kernel, dim3(c.KH, count), dim3(128), 0, s, e.qkv, e.a, e.b, L.alog,
                                    L.dt, c.KH, c.VH, c.KD, c.VD);
-                hipLaunchKernelGGL(delta_scan_kernel, dim3(c.VH * kScanSlices), dim3(kScanThreads), 0, s, e.qkv,
-                                   e.a, e.b, L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD, count);
+                if (e.delta_ws) {
+                    // The recurrence in chunks on the matrix cores.
+                    hipLaunchKernelGGL(delta_chunk_prep_kernel, dim3((count + kDeltaChunk - 1) / kDeltaChunk, c.VH),
+                                       dim3(kDeltaPrepThreads), 0, s, e.qkv, e.a, e.b, e.delta_ws, c.KH, c.VH, c.KD,
+                                       c.VD, count);
+                    hipLaunchKernelGGL(delta_chunk_scan_kernel, dim3(c.VH * (c.VD / 32)),
+                                       dim3(kDeltaScanWaves * kWave), 0, s, e.qkv, e.delta_ws, L.memory,
+                                       e.delta_out, c.KH, c.VH, c.KD, c.VD, count);
+                } else {
+                    hipLaunchKernelGGL(delta_scan_kernel, dim3(c.VH * kScanSlices), dim3(kScanThreads), 0, s,
+                                       e.qkv, e.a, e.b, L.memory, e.delta_out, c.KH, c.VH, c.KD, c.VD, count);
+                }
                 hipLaunchKernelGGL(delta_norm_kernel, dim3(c.VH, count), dim3(128), 0, s, e.delta_out, e.z, L.norm,
                                    c.VH, c.VD);
                 rc = apply(L.out, type, e.delta_out, count, e.hidden, true, s);
@@ -1632,6 +1963,10 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
         e->moe_ws_bytes = std::max(q3x_hip_moe_layer_workspace_bytes(&e->layers[0].moe, 1),
                                    q3x_hip_moe_layer_workspace_bytes(&e->layers[0].moe, static_cast<int>(R)));
     e->token_capacity = context;
+    // The chunked delta rule takes key and value heads of whole 32-wide
+    // blocks (every model of the family: 128); others run the token scan.
+    if (c.VH > 0 && c.KD % 32 == 0 && c.VD % 32 == 0)
+        e->delta_ws_floats = (R + kDeltaChunk - 1) / kDeltaChunk * c.VH * static_cast<size_t>(kDeltaChunkFloats);
     // One arena: the work rows of a chunk, the recurrent state and its
     // checkpoint, the KV caches, the logits, the token list and counters.
     // plan(base) carves it; plan(nullptr) only measures it.
@@ -1685,6 +2020,7 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
         e->d_tokens = e->d_step + 2;
         e->d_argmax = reinterpret_cast<int*>(take(1, 4));
         e->moe_ws = e->moe_ws_bytes ? take(e->moe_ws_bytes, 1) : nullptr;
+        e->delta_ws = e->delta_ws_floats ? f(e->delta_ws_floats) : nullptr;
         return at;
     };
     const size_t total = plan(nullptr);

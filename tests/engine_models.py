@@ -28,6 +28,9 @@ CONFIGS = {
     # zero-padded key and value slots in the scans, the gated norm over heads
     # that are not 128 wide, an output projection 288 columns wide
     "narrow_q4": dict(BASE, id=6, matrix_type=Q4_0, KD=64, VD=96, KH=1, VH=3),
+    # head sizes that are not multiples of 32 (KD = 48, VD = 80): the prefill
+    # recurrence runs token by token instead of in chunks on the matrix cores
+    "odd_q8": dict(BASE, id=7, matrix_type=Q8_0, KD=48, VD=80, KH=2, VH=4),
 }
 
 

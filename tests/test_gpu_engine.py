@@ -48,12 +48,13 @@ def test_engine_logits_match_the_reference_forward(name):
 
 @pytest.mark.parametrize("name,prompt,chunk", [("dense_q8", 40, 0), ("dense_q4", 530, 256), ("moe_q4", 300, 0),
                                                ("moe_q8_tied", 64, 48), ("gqa8_q8", 100, 0), ("dense_q8", 333, 100),
-                                               ("gqa8_q8", 2100, 0), ("narrow_q4", 300, 128),
+                                               ("gqa8_q8", 2100, 0), ("narrow_q4", 300, 128), ("odd_q8", 300, 0),
                                                ("gqa8_q8", 4200, 0), ("dense_q8", 8300, 0)])
 def test_prefill_then_decode_match_the_reference_forward(name, prompt, chunk):
-    # A forward of many tokens runs them as prefill chunks (GEMMs, the
-    # recurrences token by token inside one launch, attention on the matrix
-    # cores); its logits, and those of the decode steps that follow, against
+    # A forward of many tokens runs them as prefill chunks (GEMMs, the delta
+    # rule in 32-token chunks on the matrix cores -- token by token for the
+    # odd head sizes -- attention on the matrix cores); its logits, and
+    # those of the decode steps that follow, against
     # the reference's token-by-token forward.  Chunks of 256, 48 and 100 rows
     # put chunk boundaries inside the prompts, and tiles of 32 query rows
     # end partly filled; 2100 tokens cross the default 2048-row chunk with
