@@ -598,7 +598,8 @@ __global__ __launch_bounds__(kDeltaPrepThreads) void delta_chunk_prep_kernel(
 // wave order to U = U0 - W S0 (the updates, in the accumulator layout: the
 // B operand of the next products), every wave adds a quarter of P U (its
 // four k steps) to e^G (Q_a S0), and writes that part of O to LDS, added in
-// wave order by wave 0 after the next chunk's barrier; each wave then
+// wave order after the next chunk's barrier (each wave stores a quarter of
+// the rows); each wave then
 // updates its block S = e^G_C S + K^T (e^(G_C - G) U).  The next chunk's
 // operands are loaded while the current chunk's run.  Blocks 8 apart run
 // on one XCD: the slices of a head are placed so, and share its operands
@@ -638,9 +639,9 @@ __global__ __launch_bounds__(kDeltaScanWaves * kWave) void delta_chunk_scan_kern
     // token read the last token's q and k: their rows of P, W and U0 are
     // zero, so those values meet only zeros.
     struct Ops {
-        f32x16 w, q, k, u0, e, ec;
+        f32x16 w, q, k, u0, ec;
         f32x4 p;
-        float gc;
+        float el, gc;  // e^G of token li, e^G_C
     };
     auto load_ops = [&](int chunk, Ops& o) {
         const float* W = ws + (static_cast<size_t>(chunk) * VH + head) * kDeltaChunkFloats;
@@ -655,12 +656,10 @@ __global__ __launch_bounds__(kDeltaScanWaves * kWave) void delta_chunk_scan_kern
             // A operands of W S0 and Q S0: row li, keys key0 + key_of(4 qd ..).
             const f32x4 w = *reinterpret_cast<const f32x4*>(W + li * 128 + key0 + 8 * qd + 4 * kh);
             const f32x4 qq = *reinterpret_cast<const f32x4*>(q + 8 * qd + 4 * kh);
-            // Row scales: tokens key_of(4 qd ..).
-            const f32x4 e = *reinterpret_cast<const f32x4*>(E + 8 * qd + 4 * kh);
+            // Update scales: tokens key_of(4 qd ..).
             const f32x4 ec = *reinterpret_cast<const f32x4*>(EC + 8 * qd + 4 * kh);
             o.w[4 * qd + 0] = w.x; o.w[4 * qd + 1] = w.y; o.w[4 * qd + 2] = w.z; o.w[4 * qd + 3] = w.w;
             o.q[4 * qd + 0] = qq.x; o.q[4 * qd + 1] = qq.y; o.q[4 * qd + 2] = qq.z; o.q[4 * qd + 3] = qq.w;
-            o.e[4 * qd + 0] = e.x; o.e[4 * qd + 1] = e.y; o.e[4 * qd + 2] = e.z; o.e[4 * qd + 3] = e.w;
             o.ec[4 * qd + 0] = ec.x; o.ec[4 * qd + 1] = ec.y; o.ec[4 * qd + 2] = ec.z; o.ec[4 * qd + 3] = ec.w;
         }
         // A operand of this wave's quarter of P U: row li, tokens key_of(4 wave ..).
@@ -670,28 +669,34 @@ __global__ __launch_bounds__(kDeltaScanWaves * kWave) void delta_chunk_scan_kern
             // A operand of K^T U: key key0 + li, token key_of(r).
             o.k[r] = krow[static_cast<size_t>(min(r0 + key_of(r), count - 1)) * DQKV];
         }
-        if (wave == 0) {
-            // U0 in the accumulator layout: token key_of(r), column col.
+        // U0 in the accumulator layout: token key_of(r), column col (every
+        // wave loads it, wave 0 uses it: no branch around the loads, whose
+        // waits would then cover the prefetch as well).
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o.u0[r] = U0[key_of(r) * 128 + col];
-        }
+        for (int r = 0; r < 16; ++r) o.u0[r] = U0[key_of(r) * 128 + col];
+        o.el = E[li];
         o.gc = EC[kDeltaChunk];
     };
-    // O of chunk `chunk` from its parts in red[parity][1], added in wave order.
+    // Rows key_of(4 wave ..) of O of chunk `chunk`, from its parts in
+    // red[parity][1] added in wave order (each wave stores a quarter).  The
+    // stores go through a buffer resource that ends at the last row, so rows
+    // past it are dropped without a branch.
     auto store_o = [&](int chunk, int parity) {
         const int r0 = chunk * kDeltaChunk;
+        const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
+            out + static_cast<size_t>(r0) * DO, 0, min(kDeltaChunk, count - r0) * DO * 4, kBufferFlags);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            float y = red[parity][1][0][r][lane];
+        for (int e = 0; e < 4; ++e) {
+            float y = red[parity][1][0][4 * wave + e][lane];
 #pragma unroll
-            for (int a = 1; a < kDeltaScanWaves; ++a) y += red[parity][1][a][r][lane];
-            const int row = r0 + key_of(r);
-            if (row < count) out[static_cast<size_t>(row) * DO + head * VD + col] = y;
+            for (int a = 1; a < kDeltaScanWaves; ++a) y += red[parity][1][a][4 * wave + e][lane];
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rows,
+                                                  4 * (key_of(4 * wave + e) * DO + head * VD + col), 0, 0);
         }
     };
     const int chunks = (count + kDeltaChunk - 1) / kDeltaChunk;
     auto step = [&](int ch, const Ops& cur, Ops& nxt) {
-        if (ch + 1 < chunks) load_ops(ch + 1, nxt);
+        load_ops(min(ch + 1, chunks - 1), nxt);  // unconditional: see U0 above
         const int par = ch & 1;
         f32x16 X, Y;
 #pragma unroll
@@ -699,15 +704,16 @@ __global__ __launch_bounds__(kDeltaScanWaves * kWave) void delta_chunk_scan_kern
             X[r] = wave == 0 ? -cur.u0[r] : 0.0f;
             Y[r] = 0.0f;
         }
+        // e^G (Q S0) with e^G_li on the A operand's row li.
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             X = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.w[r], S[r], X, 0, 0, 0);
-            Y = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.q[r], S[r], Y, 0, 0, 0);
+            Y = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.q[r] * cur.el, S[r], Y, 0, 0, 0);
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) red[par][0][wave][r][lane] = X[r];
         __syncthreads();
-        if (ch > 0 && wave == 0) store_o(ch - 1, par ^ 1);
+        if (ch > 0) store_o(ch - 1, par ^ 1);
         // U = U0 - W S0: minus the parts, added in wave order.
         f32x16 U;
 #pragma unroll
@@ -718,8 +724,6 @@ __global__ __launch_bounds__(kDeltaScanWaves * kWave) void delta_chunk_scan_kern
             U[r] = -x;
         }
         // This wave's part of O: e^G (Q_a S0) + P[:, tokens key_of(4 wave ..)] U.
-#pragma unroll
-        for (int r = 0; r < 16; ++r) Y[r] *= cur.e[r];
 #pragma unroll
         for (int r = 0; r < 16; ++r)
             if ((r >> 2) == wave) Y = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.p[r & 3], U[r], Y, 0, 0, 0);
@@ -742,7 +746,7 @@ __global__ __launch_bounds__(kDeltaScanWaves * kWave) void delta_chunk_scan_kern
         if (ch + 1 < chunks) step(ch + 1, b, a);
     }
     __syncthreads();
-    if (wave == 0) store_o(chunks - 1, (chunks - 1) & 1);
+    store_o(chunks - 1, (chunks - 1) & 1);
     if (active) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
