@@ -21,6 +21,21 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Accesses of global memory through a pointer the compiler cannot trace to
+// a kernel argument (a table entry picked at run time).  A plain access
+// would be a flat instruction, which may address LDS as well as memory: the
+// compiler then counts it in both wait counters and, with one in flight,
+// waits for every outstanding load where it needs only the oldest (a
+// prefetch ring then has nothing in flight across the loop's back edge).
+__device__ __forceinline__ float load_global(const float* p) {
+    typedef const __attribute__((address_space(1))) float GlobalFloat;
+    return *(GlobalFloat*)p;
+}
+__device__ __forceinline__ void store_global(float* p, float v) {
+    typedef __attribute__((address_space(1))) float GlobalFloat;
+    *(GlobalFloat*)p = v;
+}
+
 __host__ __device__ constexpr int block_bytes(uint32_t type) {
     return type == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
 }

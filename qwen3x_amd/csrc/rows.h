@@ -51,8 +51,8 @@ struct OneMatrix {
     __device__ const uint8_t* row(int r) const { return w ? w + static_cast<size_t>(r) * row_bytes : nullptr; }
     __device__ const uint8_t* any() const { return any_w; }
     __device__ const float* input(int) const { return x; }
-    __device__ float previous(int r) const { return accumulate ? y[r] : 0.0f; }
-    __device__ void store(int r, float v) const { y[r] = silu ? silu_ref(v) : v; }
+    __device__ float previous(int r) const { return accumulate ? load_global(y + r) : 0.0f; }
+    __device__ void store(int r, float v) const { store_global(y + r, silu ? silu_ref(v) : v); }
 };
 
 // Up to Q3X_HIP_MV_MULTI_MAX matrices of one type and width that read the
@@ -231,7 +231,7 @@ struct GateUpPairs {
     __device__ const float* input(int) const { return x; }
     __device__ void store_pair(int v_gate, float gate_dot, float up_dot) const {
         const int q = pair(v_gate);
-        if (q < I) h[q] = silu_ref(gate_dot) * up_dot;
+        if (q < I) store_global(h + q, silu_ref(gate_dot) * up_dot);
     }
 };
 
