@@ -366,6 +366,29 @@ def cpu_matvecs(cpu, mats, seconds):
     return cpu_median(one_pass, seconds)
 
 
+def gemm_entry(torch, q3x, mats, X, H, Ys, count, ms_plain, flops, replays):
+    """A GEMM config's line: q3x_hip_gemm_ws with the workspace its plan asks
+    for (K split over workgroups where few tiles meet a long K) when any
+    matrix splits, q3x_hip_gemm beside it; otherwise q3x_hip_gemm alone."""
+    plain = {"TFLOPs": flops / (ms_plain * 1e-3) / 1e12, "ms": ms_plain,
+             "frac_x3_peak": flops / (ms_plain * 1e-3) / 1e12 / X3_PEAK_TFLOPS}
+    need = max(q3x.gemm_workspace_bytes(mm.linear, count) for mm in mats)
+    if need == 0:
+        return plain
+    ws = torch.empty(need // 4, dtype=torch.float32, device="cuda")
+
+    def run(i):
+        for mm in mats:
+            q3x.batch_mv_ws(mm.linear, H if mm.name == "down" else X, Ys[mm.name], count, ws)
+    ms = time_graph(torch, run, 1, replays)
+    del ws
+    return {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms, "frac_x3_peak": flops / (ms * 1e-3) / 1e12 / X3_PEAK_TFLOPS,
+            "workspace_bytes": need, "split_k": {mm.name: q3x.gemm_workspace_bytes(mm.linear, count) > 0 for mm in mats},
+            "no_workspace": plain,
+            "note": "q3x_hip_gemm_ws with the workspace its plan asks for (the matrices marked split_k run K over "
+                    "several workgroups and a fixup launch); no_workspace: q3x_hip_gemm"}
+
+
 def extra_configs(torch, q3x, wl, only=None, cpu=False):
     out = {}
     want = (lambda c: only is None or c in only)
@@ -398,8 +421,8 @@ def extra_configs(torch, q3x, wl, only=None, cpu=False):
                     q3x.batch_mv(mm.linear, H if mm.name == "down" else X, Ys[mm.name], count)
             ms = time_graph(torch, run, 1, 4 if count == 4096 else 10)
             flops = sum(2.0 * count * mm.rows * mm.cols for mm in mats)
-            out[f"cfg2_q8_gemm_N{count}"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
-                                             "frac_x3_peak": flops / (ms * 1e-3) / 1e12 / X3_PEAK_TFLOPS}
+            out[f"cfg2_q8_gemm_N{count}"] = gemm_entry(torch, q3x, mats, X, H, Ys, count, ms, flops,
+                                                       4 if count == 4096 else 10)
             del X, H, Ys
         if ref_cpu:
             # one token through gate, up and down, the reference's prefill unit
@@ -461,8 +484,7 @@ def extra_configs(torch, q3x, wl, only=None, cpu=False):
                 q3x.batch_mv(mm.linear, H if mm.name == "down" else X, Ys[mm.name], 512)
         ms = time_graph(torch, run_gemm, 1, 10)
         flops = sum(2.0 * 512 * mm.rows * mm.cols for mm in mats)
-        out["cfg3_q4_gemm_N512"] = {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms,
-                                    "frac_x3_peak": flops / (ms * 1e-3) / 1e12 / X3_PEAK_TFLOPS}
+        out["cfg3_q4_gemm_N512"] = gemm_entry(torch, q3x, mats, X, H, Ys, 512, ms, flops, 10)
         if ref_cpu:
             t, reps = cpu_matvecs(ref_cpu, mats, 2.0)
             out["cfg3_q4_mv_27b_ffn"]["cpu_baseline"] = ref_cpu.entry(

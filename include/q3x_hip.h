@@ -98,6 +98,22 @@ int q3x_hip_gemm(const void* w, uint32_t type, int rows, int cols,
                  const float* X, int count, float* Y, int accumulate,
                  hipStream_t stream);
 
+/* Bytes of caller-owned workspace with which q3x_hip_gemm_ws splits the K
+ * dimension of this GEMM over workgroups (0: it would not split).  For the
+ * same shape and arguments as q3x_hip_gemm, with a workspace of at least
+ * q3x_hip_gemm_workspace_bytes(type, rows, cols, count) bytes (16-byte
+ * aligned; smaller or null runs q3x_hip_gemm's launch): a launch of few
+ * output tiles over a long K (e.g. 512 tokens x 5120 rows x 17408 columns)
+ * then fills the chip, each tile's K ranges summed by a second launch in K
+ * order.  Deterministic; the sums run in another order than q3x_hip_gemm's,
+ * within the same tolerance against the reference.  Same role as
+ * q3x_hip_gemm (batch_mv, arch/cuda/engine.cu:1568); no counterpart of its
+ * own in the reference. */
+size_t q3x_hip_gemm_workspace_bytes(uint32_t type, int rows, int cols, int count);
+int q3x_hip_gemm_ws(const void* w, uint32_t type, int rows, int cols,
+                    const float* X, int count, float* Y, int accumulate,
+                    void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* out[nrows, cols] = dequantised rows [row0, row0 + nrows) of W, bit-exact
  * with the reference's embed (arch/cpu.cpp:55-63, 81-90; CUDA embed_q8_kernel
  * / embed_q4_kernel engine.cu:490-517, batch_embed_q8_kernel :701). */

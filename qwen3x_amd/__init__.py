@@ -54,6 +54,8 @@ SIGNATURES = {
     "q3x_hip_mv": (_I, [_P, _U, _I, _I, _P, _P, _I, _P]),
     "q3x_hip_mv_multi": (_I, [_P, _I, _U, _I, _P, _P]),
     "q3x_hip_gemm": (_I, [_P, _U, _I, _I, _P, _I, _P, _I, _P]),
+    "q3x_hip_gemm_workspace_bytes": (_S, [_U, _I, _I, _I]),
+    "q3x_hip_gemm_ws": (_I, [_P, _U, _I, _I, _P, _I, _P, _I, _P, _S, _P]),
     "q3x_hip_dequant": (_I, [_P, _U, _I, _I, _I, _P, _P]),
     "q3x_hip_router_topk": (_I, [_P, _I, _I, _I, _P, _P, _P]),
     "q3x_hip_moe_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),
@@ -270,6 +272,25 @@ def batch_mv(linear: Linear, X, Y, count: int, add: bool = False, stream=None):
     _need_device(linear.weight, X, Y)
     _check("q3x_hip_gemm", lib().q3x_hip_gemm(_ptr(linear.weight), linear.type, linear.rows, linear.columns,
                                               _ptr(X), count, _ptr(Y), int(add), _stream(stream)))
+    return Y
+
+
+def gemm_workspace_bytes(linear: Linear, count: int) -> int:
+    """Bytes of workspace with which batch_mv_ws splits K over workgroups
+    for `count` tokens (0: no split)."""
+    return int(lib().q3x_hip_gemm_workspace_bytes(linear.type, linear.rows, linear.columns, count))
+
+
+def batch_mv_ws(linear: Linear, X, Y, count: int, workspace, add: bool = False, stream=None):
+    """batch_mv with a workspace (a device tensor of at least
+    gemm_workspace_bytes(linear, count) bytes, or None)."""
+    _need_device(linear.weight, X, Y)
+    ws, nbytes = (0, 0) if workspace is None else (_ptr(workspace), workspace.numel() * workspace.element_size())
+    if workspace is not None:
+        _need_device(workspace)
+    _check("q3x_hip_gemm_ws", lib().q3x_hip_gemm_ws(_ptr(linear.weight), linear.type, linear.rows, linear.columns,
+                                                    _ptr(X), count, _ptr(Y), int(add), ws, nbytes,
+                                                    _stream(stream)))
     return Y
 
 

@@ -994,6 +994,7 @@ __device__ __forceinline__ float transpose_sum64(float (&v)[64]) {
 constexpr int kAttnSplits = 128;  // ranges per KV head for a decode step
 constexpr int kMaxGroup = 8;
 constexpr int kChunk = 2048;     // default rows of a prefill chunk
+constexpr size_t kGemmScratchMax = static_cast<size_t>(512) << 20;  // K-split partial sums, at most
 
 template <int GP>
 __global__ __launch_bounds__(kHeadThreads) void attention_kernel(
@@ -1611,9 +1612,12 @@ struct q3x_hip_engine {
     void* moe_ws = nullptr;
     size_t moe_ws_bytes = 0;
     // The chunked delta rule's per-(chunk, value head) operands for a chunk
-    // of rows (null: the token-by-token scan).
+    // of rows (null: the token-by-token scan), and the prefill GEMMs' K-split
+    // partial sums, in one scratch region (never in use at once).
     float* delta_ws = nullptr;
     size_t delta_ws_floats = 0;
+    void* scratch = nullptr;
+    size_t gemm_ws_bytes = 0;
     int* h_tokens = nullptr;  // pinned staging of a forward's counters and tokens
     int token_capacity = 0;
     hipStream_t stream = nullptr;
@@ -1629,25 +1633,34 @@ T* carve(uint8_t*& cursor, size_t count) {
     return p;
 }
 
+// A prefill GEMM's workspace (its K split's partial sums): the engine's
+// scratch region, shared with the chunked delta rule's operands (their uses
+// never overlap on the engine's one stream).
+struct GemmScratch {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+
 // One matrix applied to `count` rows of x: the matvec for a decode step, the
 // prefill GEMM for a chunk.
-int apply(const Mat& m, uint32_t type, const float* x, int count, float* y, bool accumulate, hipStream_t s) {
+int apply(const Mat& m, uint32_t type, const float* x, int count, float* y, bool accumulate, hipStream_t s,
+          GemmScratch ws = {}) {
     if (count == 1) return q3x_hip_mv(m.w, type, m.rows, m.cols, x, y, accumulate ? 1 : 0, s);
-    return q3x_hip_gemm(m.w, type, m.rows, m.cols, x, count, y, accumulate ? 1 : 0, s);
+    return q3x_hip_gemm_ws(m.w, type, m.rows, m.cols, x, count, y, accumulate ? 1 : 0, ws.p, ws.bytes, s);
 }
 
 // Several matrices of width `cols` applied to the same rows: one multi-matrix
 // launch for a decode step (the reference's projection helpers,
 // engine.cu:1599-1661), one GEMM each for a chunk.
 int apply_group(const Mat* m, float* const* y, int n, uint32_t type, int cols, const float* x, int count,
-                hipStream_t s) {
+                hipStream_t s, GemmScratch ws = {}) {
     if (count == 1) {
         q3x_hip_mv_item items[Q3X_HIP_MV_MULTI_MAX];
         for (int i = 0; i < n; ++i) items[i] = q3x_hip_mv_item{m[i].w, m[i].rows, y[i], 0};
         return q3x_hip_mv_multi(items, n, type, cols, x, s);
     }
     for (int i = 0; i < n; ++i) {
-        const int rc = q3x_hip_gemm(m[i].w, type, m[i].rows, cols, x, count, y[i], 0, s);
+        const int rc = q3x_hip_gemm_ws(m[i].w, type, m[i].rows, cols, x, count, y[i], 0, ws.p, ws.bytes, s);
         if (rc) return rc;
     }
     return Q3X_HIP_OK;
@@ -1697,6 +1710,7 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
     hipStream_t s = e.stream;
     const int DO = c.VH * c.VD, DQKV = 2 * c.KH * c.KD + DO;
     const uint32_t type = c.matrix_type;
+    const GemmScratch gemm_ws{e.scratch, e.gemm_ws_bytes};
     const dim3 eg((c.H + 255) / 256, count);
     if (type == Q3X_HIP_MATRIX_Q8_0)
         hipLaunchKernelGGL(embed_kernel<Q3X_HIP_MATRIX_Q8_0>, eg, dim3(256), 0, s,
@@ -1723,7 +1737,7 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
         if (rc == Q3X_HIP_ENOTSUP) {
             hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden,
                                pending ? e.branch : nullptr, L.input_norm, c.H, e.normalized);
-            rc = apply_group(proj, proj_out, nproj, type, c.H, e.normalized, count, s);
+            rc = apply_group(proj, proj_out, nproj, type, c.H, e.normalized, count, s, gemm_ws);
         }
         if (rc) break;
         if (!L.attention) {
@@ -1742,7 +1756,7 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                 if (rc == Q3X_HIP_ENOTSUP) {
                     hipLaunchKernelGGL(delta_norm_kernel, dim3(c.VH, 1), dim3(128), 0, s, e.delta_out, e.z, L.norm,
                                        c.VH, c.VD);
-                    rc = apply(L.out, type, e.delta_out, count, e.hidden, true, s);
+                    rc = apply(L.out, type, e.delta_out, count, e.hidden, true, s, gemm_ws);
                 }
             } else {
                 hipLaunchKernelGGL(delta_conv_kernel<16>, dim3((DQKV + kConvThreads / 16 - 1) / (kConvThreads / 16)),
@@ -1764,7 +1778,7 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                 }
                 hipLaunchKernelGGL(delta_norm_kernel, dim3(c.VH, count), dim3(128), 0, s, e.delta_out, e.z, L.norm,
                                    c.VH, c.VD);
-                rc = apply(L.out, type, e.delta_out, count, e.hidden, true, s);
+                rc = apply(L.out, type, e.delta_out, count, e.hidden, true, s, gemm_ws);
             }
         } else {
             hipLaunchKernelGGL(attention_prep_kernel, dim3(c.AH + c.KVH, count), dim3(kHeadThreads), 0, s,
@@ -1783,7 +1797,7 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                                    dim3(kFlashWaves * kWave), kFlashLds, s, e.query, e.gate, L.key_cache,
                                    L.value_cache, e.d_position, e.attn_out, c.AH, c.KVH, c.AD, count);
             }
-            rc = apply(L.o, type, e.attn_out, count, e.hidden, true, s);
+            rc = apply(L.o, type, e.attn_out, count, e.hidden, true, s, gemm_ws);
         }
         if (rc) break;
         if (c.experts) {
@@ -1810,7 +1824,7 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
             if (rc == Q3X_HIP_ENOTSUP) {
                 hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden, nullptr,
                                    L.post_norm, c.H, e.normalized);
-                rc = apply_group(gate_up, ffn, 2, type, c.H, e.normalized, count, s);
+                rc = apply_group(gate_up, ffn, 2, type, c.H, e.normalized, count, s, gemm_ws);
             }
             if (rc) break;
             const bool add = true;
@@ -1823,7 +1837,7 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                     hipLaunchKernelGGL(product_kernel, dim3((n + 255) / 256), dim3(256), 0, s, e.ffn_gate, e.ffn_up, n);
                 else
                     hipLaunchKernelGGL(swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, s, e.ffn_gate, e.ffn_up, n);
-                rc = apply(L.down, type, e.ffn_gate, count, e.hidden, true, s);
+                rc = apply(L.down, type, e.ffn_gate, count, e.hidden, true, s, gemm_ws);
             }
             pending = false;
         }
@@ -1971,6 +1985,24 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
     // blocks (every model of the family: 128); others run the token scan.
     if (c.VH > 0 && c.KD % 32 == 0 && c.VD % 32 == 0)
         e->delta_ws_floats = (R + kDeltaChunk - 1) / kDeltaChunk * c.VH * static_cast<size_t>(kDeltaChunkFloats);
+    // The prefill GEMMs' K splits: the most any of the chunk's GEMMs asks
+    // for at any row count up to a chunk (a call given less runs unsplit),
+    // within kGemmScratchMax.
+    if (R > 1) {
+        auto need = [&](const Mat& m) {
+            size_t most = 0;
+            if (!m.w) return most;
+            for (size_t n = 64; n < R + 64; n += 64) {
+                const int count = static_cast<int>(std::min(n, R));
+                most = std::max(most, q3x_hip_gemm_workspace_bytes(c.matrix_type, m.rows, m.cols, count));
+            }
+            return most;
+        };
+        for (const LayerWeights& L : e->layers)
+            for (const Mat* m : {&L.qkv, &L.z, &L.a, &L.b, &L.out, &L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down})
+                e->gemm_ws_bytes = std::max(e->gemm_ws_bytes, need(*m));
+        if (e->gemm_ws_bytes > kGemmScratchMax) e->gemm_ws_bytes = kGemmScratchMax;
+    }
     // One arena: the work rows of a chunk, the recurrent state and its
     // checkpoint, the KV caches, the logits, the token list and counters.
     // plan(base) carves it; plan(nullptr) only measures it.
@@ -2024,7 +2056,9 @@ extern "C" int q3x_hip_engine_create(const q3x_hip_model_config* config, const v
         e->d_tokens = e->d_step + 2;
         e->d_argmax = reinterpret_cast<int*>(take(1, 4));
         e->moe_ws = e->moe_ws_bytes ? take(e->moe_ws_bytes, 1) : nullptr;
-        e->delta_ws = e->delta_ws_floats ? f(e->delta_ws_floats) : nullptr;
+        const size_t scratch = std::max(e->delta_ws_floats * sizeof(float), e->gemm_ws_bytes);
+        e->scratch = scratch ? take(scratch, 1) : nullptr;
+        e->delta_ws = e->delta_ws_floats ? static_cast<float*>(e->scratch) : nullptr;
         return at;
     };
     const size_t total = plan(nullptr);

@@ -25,6 +25,8 @@ struct DenseGemm {
     float* Y;
     int rows;
     bool accumulate;
+    int ksplit = 1;         // units per tile over K (set by the launch)
+    float* part = nullptr;  // their partial sums (caller's workspace)
     __device__ bool tile(int ty, int bm, GemmTile& t) const {
         t.m0 = ty * bm;
         t.mcount = min(bm, count - t.m0);
@@ -49,12 +51,15 @@ struct DenseGemm {
 
 using namespace q3x;
 
-extern "C" int q3x_hip_gemm(const void* w, uint32_t type, int rows, int cols, const float* X,
-                            int count, float* Y, int accumulate, hipStream_t stream) {
+namespace {
+
+int gemm(const void* w, uint32_t type, int rows, int cols, const float* X, int count, float* Y, int accumulate,
+         void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (type == Q3X_HIP_MATRIX_BF16) return Q3X_HIP_ENOTSUP;
     size_t bytes;
     if (!w || !X || !Y || count <= 0 || !quantized_size(type, rows, cols, &bytes))
         return Q3X_HIP_EINVAL;
+    if (workspace_bytes > 0 && !workspace) return Q3X_HIP_EINVAL;
     const int bpr = cols / kBlock;
     const size_t row_bytes = static_cast<size_t>(bpr) * block_bytes(type);
     if (!aligned(w, 2) || !aligned(X, 16) || !aligned(Y, 4)) {
@@ -67,7 +72,31 @@ extern "C" int q3x_hip_gemm(const void* w, uint32_t type, int rows, int cols, co
         }
         return Q3X_HIP_OK;
     }
-    DenseGemm g{0, X, cols, count, static_cast<const uint8_t*>(w), row_bytes, Y, rows, accumulate != 0};
-    return type == Q3X_HIP_MATRIX_Q8_0 ? launch_x3<Q3X_HIP_MATRIX_Q8_0>(g, rows, count, cols, stream)
-                                       : launch_x3<Q3X_HIP_MATRIX_Q4_0>(g, rows, count, cols, stream);
+    // The split plan runs only with all of the workspace it asks for (16-byte
+    // aligned); otherwise q3x_hip_gemm's plan.
+    const size_t need = x3_plan(rows, count, cols, false, SIZE_MAX).workspace_bytes();
+    const size_t usable = need > 0 && aligned(workspace, 16) && workspace_bytes >= need ? need : 0;
+    DenseGemm g{0, X, cols, count, static_cast<const uint8_t*>(w), row_bytes, Y, rows, accumulate != 0, 1,
+                static_cast<float*>(workspace)};
+    return type == Q3X_HIP_MATRIX_Q8_0 ? launch_x3<Q3X_HIP_MATRIX_Q8_0>(g, rows, count, cols, stream, usable)
+                                       : launch_x3<Q3X_HIP_MATRIX_Q4_0>(g, rows, count, cols, stream, usable);
+}
+
+}  // namespace
+
+extern "C" int q3x_hip_gemm(const void* w, uint32_t type, int rows, int cols, const float* X,
+                            int count, float* Y, int accumulate, hipStream_t stream) {
+    return gemm(w, type, rows, cols, X, count, Y, accumulate, nullptr, 0, stream);
+}
+
+extern "C" size_t q3x_hip_gemm_workspace_bytes(uint32_t type, int rows, int cols, int count) {
+    size_t bytes;
+    if (type == Q3X_HIP_MATRIX_BF16 || count <= 0 || !quantized_size(type, rows, cols, &bytes)) return 0;
+    return x3_plan(rows, count, cols, false, SIZE_MAX).workspace_bytes();
+}
+
+extern "C" int q3x_hip_gemm_ws(const void* w, uint32_t type, int rows, int cols, const float* X, int count,
+                               float* Y, int accumulate, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream) {
+    return gemm(w, type, rows, cols, X, count, Y, accumulate, workspace, workspace_bytes, stream);
 }

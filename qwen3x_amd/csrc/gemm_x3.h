@@ -79,6 +79,62 @@ __device__ __forceinline__ void split3(float a, uint32_t& h1, uint32_t& h2, uint
     h3 = __float_as_uint(r - __uint_as_float(h2));
 }
 
+// K split over workgroups (policies with ksplit and part members, e.g. a
+// GEMM given a workspace): the launch has ksplit units per tile, unit s
+// taking the tile's K blocks [s * per, (s + 1) * per), per = ceil(blocks /
+// ksplit); each unit writes its sums, as its threads hold them, to its slot
+// of `part`, and gemm_x3_fixup_kernel adds a tile's units in K order and
+// stores.  So a launch of few tiles over long K (512 tokens x 5120 rows x
+// 17408 columns is 80 tiles of 128 x 256 for 256 CUs) fills the chip;
+// results are deterministic, their sums in another order than unsplit.
+template <class P, class = void>
+struct KSplit {
+    __device__ static int count(const P&) { return 1; }
+    __device__ static float* part(const P&) { return nullptr; }
+};
+template <class P>
+struct KSplit<P, decltype(void(std::declval<const P&>().ksplit))> {
+    __device__ static int count(const P& p) { return p.ksplit; }
+    __device__ static float* part(const P& p) { return p.part; }
+};
+
+// Floats of one unit's partial sums: every thread's SM x SN x 4 values.
+template <int WM, int WN, int SM, int SN>
+constexpr size_t x3_unit_floats() { return static_cast<size_t>(SM) * SN * 4 * WM * WN * kWave; }
+
+// The tile's stores: output block (i, j) of wave (wm, wn), lane rows
+// 4 g16 + e, column l16.
+template <int WM, int WN, int SM, int SN, class Policy>
+__device__ __forceinline__ void x3_store(const Policy& pol, const GemmTile& tile, int n0, int rows, int wm,
+                                         int wn, int l16, int g16, int nsub, const f32x4 (&acc)[SM][SN]) {
+#pragma unroll
+    for (int i = 0; i < SM; ++i) {
+        if (i >= nsub) break;
+        const int row0 = 16 * (i * WM + wm);
+#pragma unroll
+        for (int j = 0; j < SN; ++j) {
+            const int n = n0 + (wn * SN + j) * 16 + l16;
+            if constexpr (Policy::kPairedColumns) {
+                // Column blocks 2s and 2s + 1 hold columns q and q + 16 of a
+                // 32-column group (e.g. gate and up of one output feature).
+                if (j % 2 == 1) continue;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = row0 + 4 * g16 + e;
+                    if (m < tile.mcount && n < rows) pol.store_pair(tile, m, n, acc[i][j][e], acc[i][j + 1][e]);
+                }
+            } else {
+                if (n >= rows) continue;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = row0 + 4 * g16 + e;
+                    if (m < tile.mcount) pol.store(tile, m, n, acc[i][j][e]);
+                }
+            }
+        }
+    }
+}
+
 template <uint32_t QT, int WM, int WN, int SM, int SN, class Policy, int PF = 1, bool CF = false, int KS = 1>
 __global__ __launch_bounds__(KS * WM * WN * kWave) void gemm_x3_kernel(Policy pol, int rows, int cols) {
     static_assert(PF == 1 || PF == 2, "one or two stages in flight");
@@ -119,12 +175,21 @@ __global__ __launch_bounds__(KS * WM * WN * kWave) void gemm_x3_kernel(Policy po
         else return c;
     };
 
-    int bx = blockIdx.x, by = blockIdx.y;
+    // Units of a split launch are numbered split-major (unit = split *
+    // tiles + tile), so an XCD's contiguous run shares its A tile's K range.
+    const int S = KSplit<Policy>::count(pol);
+    int bx = blockIdx.x, by = blockIdx.y, split = 0, tile_id = 0;
     if constexpr (Policy::kLinearGrid) {
         const int total = LinearTotal<Policy>::get(pol, gridDim.x), L = blockIdx.x;
         if (L >= total) return;
         const int q = total / kXcds, r = total % kXcds, xcd = L % kXcds, k = L / kXcds;
-        const int t = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + k;
+        int t = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + k;
+        if (S > 1) {
+            const int tiles = total / S;
+            split = t / tiles;
+            t %= tiles;
+        }
+        tile_id = t;
         bx = t % pol.tiles_x;
         by = t / pol.tiles_x;
     }
@@ -158,9 +223,11 @@ __global__ __launch_bounds__(KS * WM * WN * kWave) void gemm_x3_kernel(Policy po
     // kmax stages (the same barriers), a half past its own count computes
     // nothing.
     const int nblk_all = cols / kBlock;
-    const int kmax = (nblk_all + KS - 1) / KS;
-    const int kbeg = half * kmax;
-    const int kcnt = KS == 1 ? nblk_all : min(kmax, nblk_all - kbeg);
+    const int per = (nblk_all + S - 1) / S;                 // the unit's K blocks
+    const int ubeg = split * per, ucnt = min(per, nblk_all - ubeg);
+    const int kmax = (ucnt + KS - 1) / KS;
+    const int kbeg = ubeg + half * kmax;
+    const int kcnt = KS == 1 ? ucnt : min(kmax, ubeg + ucnt - kbeg);
     f32x4 a_reg[PF][A_PER_T];
     uint32_t b_raw[PF][B_PASSES][1 + Part::WORDS];
     auto load_stage = [&](int kb, int r) {
@@ -304,31 +371,54 @@ __global__ __launch_bounds__(KS * WM * WN * kWave) void gemm_x3_kernel(Policy po
                 for (int e = 0; e < 4; ++e) acc[i][j][e] += part[((i * SN + j) * 4 + e) * NT + tid];
     }
 
+    if (S > 1) {
+        // This unit's sums to its slot (coalesced: value v of thread t at
+        // v * NT + t); the fixup adds the tile's units and stores.
+        float* slot = KSplit<Policy>::part(pol) +
+                      (static_cast<size_t>(tile_id) * S + split) * x3_unit_floats<WM, WN, SM, SN>();
 #pragma unroll
-    for (int i = 0; i < SM; ++i) {
-        if (i >= nsub) break;
+        for (int i = 0; i < SM; ++i)
 #pragma unroll
-        for (int j = 0; j < SN; ++j) {
-            const int n = n0 + (wn * SN + j) * 16 + l16;
-            if constexpr (Policy::kPairedColumns) {
-                // Column blocks 2s and 2s + 1 hold columns q and q + 16 of a
-                // 32-column group (e.g. gate and up of one output feature).
-                if (j % 2 == 1) continue;
+            for (int j = 0; j < SN; ++j)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int m = sub_row(i) + 4 * g16 + e;
-                    if (m < tile.mcount && n < rows) pol.store_pair(tile, m, n, acc[i][j][e], acc[i][j + 1][e]);
-                }
-            } else {
-                if (n >= rows) continue;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int m = sub_row(i) + 4 * g16 + e;
-                    if (m < tile.mcount) pol.store(tile, m, n, acc[i][j][e]);
-                }
-            }
-        }
+                for (int e = 0; e < 4; ++e) slot[((i * SN + j) * 4 + e) * NT + tid] = acc[i][j][e];
+        return;
     }
+    x3_store<WM, WN, SM, SN>(pol, tile, n0, rows, wm, wn, l16, g16, nsub, acc);
+}
+
+// The stores of a split launch: tile blockIdx.x's units added in K order
+// (unit 0 first), with the thread layout of gemm_x3_kernel's first K half.
+template <int WM, int WN, int SM, int SN, class Policy>
+__global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_fixup_kernel(Policy pol, int rows) {
+    constexpr int NT = WM * WN * kWave;
+    constexpr int BM = WM * SM * 16, BN = WN * SN * 16;
+    constexpr size_t U = x3_unit_floats<WM, WN, SM, SN>();
+    const int t = blockIdx.x;
+    GemmTile tile;
+    if (!pol.tile(t / pol.tiles_x, BM, tile)) return;
+    const int n0 = (t % pol.tiles_x) * BN;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int wm = wave / WN, wn = wave % WN, l16 = lane & 15, g16 = lane >> 4;
+    const int S = pol.ksplit;
+    const float* units = pol.part + static_cast<size_t>(t) * S * U;
+    f32x4 acc[SM][SN];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][e] = units[((i * SN + j) * 4 + e) * NT + tid];
+    for (int u = 1; u < S; ++u)
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+#pragma unroll
+            for (int j = 0; j < SN; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[i][j][e] += units[u * U + ((i * SN + j) * 4 + e) * NT + tid];
+    const int s16 = (tile.mcount + 15) / 16;
+    const int nsub = Policy::kPartialTiles ? max(0, min(SM, (s16 - wm + WM - 1) / WM)) : SM;
+    x3_store<WM, WN, SM, SN>(pol, tile, n0, rows, wm, wn, l16, g16, nsub, acc);
 }
 
 // Tile shapes of the launches: 128 A rows x 256 weight rows on 8 waves of
@@ -356,12 +446,14 @@ __global__ __launch_bounds__(KS * WM * WN * kWave) void gemm_x3_kernel(Policy po
 // on 64 x 128 (272 tiles of 128 x 256 would leave 16 CUs a second one).
 enum class X3Shape { k128x256, k64x128, k64x64, k128x192, k64x128_split };
 
-inline double x3_estimate(long long tiles, int area, int occupancy, const double* rate) {
+// Per-CU time of `tiles` tiles (or units) of `area` outputs each (in units
+// of area / (TFLOP/s): multiply by 2 K 256 / 1e12 for seconds).
+inline double x3_estimate(long long tiles, double area, int occupancy, const double* rate) {
     long long left = (tiles + kCUs - 1) / kCUs;
     double t = 0.0;
     while (left > 0) {
         const int k = static_cast<int>(left < occupancy ? left : occupancy);
-        t += k * static_cast<double>(area) / rate[k - 1];
+        t += k * area / rate[k - 1];
         left -= k;
     }
     return t;
@@ -371,8 +463,22 @@ inline double x3_estimate(long long tiles, int area, int occupancy, const double
 // 512 tokens x 12288- and 17408-column matrices, a few % slower on short K).
 constexpr int kX3LongK = 8192;
 
-// rows = weight rows (outputs per A row), count = A rows, cols = K.
-inline X3Shape x3_shape(int rows, int count, int cols, bool paired = false) {
+// A launch: the tile shape and the units per tile of a K split (1: none).
+struct X3Plan {
+    X3Shape shape;
+    int split;
+    long long tiles;
+    int bm, bn;
+    size_t workspace_bytes() const { return split > 1 ? static_cast<size_t>(tiles) * split * bm * bn * 4 : 0; }
+};
+
+// The plan of least estimated time for rows weight rows, count A rows and
+// K = cols; splits only where their partial sums fit `workspace` bytes.
+// A split unit runs the tile shape over K / split blocks at the shape's
+// rate, plus a per-round cost for its shorter pipeline (prologue, drain and
+// the partial-sum stores), and the launch adds the fixup: the units' sums
+// read back and the outputs written, and one more launch.
+inline X3Plan x3_plan(int rows, int count, int cols, bool paired, size_t workspace) {
     auto tiles = [&](int bm, int bn) {
         return static_cast<long long>((rows + bn - 1) / bn) * ((count + bm - 1) / bm);
     };
@@ -382,45 +488,112 @@ inline X3Shape x3_shape(int rows, int count, int cols, bool paired = false) {
     static constexpr double r64[] = {150.0, 190.0, 215.0, 230.0};
     static constexpr double r192[] = {300.0};
     static constexpr double r64x128_split[] = {240.0};  // K halves on 16 waves, one workgroup per CU
-    const double e[5] = {x3_estimate(tiles(128, 256), 128 * 256, 1, r256),
-                         x3_estimate(tiles(64, 128), 64 * 128, 3, cols >= kX3LongK ? r64x128_long : r64x128),
-                         x3_estimate(tiles(64, 64), 64 * 64, 4, r64),
-                         paired ? 1e300 : x3_estimate(tiles(128, 192), 128 * 192, 1, r192),
-                         cols >= kX3LongK ? x3_estimate(tiles(64, 128), 64 * 128, 1, r64x128_split) : 1e300};
-    int best = 0;
-    for (int i = 1; i < 5; ++i)
-        if (e[i] < e[best]) best = i;
-    return static_cast<X3Shape>(best);
+    struct Option {
+        X3Shape shape;
+        int bm, bn, occupancy;
+        const double* rate;
+        bool ok;
+    };
+    const bool long_k = cols >= kX3LongK;
+    const Option options[5] = {
+        {X3Shape::k128x256, 128, 256, 1, r256, true},
+        {X3Shape::k64x128, 64, 128, 3, long_k ? r64x128_long : r64x128, true},
+        {X3Shape::k64x64, 64, 64, 4, r64, true},
+        {X3Shape::k128x192, 128, 192, 1, r192, !paired},
+        {X3Shape::k64x128_split, 64, 128, 1, r64x128_split, long_k},
+    };
+    const int blocks = cols / kBlock;
+    // Fitted to a sweep of every shape at splits 1, 2, 3, 4, 6 and 8 on six
+    // prefill shapes (512 and 2048 tokens, 4096-17408 columns): the fit's
+    // choice is within 2% of the fastest on each.  A unit's pipeline fill and
+    // drain cost per round (less where other resident units hide them), and
+    // the fixup's traffic moves at about a quarter of HBM's peak.
+    constexpr double kRoundSeconds = 3e-6, kRoundSecondsShared = 2e-6;
+    constexpr double kFixupBytesPerSecond = 2e12;
+    constexpr double kLaunchSeconds = 5e-6;
+    constexpr int kSplits[] = {1, 2, 3, 4, 6, 8};
+    X3Plan best{X3Shape::k128x256, 1, 0, 128, 256};
+    double best_t = 1e300;
+    for (const Option& o : options) {
+        if (!o.ok) continue;
+        const long long t = tiles(o.bm, o.bn);
+        const double area = static_cast<double>(o.bm) * o.bn;
+        for (const int split : kSplits) {
+            const int per = (blocks + split - 1) / split;
+            if (split > 1 && (per < 8 || (split - 1) * per >= blocks)) continue;
+            const X3Plan plan{o.shape, split, t, o.bm, o.bn};
+            if (plan.workspace_bytes() > workspace) continue;
+            double sec = x3_estimate(t * split, area / split, o.occupancy, o.rate) * 2.0 * cols * kCUs / 1e12;
+            if (split > 1) {
+                const long long rounds = (t * split + static_cast<long long>(kCUs) * o.occupancy - 1) /
+                                         (static_cast<long long>(kCUs) * o.occupancy);
+                sec += rounds * (o.occupancy == 1 ? kRoundSeconds : kRoundSecondsShared) + kLaunchSeconds +
+                       static_cast<double>(t) * area * 4.0 * (split + 1) / kFixupBytesPerSecond;
+            }
+            if (sec < best_t) {
+                best_t = sec;
+                best = plan;
+            }
+        }
+    }
+    return best;
 }
 
+inline X3Shape x3_shape(int rows, int count, int cols, bool paired = false) {
+    return x3_plan(rows, count, cols, paired, 0).shape;
+}
+
+template <class P, class = void>
+struct HasKSplit : std::false_type {};
+template <class P>
+struct HasKSplit<P, decltype(void(std::declval<P&>().ksplit))> : std::true_type {};
+
 // One launch of gemm_x3_kernel over count A rows (pol.count) and `rows`
-// weight rows, on a 1-D grid (Policy::kLinearGrid) of all tiles.
+// weight rows, on a 1-D grid (Policy::kLinearGrid) of all tiles (units);
+// with split > 1 (policies with a workspace), the fixup launch follows.
 template <uint32_t QT, int WM, int WN, int SM, int SN, int PF, bool CF, class P, int KS = 1>
-int launch_x3_tiles(P pol, int rows, int count, int cols, hipStream_t stream) {
+int launch_x3_tiles(P pol, int rows, int count, int cols, hipStream_t stream, int split = 1) {
     constexpr int BM = WM * SM * 16, BN = WN * SN * 16;
     pol.tiles_x = (rows + BN - 1) / BN;
     const long long tiles = static_cast<long long>(pol.tiles_x) * ((count + BM - 1) / BM);
-    if (tiles > 0x7fffffffLL) return Q3X_HIP_EINVAL;
-    hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, P, PF, CF, KS>), dim3(static_cast<unsigned>(tiles)),
-                       dim3(KS * WM * WN * kWave), 0, stream, pol, rows, cols);
+    if (tiles * split > 0x7fffffffLL) return Q3X_HIP_EINVAL;
+    if constexpr (HasKSplit<P>::value) pol.ksplit = split;
+    else if (split != 1) return Q3X_HIP_EINVAL;
+    hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, P, PF, CF, KS>),
+                       dim3(static_cast<unsigned>(tiles * split)), dim3(KS * WM * WN * kWave), 0, stream, pol, rows,
+                       cols);
+    if constexpr (HasKSplit<P>::value) {
+        if (split > 1) {
+            const int status = launch_status();
+            if (status != Q3X_HIP_OK) return status;
+            hipLaunchKernelGGL((gemm_x3_fixup_kernel<WM, WN, SM, SN, P>), dim3(static_cast<unsigned>(tiles)),
+                               dim3(WM * WN * kWave), 0, stream, pol, rows);
+        }
+    }
     return launch_status();
 }
 
+// A launch by plan; `workspace` bytes at pol.part for split plans
+// (policies with a workspace; 0 otherwise).
 template <uint32_t QT, class P>
-int launch_x3(const P& pol, int rows, int count, int cols, hipStream_t stream) {
-    switch (x3_shape(rows, count, cols, P::kPairedColumns)) {
-        case X3Shape::k128x256: return launch_x3_tiles<QT, 2, 4, 4, 4, 1, true>(pol, rows, count, cols, stream);
+int launch_x3(const P& pol, int rows, int count, int cols, hipStream_t stream, size_t workspace = 0) {
+    const X3Plan plan = x3_plan(rows, count, cols, P::kPairedColumns, workspace);
+    const int split = plan.split;
+    switch (plan.shape) {
+        case X3Shape::k128x256:
+            return launch_x3_tiles<QT, 2, 4, 4, 4, 1, true>(pol, rows, count, cols, stream, split);
         case X3Shape::k128x192:
             if constexpr (!P::kPairedColumns)
-                return launch_x3_tiles<QT, 2, 4, 4, 3, 1, false>(pol, rows, count, cols, stream);
+                return launch_x3_tiles<QT, 2, 4, 4, 3, 1, false>(pol, rows, count, cols, stream, split);
             else
-                return launch_x3_tiles<QT, 2, 4, 4, 4, 1, true>(pol, rows, count, cols, stream);
+                return launch_x3_tiles<QT, 2, 4, 4, 4, 1, true>(pol, rows, count, cols, stream, split);
         case X3Shape::k64x128_split:
-            return launch_x3_tiles<QT, 2, 4, 2, 2, 1, false, P, 2>(pol, rows, count, cols, stream);
+            return launch_x3_tiles<QT, 2, 4, 2, 2, 1, false, P, 2>(pol, rows, count, cols, stream, split);
         case X3Shape::k64x128:
-            if (cols >= kX3LongK) return launch_x3_tiles<QT, 2, 4, 2, 2, 2, false>(pol, rows, count, cols, stream);
-            return launch_x3_tiles<QT, 2, 4, 2, 2, 1, false>(pol, rows, count, cols, stream);
-        default: return launch_x3_tiles<QT, 2, 2, 2, 2, 1, false>(pol, rows, count, cols, stream);
+            if (cols >= kX3LongK)
+                return launch_x3_tiles<QT, 2, 4, 2, 2, 2, false>(pol, rows, count, cols, stream, split);
+            return launch_x3_tiles<QT, 2, 4, 2, 2, 1, false>(pol, rows, count, cols, stream, split);
+        default: return launch_x3_tiles<QT, 2, 2, 2, 2, 1, false>(pol, rows, count, cols, stream, split);
     }
 }
 

@@ -47,6 +47,16 @@ void batch_mv(const Linear& linear, const float* input, float* output, int count
                                output, add ? 1 : 0, stream));
 }
 
+size_t batch_mv_workspace_bytes(const Linear& linear, int count) {
+    return q3x_hip_gemm_workspace_bytes(linear.type, linear.rows, linear.columns, count);
+}
+
+void batch_mv(const Linear& linear, const float* input, float* output, int count, bool add, void* workspace,
+              size_t workspace_bytes, hipStream_t stream) {
+    Q3X_HIP_CHECK(q3x_hip_gemm_ws(linear.weight, linear.type, linear.rows, linear.columns, input, count, output,
+                                  add ? 1 : 0, workspace, workspace_bytes, stream));
+}
+
 void embed(const Linear& table, int token, float* output, hipStream_t stream) {
     if (token < 0 || token >= table.rows) {
         std::fprintf(stderr, "embedding token=%d rows=%d\n", token, table.rows);

@@ -51,6 +51,12 @@ void projections(const Linear* linears, float* const* outputs, int count, const 
 // the cuBLAS handle and BF16 staging buffer of the BF16 path).
 void batch_mv(const Linear& linear, const float* input, float* output, int count, bool add,
               hipStream_t stream);
+// The same with a caller-owned workspace of at least
+// batch_mv_workspace_bytes(linear, count) bytes: shapes of few output tiles
+// over a long K split K over workgroups (deterministic; another sum order).
+size_t batch_mv_workspace_bytes(const Linear& linear, int count);
+void batch_mv(const Linear& linear, const float* input, float* output, int count, bool add, void* workspace,
+              size_t workspace_bytes, hipStream_t stream);
 // output[columns] = dequantised row `token` (engine.cu:1499 embed).
 void embed(const Linear& table, int token, float* output, hipStream_t stream);
 // ids / weights [tokens, top_k] from logits [tokens, experts] (engine.cu:1153).

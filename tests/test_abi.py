@@ -69,6 +69,10 @@ def test_invalid_arguments_are_rejected_without_device_work():
     assert lib.q3x_hip_gemm(P, 1, 4, 64, P, 0, P, 0, N) == q3x.EINVAL
     assert lib.q3x_hip_gemm(P, 2, 4, 40, P, 3, P, 0, N) == q3x.EINVAL
     assert lib.q3x_hip_gemm(P, 0, 4, 64, P, 3, P, 0, N) == q3x.ENOTSUP
+    gw = lib.q3x_hip_gemm_ws
+    assert gw(P, 1, 4, 64, P, 0, P, 0, P, 1024, N) == q3x.EINVAL
+    assert gw(P, 0, 4, 64, P, 3, P, 0, P, 1024, N) == q3x.ENOTSUP
+    assert gw(P, 1, 4, 64, P, 3, P, 0, N, 1024, N) == q3x.EINVAL       # bytes but no workspace
     assert lib.q3x_hip_dequant(P, 1, 64, -1, 1, P, N) == q3x.EINVAL
     assert lib.q3x_hip_dequant(P, 2, 64, 0, 0, P, N) == q3x.EINVAL
     assert lib.q3x_hip_read_probe(N, 16, P, N) == q3x.EINVAL
@@ -165,3 +169,18 @@ def test_cpp_host_interface_binary_skips_without_gpu():
         pytest.skip("GPU present: the binary runs in the GPU suite")
     r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
     assert r.returncode == 77, r.stdout + r.stderr
+
+
+def test_gemm_workspace_sizes():
+    # Splits only where few output tiles meet a long K; a pure function of
+    # the shape (the plan a call makes with that many bytes).
+    lib = q3x.lib()
+    Q8, Q4 = q3x.MATRIX_Q8_0, q3x.MATRIX_Q4_0
+    assert lib.q3x_hip_gemm_workspace_bytes(Q8, 12288, 4096, 4096) == 0      # 1536 tiles: no split
+    down = lib.q3x_hip_gemm_workspace_bytes(Q4, 5120, 17408, 512)            # 80 tiles, 544 K blocks
+    assert down > 0 and down % (128 * 256 * 4 * 80) == 0
+    assert down == lib.q3x_hip_gemm_workspace_bytes(Q4, 5120, 17408, 512)
+    assert lib.q3x_hip_gemm_workspace_bytes(Q8, 256, 8192, 64) > 0          # one tile, 256 K blocks
+    assert lib.q3x_hip_gemm_workspace_bytes(Q8, 4, 64, 3) == 0
+    assert lib.q3x_hip_gemm_workspace_bytes(Q8, 4, 40, 3) == 0              # invalid shape
+    assert lib.q3x_hip_gemm_workspace_bytes(0, 4096, 4096, 512) == 0        # BF16

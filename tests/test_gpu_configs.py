@@ -66,15 +66,24 @@ def test_decode_matvec_configs(index):
         say(f"  worst |delta|/bound = {worst:.3g}")
 
 
-@pytest.mark.parametrize("index,count", [(2, 512), (2, 4096), (3, 512)])
-def test_prefill_gemm_configs(index, count):
+@pytest.mark.parametrize("index,count,split", [(2, 512, False), (2, 4096, False), (3, 512, False),
+                                               (2, 512, True), (3, 512, True)])
+def test_prefill_gemm_configs(index, count, split):
+    # split: q3x_hip_gemm_ws with the workspace its plan asks for (the down
+    # projections at N = 512 split K over workgroups).
     torch = _torch()
     mats = wl.dense_matrices(index)
     for m in mats:
-        say(f"config {index} N={count} {m.name} {m.rows}x{m.cols}")
+        say(f"config {index} N={count} {m.name} {m.rows}x{m.cols} split={split}")
         X = wl.activations(index, count, m.cols, salt=m.rows)
         Y = torch.empty((count, m.rows), dtype=torch.float32, device="cuda:0")
-        q3x.batch_mv(m.linear, X, Y, count)
+        if split:
+            nbytes = q3x.gemm_workspace_bytes(m.linear, count)
+            ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device="cuda:0")
+            q3x.batch_mv_ws(m.linear, X, Y, count, ws if nbytes else None)
+            del ws
+        else:
+            q3x.batch_mv(m.linear, X, Y, count)
         w = host(m.weight)
         Xh = host(X)
         Yh = host(Y)

@@ -422,6 +422,76 @@ def test_gemm_one_product_per_row(type_, rows, cols, count):
     assert np.array_equal(bits(host(Y)), bits(got + got))
 
 
+# Split K (q3x_hip_gemm_ws): shapes whose plan splits (few output tiles over
+# a long K), against the oracle's bound, with accumulate, twice in a row bit
+# for bit (deterministic), and with a workspace one byte short (the unsplit
+# launch, equal to q3x_hip_gemm bit for bit).  Odd and uneven K block counts
+# give units of unequal length; partial tiles on both edges.
+SPLIT_CASES = [(Q8_0, 256, 8192, 64), (Q4_0, 300, 8224, 70), (Q8_0, 1000, 12288, 130), (Q4_0, 640, 17408, 40),
+               (Q8_0, 77, 16416, 3)]
+
+
+def _workspace(linear, count):
+    torch = _torch()
+    nbytes = q3x.gemm_workspace_bytes(linear, count)
+    assert nbytes > 0, "the plan must split this shape"
+    return torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0"), nbytes
+
+
+@pytest.mark.parametrize("type_,rows,cols,count", SPLIT_CASES)
+def test_gemm_split_parity(type_, rows, cols, count):
+    torch = _torch()
+    rng = np.random.default_rng(rows + 3 * cols + count + type_)
+    w = random_blocks(rng, type_, rows, cols)
+    X = rng.normal(0, 1, (count, cols)).astype(np.float32)
+    want = oracle.gemm(w, type_, rows, cols, X)
+    wd = dequant_numpy(w, type_, rows, cols)
+    lin = q3x.Linear(dev(w), rows, cols, type_)
+    ws, nbytes = _workspace(lin, count)
+    say(f"gemm split type={type_} {rows}x{cols} count={count} workspace={nbytes}")
+    Xd = dev(X)
+    Y = torch.full((count, rows), float("nan"), dtype=torch.float32, device="cuda:0")
+    q3x.batch_mv_ws(lin, Xd, Y, count, ws)
+    got = host(Y)
+    check_bound(got, want, wd, X, f"gemm split {rows}x{cols}x{count}")
+    Y2 = torch.full_like(Y, float("nan"))
+    q3x.batch_mv_ws(lin, Xd, Y2, count, ws)
+    assert np.array_equal(bits(host(Y2)), bits(got))
+    q3x.batch_mv_ws(lin, Xd, Y, count, ws, add=True)
+    check_bound(host(Y), 2 * want, wd, 2 * X, "gemm split add")
+    # one byte short: the unsplit launch, q3x_hip_gemm's result
+    short = ws.view(torch.uint8)[: nbytes - 1]
+    Y3 = torch.full_like(Y, float("nan"))
+    q3x.batch_mv_ws(lin, Xd, Y3, count, short)
+    Y4 = torch.full_like(Y, float("nan"))
+    q3x.batch_mv(lin, Xd, Y4, count)
+    assert np.array_equal(bits(host(Y3)), bits(host(Y4)))
+
+
+# The one-product matrices through the split launch: a block's product lands
+# in one unit, the others add exact zeros, so the same 2-ulp bar holds; a
+# unit summed into the wrong tile or slot gives unrelated values.
+@pytest.mark.parametrize("type_,rows,cols,count", [(Q8_0, 256, 8192, 64), (Q4_0, 300, 8224, 70),
+                                                   (Q8_0, 5120, 17408, 512)])
+def test_gemm_split_one_product_per_row(type_, rows, cols, count):
+    torch = _torch()
+    rng = np.random.default_rng(rows * 11 + cols + count + type_)
+    w, col, q, d = _one_product_matrix(rng, type_, rows, cols)
+    mant = rng.uniform(1.0, 2.0, (count, cols)) * rng.choice([-1.0, 1.0], (count, cols))
+    X = np.ldexp(mant, rng.integers(-90, 91, (count, cols))).astype(np.float32)
+    want = d[None, :] * (q[None, :] * X[:, col])
+    lin = q3x.Linear(dev(w), rows, cols, type_)
+    ws, nbytes = _workspace(lin, count)
+    Y = torch.full((count, rows), float("nan"), dtype=torch.float32, device="cuda:0")
+    say(f"gemm split one product per row: type={type_} {rows}x{cols} count={count} workspace={nbytes}")
+    q3x.batch_mv_ws(lin, dev(X), Y, count, ws)
+    got = host(Y)
+    assert np.all(np.sign(got) == np.sign(want))
+    ulps = np.abs(bits(got).astype(np.int64) - bits(want).astype(np.int64))
+    say(f"  exact {np.mean(ulps == 0):.3f}, worst {ulps.max()} ulp")
+    assert ulps.max() <= 2, f"{np.count_nonzero(ulps > 2)} outputs beyond 2 ulp; first at {np.argwhere(ulps > 2)[0]}"
+
+
 # ---------------------------------------------------------------- router ----
 
 def _router_logits(rng, tokens, experts, kind):
