@@ -893,12 +893,16 @@ template <uint32_t QT>
 int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
                 int tokens, const int* ids, const float* weights, int top_k, float* Y, int accumulate,
                 uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
-    // 64 pairs x 128 weight rows on 8 waves of 32x32.  At 2048 tokens x top
-    // 8 of 256 experts (64 pairs per expert on average) 64 x 128, 128 x 128
-    // and 128 x 256 tiles measured within 2% (0.587-0.597 ms for the routed
-    // GEMMs and combine), 64 x 64 0.72 ms; the smallest of the three wastes
-    // the least on an expert's short last tile.
-    return moe_grouped_tiles<QT, 2, 4, 2, 2>(gate_up, down, experts, H, I, X, tokens, ids, weights, top_k, Y,
+    // 64 pairs x 256 weight rows on 8 waves of 32x64: 64 pairs (an expert's
+    // average at 2048 tokens x top 8 of 256 experts) keep the padding of an
+    // expert's short last tile low, and the wide wave tile gives each
+    // activation split and scale fold twice the matrix work of a 32x32 one.
+    // At config 4 (T = 2048), alternating runs of one box: 162-180 TFLOP/s
+    // against 145-160 for 64 x 128 on 32x32 waves; 64 x 512 on 8 waves of
+    // 64x64, 64 x 256 on 8 waves of 64x32 or on 4 of 64x64, 64 x 512 on 8
+    // waves of 32x128, 64 x 128 on 4 waves of 32x64 and 64 x 256 on 16
+    // waves of 32x32 all fell between the two.
+    return moe_grouped_tiles<QT, 2, 4, 2, 4>(gate_up, down, experts, H, I, X, tokens, ids, weights, top_k, Y,
                                              accumulate, ws, L, stream);
 }
 
