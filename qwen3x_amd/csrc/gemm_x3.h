@@ -387,38 +387,33 @@ __global__ __launch_bounds__(KS * WM * WN * kWave) void gemm_x3_kernel(Policy po
     x3_store<WM, WN, SM, SN>(pol, tile, n0, rows, wm, wn, l16, g16, nsub, acc);
 }
 
-// The stores of a split launch: tile blockIdx.x's units added in K order
-// (unit 0 first), with the thread layout of gemm_x3_kernel's first K half.
+// The stores of a split launch, one output value per thread: value f (in
+// the units' layout, f = v * NT + t for value v of thread t) of tile
+// blockIdx.x / (BM * BN / 256), its units added in K order (unit 0 first),
+// stored where gemm_x3_kernel's thread t would store its value v.
 template <int WM, int WN, int SM, int SN, class Policy>
-__global__ __launch_bounds__(WM * WN * kWave) void gemm_x3_fixup_kernel(Policy pol, int rows) {
+__global__ __launch_bounds__(256) void gemm_x3_fixup_kernel(Policy pol, int rows) {
+    static_assert(!Policy::kPairedColumns, "split launches store single columns");
     constexpr int NT = WM * WN * kWave;
     constexpr int BM = WM * SM * 16, BN = WN * SN * 16;
-    constexpr size_t U = x3_unit_floats<WM, WN, SM, SN>();
-    const int t = blockIdx.x;
+    constexpr int U = static_cast<int>(x3_unit_floats<WM, WN, SM, SN>());  // BM * BN
+    static_assert(U % 256 == 0, "whole workgroups per tile");
+    constexpr int kPerTile = U / 256;
+    const int t = blockIdx.x / kPerTile;
+    const int f = (blockIdx.x % kPerTile) * 256 + threadIdx.x;
     GemmTile tile;
     if (!pol.tile(t / pol.tiles_x, BM, tile)) return;
-    const int n0 = (t % pol.tiles_x) * BN;
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const int wm = wave / WN, wn = wave % WN, l16 = lane & 15, g16 = lane >> 4;
     const int S = pol.ksplit;
     const float* units = pol.part + static_cast<size_t>(t) * S * U;
-    f32x4 acc[SM][SN];
-#pragma unroll
-    for (int i = 0; i < SM; ++i)
-#pragma unroll
-        for (int j = 0; j < SN; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[i][j][e] = units[((i * SN + j) * 4 + e) * NT + tid];
-    for (int u = 1; u < S; ++u)
-#pragma unroll
-        for (int i = 0; i < SM; ++i)
-#pragma unroll
-            for (int j = 0; j < SN; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[i][j][e] += units[u * U + ((i * SN + j) * 4 + e) * NT + tid];
-    const int s16 = (tile.mcount + 15) / 16;
-    const int nsub = Policy::kPartialTiles ? max(0, min(SM, (s16 - wm + WM - 1) / WM)) : SM;
-    x3_store<WM, WN, SM, SN>(pol, tile, n0, rows, wm, wn, l16, g16, nsub, acc);
+    float sum = units[f];
+    for (int u = 1; u < S; ++u) sum += units[static_cast<size_t>(u) * U + f];
+    const int v = f / NT, tid = f % NT;
+    const int i = v / (SN * 4), j = (v / 4) % SN, e = v % 4;
+    const int lane = tid & (kWave - 1), wave = tid / kWave;
+    const int wm = wave / WN, wn = wave % WN, l16 = lane & 15, g16 = lane >> 4;
+    const int m = 16 * (i * WM + wm) + 4 * g16 + e;
+    const int n = (t % pol.tiles_x) * BN + (wn * SN + j) * 16 + l16;
+    if (m < tile.mcount && n < rows) pol.store(tile, m, n, sum);
 }
 
 // Tile shapes of the launches: 128 A rows x 256 weight rows on 8 waves of
@@ -556,7 +551,8 @@ int launch_x3_tiles(P pol, int rows, int count, int cols, hipStream_t stream, in
     constexpr int BM = WM * SM * 16, BN = WN * SN * 16;
     pol.tiles_x = (rows + BN - 1) / BN;
     const long long tiles = static_cast<long long>(pol.tiles_x) * ((count + BM - 1) / BM);
-    if (tiles * split > 0x7fffffffLL) return Q3X_HIP_EINVAL;
+    if (tiles * split > 0x7fffffffLL || (split > 1 && tiles * (BM * BN / 256) > 0x7fffffffLL))
+        return Q3X_HIP_EINVAL;
     if constexpr (HasKSplit<P>::value) pol.ksplit = split;
     else if (split != 1) return Q3X_HIP_EINVAL;
     hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, P, PF, CF, KS>),
@@ -566,8 +562,9 @@ int launch_x3_tiles(P pol, int rows, int count, int cols, hipStream_t stream, in
         if (split > 1) {
             const int status = launch_status();
             if (status != Q3X_HIP_OK) return status;
-            hipLaunchKernelGGL((gemm_x3_fixup_kernel<WM, WN, SM, SN, P>), dim3(static_cast<unsigned>(tiles)),
-                               dim3(WM * WN * kWave), 0, stream, pol, rows);
+            constexpr int kPerTile = BM * BN / 256;
+            hipLaunchKernelGGL((gemm_x3_fixup_kernel<WM, WN, SM, SN, P>),
+                               dim3(static_cast<unsigned>(tiles * kPerTile)), dim3(256), 0, stream, pol, rows);
         }
     }
     return launch_status();
