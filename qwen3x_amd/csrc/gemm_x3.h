@@ -40,9 +40,9 @@
 // loads repeat the last block (into a buffer no stage reads), so a step has
 // no branch.  CF ("compute first") issues stage kb's matrix instructions
 // before stage kb + 1's conversion instead, so the scheduler places the
-// split and the weight conversion in the matrix instructions' shadow: 3-13%
-// faster with 64x64 wave tiles, slower with smaller ones (the registers the
-// overlap holds cost them a wave of occupancy).
+// split and the weight conversion in the matrix instructions' shadow; with
+// two stages of loads ahead it measures 1-4% slower on 64x64 wave tiles and
+// with smaller ones it costs a wave of occupancy, so no launch uses it.
 //
 // A policy supplies the tiles and the operand rows: tile(ty, BM, tile)
 // (false: no such tile), a_row(tile, m) (an FP32 A row), b_row(tile, n) (a
@@ -577,13 +577,15 @@ int launch_x3(const P& pol, int rows, int count, int cols, hipStream_t stream, s
     const X3Plan plan = x3_plan(rows, count, cols, P::kPairedColumns, workspace);
     const int split = plan.split;
     switch (plan.shape) {
+        // The one-per-CU shapes with two stages of loads ahead: 1-3% faster
+        // than one (and than compute-first) at 512-4096 tokens.
         case X3Shape::k128x256:
-            return launch_x3_tiles<QT, 2, 4, 4, 4, 1, true>(pol, rows, count, cols, stream, split);
+            return launch_x3_tiles<QT, 2, 4, 4, 4, 2, false>(pol, rows, count, cols, stream, split);
         case X3Shape::k128x192:
             if constexpr (!P::kPairedColumns)
-                return launch_x3_tiles<QT, 2, 4, 4, 3, 1, false>(pol, rows, count, cols, stream, split);
+                return launch_x3_tiles<QT, 2, 4, 4, 3, 2, false>(pol, rows, count, cols, stream, split);
             else
-                return launch_x3_tiles<QT, 2, 4, 4, 4, 1, true>(pol, rows, count, cols, stream, split);
+                return launch_x3_tiles<QT, 2, 4, 4, 4, 2, false>(pol, rows, count, cols, stream, split);
         case X3Shape::k64x128_split:
             return launch_x3_tiles<QT, 2, 4, 2, 2, 1, false, P, 2>(pol, rows, count, cols, stream, split);
         case X3Shape::k64x128:
