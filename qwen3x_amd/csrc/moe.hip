@@ -914,47 +914,42 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
 
 // logits[r] = router[r] . x for r < experts and *gate_logit = gate_row . x
 // (engine.cpp:408, 427, the BF16 branch of mv :200-212): one wave per row,
-// eight BF16 values per lane per step, fixed-order DPP sum.  Rows and x
-// 16-byte aligned, H % 8 == 0.
+// eight BF16 values per lane per step, fixed-order DPP sum.  Each wave first
+// requests its row's first kRouterHeld steps; then the workgroup stages x in
+// LDS once (In: PlainInput, or NormInput forming the RMSNorm exactly as the
+// experts' matvec stages it -- same sum order, same products -- so router
+// and experts see identical normalised values), and the row's dot reads x
+// from there.  Rows and x 16-byte aligned, H % 32 == 0, x within
+// router_gemv_lds_bytes.
+constexpr int kRouterHeld = 8;
+inline size_t router_gemv_lds_bytes(int H) { return pipe_x_bytes(H / kBlock) + 64; }
+
+template <class In>
 __global__ __launch_bounds__(256) void router_gemv_bf16_kernel(const uint16_t* __restrict__ router,
                                                                const uint16_t* __restrict__ gate_row, int experts,
-                                                               int H, const float* __restrict__ x,
-                                                               const uint16_t* __restrict__ norm_w,
+                                                               int H, const float* __restrict__ x, In in,
                                                                float* __restrict__ logits,
                                                                float* __restrict__ gate_logit) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t router_lds[];
     const int lane = threadIdx.x & (kWave - 1);
-    const int r = blockIdx.x * 4 + threadIdx.x / kWave;
-    if (r > experts) return;  // whole waves leave together
-    // With norm_w, x is the raw residual and each wave normalises it as
-    // NormInput stages it for the experts' matvec (same sum order, same
-    // products), so router and experts see identical normalised values.
-    float scale = 0.0f;
-    if (norm_w) {
-        float square = 0.0f;
-        for (int c = lane; c < H / 4; c += kWave) {
-            const f32x4 v = reinterpret_cast<const f32x4*>(x)[c];
-            square = fmaf(v.x, v.x, square);
-            square = fmaf(v.y, v.y, square);
-            square = fmaf(v.z, v.z, square);
-            square = fmaf(v.w, v.w, square);
-        }
-        scale = 1.0f / sqrtf(wave_sum_f32(square) / static_cast<float>(H) + kEps);
-    }
-    auto normed = [&](f32x4 v, int c) {
-        if (norm_w) {
-            v.x = v.x * scale * (1.0f + bf16_value(norm_w[c]));
-            v.y = v.y * scale * (1.0f + bf16_value(norm_w[c + 1]));
-            v.z = v.z * scale * (1.0f + bf16_value(norm_w[c + 2]));
-            v.w = v.w * scale * (1.0f + bf16_value(norm_w[c + 3]));
-        }
-        return v;
-    };
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int r = blockIdx.x * 4 + wave;  // rows past the gate row read zeros and store nothing
+    const int bpr = H / kBlock;
     const uint16_t* row = r < experts ? router + static_cast<size_t>(r) * H : gate_row;
+    // A buffer resource of the row's bytes: zeros past its end (and for rows
+    // past the gate row), with no branch around the loads.
+    const __amdgpu_buffer_rsrc_t rr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(row), 0, r <= experts ? 2 * H : 0, kBufferFlags);
+    u32x4 held[kRouterHeld];
+#pragma unroll
+    for (int j = 0; j < kRouterHeld; ++j)
+        held[j] = __builtin_amdgcn_raw_buffer_load_b128(rr, 2 * (8 * lane + 8 * kWave * j), 0, 0);
+    in.stage(x, router_lds, bpr, reinterpret_cast<float*>(router_lds + pipe_x_bytes(bpr)));
     float acc = 0.0f;
-    for (int c = 8 * lane; c < H; c += 8 * kWave) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(row + c);
-        const f32x4 x0 = normed(*reinterpret_cast<const f32x4*>(x + c), c);
-        const f32x4 x1 = normed(*reinterpret_cast<const f32x4*>(x + c + 4), c + 4);
+    auto step = [&](int c, u32x4 w) {
+        const uint8_t* xs = router_lds + x_block_offset(c >> 5) + 4 * (c & 31);
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(xs);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(xs + 16);
         acc = fmaf(__uint_as_float(w.x << 16), x0.x, acc);
         acc = fmaf(__uint_as_float(w.x & 0xffff0000u), x0.y, acc);
         acc = fmaf(__uint_as_float(w.y << 16), x0.z, acc);
@@ -963,9 +958,18 @@ __global__ __launch_bounds__(256) void router_gemv_bf16_kernel(const uint16_t* _
         acc = fmaf(__uint_as_float(w.z & 0xffff0000u), x1.y, acc);
         acc = fmaf(__uint_as_float(w.w << 16), x1.z, acc);
         acc = fmaf(__uint_as_float(w.w & 0xffff0000u), x1.w, acc);
+    };
+    // Columns in order, the held steps first (a lane's 8 columns lie inside
+    // the row or past it together).
+#pragma unroll
+    for (int j = 0; j < kRouterHeld; ++j) {
+        const int c = 8 * lane + 8 * kWave * j;
+        if (c < H) step(c, held[j]);
     }
+    for (int c = 8 * lane + 8 * kWave * kRouterHeld; c < H; c += 8 * kWave)
+        step(c, __builtin_amdgcn_raw_buffer_load_b128(rr, 2 * c, 0, 0));
     const float total = group_sum<kWave>(acc);
-    if (lane == 0) {
+    if (lane == 0 && r <= experts) {
         if (r < experts) logits[r] = total;
         else *gate_logit = total;
     }
@@ -1124,11 +1128,19 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
     int status;
 
     // Router logits and the shared expert's gate logit.
-    if (tokens == 1) {
-        hipLaunchKernelGGL(router_gemv_bf16_kernel, dim3((E + 1 + 3) / 4), dim3(256), 0, stream,
-                           reinterpret_cast<const uint16_t*>(router), reinterpret_cast<const uint16_t*>(gate_row),
-                           E, H, X, norm_w, logits, gate);
+    if (tokens == 1 && router_gemv_lds_bytes(H) <= 64 * 1024) {
+        const auto* rows = reinterpret_cast<const uint16_t*>(router);
+        const auto* grow = reinterpret_cast<const uint16_t*>(gate_row);
+        const dim3 grid((E + 1 + 3) / 4);
+        if (norm_w)
+            hipLaunchKernelGGL(router_gemv_bf16_kernel<NormInput>, grid, dim3(256), router_gemv_lds_bytes(H), stream,
+                               rows, grow, E, H, X, NormInput{norm_w}, logits, gate);
+        else
+            hipLaunchKernelGGL(router_gemv_bf16_kernel<PlainInput>, grid, dim3(256), router_gemv_lds_bytes(H),
+                               stream, rows, grow, E, H, X, PlainInput{}, logits, gate);
         status = launch_status();
+    } else if (norm_w) {
+        return Q3X_HIP_ENOTSUP;  // the caller normalises x and calls again without norm_w
     } else {
         RouterGemm g{};
         g.X = X; g.cols = H; g.count = tokens;
