@@ -18,7 +18,7 @@
  *   - calls are asynchronous on `stream` (0 = the null stream) and enqueue
  *     nothing when they return an error;
  *   - no entry point allocates, frees, synchronises or keeps state; the MoE
- *     workspace is caller-owned; calls are reentrant;
+ *     and split-GEMM workspaces are caller-owned; calls are reentrant;
  *   - results are deterministic: no atomics on accumulation paths, fixed
  *     reduction order per shape;
  *   - return Q3X_HIP_OK, or a negative code (arguments are validated before
@@ -400,7 +400,7 @@ enum {
 /* An engine over `weights`, a device buffer laid out as q3x_hip_model_schema
  * gives for `config` (the buffer of q3x_hip_model_load qualifies), with room
  * for `context` tokens (1 .. 262144).  A forward of several tokens runs as
- * prefill chunks of `chunk` rows (0: 2048; at most `context`), whose work
+ * prefill chunks of `chunk` rows (0: 4096; at most `context`), whose work
  * buffers the engine holds.  Needs a Q8_0 or Q4_0 model with KD, VD <= 128,
  * AD <= 256 a multiple of 32, RD <= min(64, AD) even, 2 <= CK <= 8,
  * top_k <= 8, AH / KVH <= 8 (BF16 models: Q3X_HIP_ENOTSUP, as the matmul

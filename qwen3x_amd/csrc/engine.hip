@@ -993,7 +993,7 @@ __device__ __forceinline__ float transpose_sum64(float (&v)[64]) {
 // AD <= 256 and a multiple of 4, G <= kMaxGroup.
 constexpr int kAttnSplits = 128;  // ranges per KV head for a decode step
 constexpr int kMaxGroup = 8;
-constexpr int kChunk = 2048;     // default rows of a prefill chunk
+constexpr int kChunk = 4096;     // default rows of a prefill chunk
 constexpr size_t kGemmScratchMax = static_cast<size_t>(512) << 20;  // K-split partial sums, at most
 
 template <int GP>

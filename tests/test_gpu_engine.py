@@ -48,7 +48,7 @@ def test_engine_logits_match_the_reference_forward(name):
 
 @pytest.mark.parametrize("name,prompt,chunk", [("dense_q8", 40, 0), ("dense_q4", 530, 256), ("moe_q4", 300, 0),
                                                ("moe_q8_tied", 64, 48), ("gqa8_q8", 100, 0), ("dense_q8", 333, 100),
-                                               ("gqa8_q8", 2100, 0), ("narrow_q4", 300, 128), ("odd_q8", 300, 0),
+                                               ("gqa8_q8", 2100, 2048), ("narrow_q4", 300, 128), ("odd_q8", 300, 0),
                                                ("gqa8_q8", 4200, 0), ("dense_q8", 8300, 0)])
 def test_prefill_then_decode_match_the_reference_forward(name, prompt, chunk):
     # A forward of many tokens runs them as prefill chunks (GEMMs, the delta
@@ -57,7 +57,7 @@ def test_prefill_then_decode_match_the_reference_forward(name, prompt, chunk):
     # those of the decode steps that follow, against
     # the reference's token-by-token forward.  Chunks of 256, 48 and 100 rows
     # put chunk boundaries inside the prompts, and tiles of 32 query rows
-    # end partly filled; 2100 tokens cross the default 2048-row chunk with
+    # end partly filled; 2100 tokens cross a 2048-row chunk with
     # every query tile spanning up to 66 key blocks.  At 4200 (8 query heads
     # per KV head) and 8300 (2) positions, each of a decode step's 128
     # position ranges is longer than one block of the decode attention (32 /
