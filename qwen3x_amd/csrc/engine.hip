@@ -1821,10 +1821,16 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                      ? mv_staged(gate_up, ffn, no_add, 2, type, c.H, e.hidden, NormInput{L.post_norm}, s, 1u)
                      : Q3X_HIP_ENOTSUP;
             const bool silu_stored = rc == Q3X_HIP_OK;
+            bool swiglu_done = false;  // ffn_gate holds silu(gate) * up
             if (rc == Q3X_HIP_ENOTSUP) {
                 hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden, nullptr,
                                    L.post_norm, c.H, e.normalized);
-                rc = apply_group(gate_up, ffn, 2, type, c.H, e.normalized, count, s, gemm_ws);
+                // A chunk: gate and up as one GEMM with the SwiGLU in its
+                // epilogue (bit for bit the two GEMMs and swiglu_kernel).
+                rc = count > 1 ? gate_up_swiglu(L.gate.w, L.up.w, type, c.I, c.H, e.normalized, count, e.ffn_gate, s)
+                               : Q3X_HIP_ENOTSUP;
+                swiglu_done = rc == Q3X_HIP_OK;
+                if (rc == Q3X_HIP_ENOTSUP) rc = apply_group(gate_up, ffn, 2, type, c.H, e.normalized, count, s, gemm_ws);
             }
             if (rc) break;
             const bool add = true;
@@ -1833,10 +1839,12 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                              : Q3X_HIP_ENOTSUP;
             if (rc == Q3X_HIP_ENOTSUP) {
                 const int n = count * c.I;
-                if (silu_stored)  // silu(gate) already: x = gate * up
+                if (swiglu_done) {
+                } else if (silu_stored) {  // silu(gate) already: x = gate * up
                     hipLaunchKernelGGL(product_kernel, dim3((n + 255) / 256), dim3(256), 0, s, e.ffn_gate, e.ffn_up, n);
-                else
+                } else {
                     hipLaunchKernelGGL(swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, s, e.ffn_gate, e.ffn_up, n);
+                }
                 rc = apply(L.down, type, e.ffn_gate, count, e.hidden, true, s, gemm_ws);
             }
             pending = false;

@@ -17,4 +17,13 @@ namespace q3x {
 int moe_layer_decode_add(const q3x_hip_moe_layer_weights& layer, const float* X, const uint16_t* norm_w, float* Y,
                          void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+// h[count, I] = silu(X G^T) * (X U^T) for X[count, H] and gate / up
+// matrices [I, H] of one type: a prefill FFN's gate and up GEMMs with the
+// SwiGLU (engine.cpp:371-376) in their epilogue -- gate row q and up row q in
+// one 32-column tile -- bit for bit the two GEMMs followed by silu(g) * u.
+// Q3X_HIP_ENOTSUP (nothing enqueued) where I % 64 != 0 or an operand is
+// unaligned (weights 2, X 16, h 4 bytes).
+int gate_up_swiglu(const void* gate, const void* up, uint32_t type, int I, int H, const float* X, int count,
+                   float* h, hipStream_t stream);
+
 }  // namespace q3x

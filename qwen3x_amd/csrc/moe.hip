@@ -1327,6 +1327,20 @@ extern "C" int q3x_hip_moe_layer(const q3x_hip_moe_layer_weights* layer, const f
     return moe_layer_checked(layer, X, tokens, Y, ids, weights, workspace, workspace_bytes, stream, false);
 }
 
+int q3x::gate_up_swiglu(const void* gate, const void* up, uint32_t type, int I, int H, const float* X, int count,
+                        float* h, hipStream_t stream) {
+    size_t bytes;
+    if (!is_quant_type(type) || count <= 0 || I % 64 != 0 || !quantized_size(type, I, H, &bytes))
+        return Q3X_HIP_ENOTSUP;
+    if (!aligned(gate, 2) || !aligned(up, 2) || !aligned(X, 16) || !aligned(h, 4)) return Q3X_HIP_ENOTSUP;
+    PairedGateUpGemm g{};
+    g.X = X; g.cols = H; g.count = count;
+    g.gate = static_cast<const uint8_t*>(gate); g.up = static_cast<const uint8_t*>(up);
+    g.row_bytes = static_cast<size_t>(H / kBlock) * block_bytes(type); g.I = I; g.h = h;
+    return type == Q3X_HIP_MATRIX_Q8_0 ? launch_token_gemm<Q3X_HIP_MATRIX_Q8_0>(g, 2 * I, stream)
+                                       : launch_token_gemm<Q3X_HIP_MATRIX_Q4_0>(g, 2 * I, stream);
+}
+
 int q3x::moe_layer_decode_add(const q3x_hip_moe_layer_weights& layer, const float* X, const uint16_t* norm_w,
                               float* Y, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     // NormInput loads the norm weights four at a time (8 bytes).
