@@ -56,8 +56,12 @@ struct BlockPart {
         }
     }
     // The block values as FP32, out[e] for e < N in the LDS column order
-    // (column part*N + e): q for Q8_0, nibble - 8 for Q4_0 (the scale is
-    // applied per block, scale()), the exact BF16 value for BF16.
+    // (column part*N + e): q for Q8_0, 16 (nibble - 8) for Q4_0 (the scale
+    // is applied per block, scale()), the exact BF16 value for BF16.
+    // Q4_0: a nibble n moved to the top of its byte with bit 3 flipped,
+    // ((n ^ 8) << 4), is the signed byte 16 (n - 8), so one xor-and per four
+    // values gives bytes that convert as signed bytes; the factor 16 is a
+    // power of two, exact in every product and sum, and scale() returns d / 16.
     __device__ static __forceinline__ void values(const uint32_t* raw, float* out) {
         if constexpr (kBF16) {
 #pragma unroll
@@ -70,20 +74,30 @@ struct BlockPart {
 #pragma unroll
         for (int i = 0; i < WORDS; ++i) {
             const uint32_t w = raw[1 + i];
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const uint32_t byte = (w >> (8 * b)) & 0xffu;
-                if constexpr (kQ4) {
-                    out[4 * i + b] = static_cast<float>(static_cast<int>(byte & 15u) - 8);
-                    out[N / 2 + 4 * i + b] = static_cast<float>(static_cast<int>(byte >> 4) - 8);
-                } else {
-                    out[4 * i + b] = static_cast<float>(static_cast<int8_t>(byte));
-                }
+            if constexpr (kQ4) {
+                const uint32_t lo = ((w << 4) ^ 0x80808080u) & 0xf0f0f0f0u;  // low nibbles
+                const uint32_t hi = (w ^ 0x80808080u) & 0xf0f0f0f0u;         // high nibbles
+                out[4 * i + 0] = sbyte<0>(lo);
+                out[4 * i + 1] = sbyte<1>(lo);
+                out[4 * i + 2] = sbyte<2>(lo);
+                out[4 * i + 3] = sbyte<3>(lo);
+                out[N / 2 + 4 * i + 0] = sbyte<0>(hi);
+                out[N / 2 + 4 * i + 1] = sbyte<1>(hi);
+                out[N / 2 + 4 * i + 2] = sbyte<2>(hi);
+                out[N / 2 + 4 * i + 3] = sbyte<3>(hi);
+            } else {
+                out[4 * i + 0] = sbyte<0>(w);
+                out[4 * i + 1] = sbyte<1>(w);
+                out[4 * i + 2] = sbyte<2>(w);
+                out[4 * i + 3] = sbyte<3>(w);
             }
         }
     }
-    // The block's fp16 scale d (exact in FP32).
-    __device__ static __forceinline__ float scale(const uint32_t* raw) { return f16_fast(raw[0]); }
+    // The block's fp16 scale d (exact in FP32); d / 16 for Q4_0, whose
+    // values() are 16 (n - 8).
+    __device__ static __forceinline__ float scale(const uint32_t* raw) {
+        return kQ4 ? f16_fast(raw[0]) * 0.0625f : f16_fast(raw[0]);
+    }
 };
 
 // Policy::linear_total() (optional, with kLinearGrid): the number of tiles
