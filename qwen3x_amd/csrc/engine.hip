@@ -1826,7 +1826,7 @@ int enqueue(q3x_hip_engine& e, int count, bool logits) {
                 hipLaunchKernelGGL(rms_kernel, dim3(count), dim3(kNormThreads), 0, s, e.hidden, nullptr,
                                    L.post_norm, c.H, e.normalized);
                 // A chunk: gate and up as one GEMM with the SwiGLU in its
-                // epilogue (bit for bit the two GEMMs and swiglu_kernel).
+                // epilogue (one pass over h instead of three).
                 rc = count > 1 ? gate_up_swiglu(L.gate.w, L.up.w, type, c.I, c.H, e.normalized, count, e.ffn_gate, s)
                                : Q3X_HIP_ENOTSUP;
                 swiglu_done = rc == Q3X_HIP_OK;

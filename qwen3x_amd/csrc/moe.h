@@ -20,7 +20,8 @@ int moe_layer_decode_add(const q3x_hip_moe_layer_weights& layer, const float* X,
 // h[count, I] = silu(X G^T) * (X U^T) for X[count, H] and gate / up
 // matrices [I, H] of one type: a prefill FFN's gate and up GEMMs with the
 // SwiGLU (engine.cpp:371-376) in their epilogue -- gate row q and up row q in
-// one 32-column tile -- bit for bit the two GEMMs followed by silu(g) * u.
+// one 32-column tile -- each product summed as the GEMM launches sum it
+// (K in block order within one half), then silu(g) * u as swiglu_kernel.
 // Q3X_HIP_ENOTSUP (nothing enqueued) where I % 64 != 0 or an operand is
 // unaligned (weights 2, X 16, h 4 bytes).
 int gate_up_swiglu(const void* gate, const void* up, uint32_t type, int I, int H, const float* X, int count,
