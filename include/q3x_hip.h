@@ -106,7 +106,9 @@ int q3x_hip_gemm(const void* w, uint32_t type, int rows, int cols,
  * output tiles over a long K (e.g. 512 tokens x 5120 rows x 17408 columns)
  * then fills the chip, each tile's K ranges summed by a second launch in K
  * order.  Deterministic; the sums run in another order than q3x_hip_gemm's,
- * within the same tolerance against the reference.  Same role as
+ * within the same tolerance against the reference.  The workspace holds the
+ * partial sums from the first launch to the second, so calls that share one
+ * must be ordered (e.g. issued on one stream).  Same role as
  * q3x_hip_gemm (batch_mv, arch/cuda/engine.cu:1568); no counterpart of its
  * own in the reference. */
 size_t q3x_hip_gemm_workspace_bytes(uint32_t type, int rows, int cols, int count);
