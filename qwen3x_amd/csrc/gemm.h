@@ -44,8 +44,16 @@ struct BlockPart {
     static constexpr bool kQ4 = QT == Q3X_HIP_MATRIX_Q4_0;
     static constexpr int N = 32 / PARTS;                                      // elements
     static constexpr int WORDS = (kQ4 ? 16 : kBF16 ? 64 : 32) / PARTS / 4;   // value words
+    // Q4_0 in two parts: one 12-byte load a part (part 0 block bytes 0-11,
+    // part 1 bytes 6-17), where two loads (the scale, then the part's 8
+    // value bytes) would each take an address slot of the vector memory
+    // pipeline; finish() puts the words in place when the stage is
+    // converted, part 1 taking the scale from its row's other lane.
+    static constexpr bool kOneLoad = kQ4 && PARTS == 2;
     __device__ static __forceinline__ void load(const uint8_t* blk, int part, uint32_t* raw) {
-        if constexpr (kBF16) {
+        if constexpr (kOneLoad) {
+            __builtin_memcpy(raw, blk + 6 * part, 12);
+        } else if constexpr (kBF16) {
             raw[0] = 0;
             const uint32_t* w = reinterpret_cast<const uint32_t*>(blk);
 #pragma unroll
@@ -53,6 +61,19 @@ struct BlockPart {
         } else {
             raw[0] = *reinterpret_cast<const uint16_t*>(blk);
             __builtin_memcpy(raw + 1, blk + 2 + 4 * WORDS * part, 4 * WORDS);
+        }
+    }
+    // raw as load() leaves it -> [scale, value words]; every lane of the
+    // wave active (the two parts of a row are lanes 2k and 2k + 1).
+    __device__ static __forceinline__ void finish(uint32_t* raw, int part) {
+        if constexpr (kOneLoad) {
+            const uint32_t partner = dpp_u32<0xB1>(raw[0]);  // lane ^ 1: part 0's bytes 0-3
+            const uint32_t scale = (part ? partner : raw[0]) & 0xffffu;
+            const uint32_t w0 = part ? raw[1] : __builtin_amdgcn_alignbyte(raw[1], raw[0], 2);
+            const uint32_t w1 = part ? raw[2] : __builtin_amdgcn_alignbyte(raw[2], raw[1], 2);
+            raw[0] = scale;
+            raw[1] = w0;
+            raw[2] = w1;
         }
     }
     // The block values as FP32, out[e] for e < N in the LDS column order

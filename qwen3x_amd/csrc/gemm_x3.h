@@ -259,12 +259,16 @@ __global__ __launch_bounds__(KS * WM * WN * kWave) void gemm_x3_kernel(Policy po
             if (BN % B_ROWS_PER_PASS == 0 || n < BN) {
                 uint32_t w[PER_PART / 2];
                 if constexpr (kScaled) {
+                    uint32_t raw[1 + Part::WORDS];
+#pragma unroll
+                    for (int i = 0; i <= Part::WORDS; ++i) raw[i] = b_raw[r][p][i];
+                    Part::finish(raw, b_part);
                     float vals[PER_PART];
-                    Part::values(b_raw[r][p], vals);
+                    Part::values(raw, vals);
 #pragma unroll
                     for (int e = 0; e < PER_PART / 2; ++e)
                         w[e] = bf16_pair(__float_as_uint(vals[2 * e]), __float_as_uint(vals[2 * e + 1]));
-                    scales(buf)[n] = Part::scale(b_raw[r][p]);  // the row's parts write the same value
+                    scales(buf)[n] = Part::scale(raw);  // the row's parts write the same value
                 } else {
 #pragma unroll
                     for (int e = 0; e < PER_PART / 2; ++e) w[e] = b_raw[r][p][1 + e];  // two bf16 a word already
