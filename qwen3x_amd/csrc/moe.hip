@@ -287,7 +287,7 @@ struct RoutedGateUpRows : ExpertGateUpRows {
 
 struct MoeLayout {
     size_t ntiles, nvalid, tile_expert, tile_start, tile_count, pos_of_pair, src_token;
-    size_t chunk_counts, chunk_base;
+    size_t chunk_counts;
     int chunks;
     size_t gu, h, d, total;
     int max_tiles;
@@ -311,7 +311,6 @@ inline MoeLayout moe_layout(int tokens, int experts, int top_k, int H, int I) {
         L.src_token = take(sizeof(int) * P);
         L.chunks = static_cast<int>((P + kChunk - 1) / kChunk);
         L.chunk_counts = take(sizeof(int) * static_cast<size_t>(L.chunks) * experts);
-        L.chunk_base = take(sizeof(int) * static_cast<size_t>(L.chunks) * experts);
     }
     L.gu = take(sizeof(float) * P * 2 * I);
     L.h = take(sizeof(float) * P * I);
@@ -338,77 +337,98 @@ __device__ int block_exclusive_scan(int v, int* buf) {
     return inclusive - v;
 }
 
-// Stable counting sort of the (token, slot) pairs by expert, in three steps:
-// a per-chunk expert histogram (moe_count_kernel), one workgroup that turns
-// the histograms into group starts, per-chunk bases and the tile table
-// (moe_scan_kernel), and a per-chunk scatter where each pair's rank is the
-// number of earlier pairs of its chunk with the same expert
-// (moe_scatter_kernel).  Every expert's group therefore lists its pairs in
-// (token, slot) order and positions are identical on every run.  Pairs with
-// an id outside [0, experts) get position -1.
-__global__ __launch_bounds__(kChunk) void moe_count_kernel(const int* __restrict__ ids, int P, int experts,
-                                                           int* __restrict__ chunk_counts) {
-    __shared__ int hist[kRouterMaxExperts];
-    for (int e = threadIdx.x; e < experts; e += kChunk) hist[e] = 0;
+// Stable counting sort of the (token, slot) pairs by expert, in two
+// launches: per chunk of kChunk pairs, the expert histogram and each pair's
+// rank -- the number of earlier pairs of its chunk with the same expert:
+// within a wave the lanes with the same id found by one ballot per distinct
+// id, across the chunk's waves an exclusive sum of the waves' counts
+// (moe_rank_kernel); then a workgroup per chunk that sums the histograms
+// into its chunk's base for every expert (group start plus the expert's
+// pairs in earlier chunks) and places its pairs at base + rank, workgroup 0
+// also writing the tile table (moe_place_kernel).  Every expert's group
+// therefore lists its pairs in (token, slot) order and positions are
+// identical on every run.  Pairs with an id outside [0, experts) get
+// position -1.
+__global__ __launch_bounds__(kChunk) void moe_rank_kernel(const int* __restrict__ ids, int P, int experts,
+                                                          int* __restrict__ chunk_counts, int* __restrict__ rank_of_pair) {
+    constexpr int kWaves = kChunk / kWave;
+    __shared__ int wave_count[kWaves][kRouterMaxExperts];  // per wave and expert: count, then exclusive base
+    for (int i = threadIdx.x; i < kWaves * experts; i += kChunk) wave_count[i / experts][i % experts] = 0;
     __syncthreads();
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
     const int p = blockIdx.x * kChunk + threadIdx.x;
-    if (p < P) {
-        const int e = ids[p];
-        if (e >= 0 && e < experts) atomicAdd(&hist[e], 1);  // integer count: order-free
+    const int e = p < P ? ids[p] : -1;
+    const bool valid = e >= 0 && e < experts;
+    // Lanes of this wave with the same id: one ballot per distinct id.
+    uint64_t same = 0;
+    uint64_t open = __ballot(1);
+    while (open) {
+        const int v = __builtin_amdgcn_readlane(e, __builtin_ctzll(open));
+        const uint64_t m = __ballot(e == v);
+        if (e == v) same = m;
+        open &= ~m;
+    }
+    const int rank_in_wave = __popcll(same & ((1ull << lane) - 1));
+    if (valid && rank_in_wave == 0) wave_count[wave][e] = __popcll(same);
+    __syncthreads();
+    for (int x = threadIdx.x; x < experts; x += kChunk) {
+        int run = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const int c = wave_count[w][x];
+            wave_count[w][x] = run;
+            run += c;
+        }
+        chunk_counts[static_cast<size_t>(blockIdx.x) * experts + x] = run;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < experts; e += kChunk)
-        chunk_counts[static_cast<size_t>(blockIdx.x) * experts + e] = hist[e];
+    if (p < P) rank_of_pair[p] = valid ? wave_count[wave][e] + rank_in_wave : -1;
 }
 
-__global__ __launch_bounds__(kGroupThreads) void moe_scan_kernel(
-    const int* __restrict__ chunk_counts, int chunks, int experts, int bm, int* __restrict__ chunk_base,
-    int* __restrict__ tile_expert, int* __restrict__ tile_start, int* __restrict__ tile_count,
-    int* __restrict__ ntiles, int* __restrict__ nvalid) {
+__global__ __launch_bounds__(kGroupThreads) void moe_place_kernel(
+    const int* __restrict__ chunk_counts, int chunks, int experts, int bm, int* __restrict__ tile_expert,
+    int* __restrict__ tile_start, int* __restrict__ tile_count, int* __restrict__ ntiles, int* __restrict__ nvalid,
+    const int* __restrict__ ids, int P, int top_k, int* __restrict__ pos_of_pair, int* __restrict__ src_token) {
+    static_assert(kChunk == kGroupThreads, "one workgroup per chunk, a pair per thread");
     __shared__ int buf[kGroupThreads];
+    __shared__ int chunk_base[kRouterMaxExperts];
     const int e = threadIdx.x;
     const bool owner = e < experts;
-    int total = 0;
+    // Expert e's pairs in all chunks and in the chunks before this one.
+    int total = 0, before = 0;
     if (owner) {
 #pragma unroll 8
-        for (int c = 0; c < chunks; ++c) total += chunk_counts[static_cast<size_t>(c) * experts + e];
-    }
-    const int start = block_exclusive_scan(total, buf);
-    if (owner) {
-        int run = start;
         for (int c = 0; c < chunks; ++c) {
-            const size_t at = static_cast<size_t>(c) * experts + e;
-            chunk_base[at] = run;
-            run += chunk_counts[at];
+            const int v = chunk_counts[static_cast<size_t>(c) * experts + e];
+            before += c < static_cast<int>(blockIdx.x) ? v : 0;
+            total += v;
         }
     }
-    const int tiles = owner ? (total + bm - 1) / bm : 0;
-    const int tile0 = block_exclusive_scan(tiles, buf);
-    for (int j = 0; j < tiles; ++j) {
-        tile_expert[tile0 + j] = e;
-        tile_start[tile0 + j] = start + j * bm;
-        tile_count[tile0 + j] = min(bm, total - j * bm);
+    const int start = block_exclusive_scan(total, buf);
+    if (owner) chunk_base[e] = start + before;
+    if (blockIdx.x == 0) {
+        const int tiles = owner ? (total + bm - 1) / bm : 0;
+        const int tile0 = block_exclusive_scan(tiles, buf);
+        for (int j = 0; j < tiles; ++j) {
+            tile_expert[tile0 + j] = e;
+            tile_start[tile0 + j] = start + j * bm;
+            tile_count[tile0 + j] = min(bm, total - j * bm);
+        }
+        if (e == kGroupThreads - 1) { *ntiles = tile0 + tiles; *nvalid = start + total; }
     }
-    if (e == kGroupThreads - 1) { *ntiles = tile0 + tiles; *nvalid = start + total; }
-}
-
-__global__ __launch_bounds__(kChunk) void moe_scatter_kernel(const int* __restrict__ ids, int P, int top_k,
-                                                             int experts, const int* __restrict__ chunk_base,
-                                                             int* __restrict__ pos_of_pair,
-                                                             int* __restrict__ src_token) {
-    __shared__ int chunk_ids[kChunk];
-    const int t = threadIdx.x;
-    const int p = blockIdx.x * kChunk + t;
-    const int e = p < P ? ids[p] : -1;
-    chunk_ids[t] = e;
     __syncthreads();
-    if (p >= P) return;
-    if (e < 0 || e >= experts) { pos_of_pair[p] = -1; return; }
-    int rank = 0;
-    for (int u = 0; u < t; ++u) rank += chunk_ids[u] == e;
-    const int pos = chunk_base[static_cast<size_t>(blockIdx.x) * experts + e] + rank;
-    pos_of_pair[p] = pos;
-    src_token[pos] = p / top_k;
+    // This chunk's pairs at base + rank (moe_rank_kernel's rank, in place in
+    // pos_of_pair).
+    const int p = blockIdx.x * kChunk + threadIdx.x;
+    if (p < P) {
+        const int rank = pos_of_pair[p];
+        if (rank >= 0) {
+            const int pos = chunk_base[ids[p]] + rank;
+            pos_of_pair[p] = pos;
+            src_token[pos] = p / top_k;
+        }
+    }
 }
 
 // Grouped GEMM policy: tile ty is the tile table's entry; A rows are
@@ -833,16 +853,13 @@ int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, 
     float* d = reinterpret_cast<float*>(ws + L.d);
 
     int* chunk_counts = reinterpret_cast<int*>(ws + L.chunk_counts);
-    int* chunk_base = reinterpret_cast<int*>(ws + L.chunk_base);
-    hipLaunchKernelGGL(moe_count_kernel, dim3(L.chunks), dim3(kChunk), 0, stream, ids, P, experts, chunk_counts);
+    hipLaunchKernelGGL(moe_rank_kernel, dim3(L.chunks), dim3(kChunk), 0, stream, ids, P, experts, chunk_counts,
+                       pos_of_pair);
     int status = launch_status();
     if (status != Q3X_HIP_OK) return status;
-    hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(kGroupThreads), 0, stream,
-                       static_cast<const int*>(chunk_counts), L.chunks, experts, BM, chunk_base, tile_expert,
-                       tile_start, tile_count, ntiles, nvalid);
-    if ((status = launch_status()) != Q3X_HIP_OK) return status;
-    hipLaunchKernelGGL(moe_scatter_kernel, dim3(L.chunks), dim3(kChunk), 0, stream, ids, P, top_k, experts,
-                       static_cast<const int*>(chunk_base), pos_of_pair, src_token);
+    hipLaunchKernelGGL(moe_place_kernel, dim3(L.chunks), dim3(kGroupThreads), 0, stream,
+                       static_cast<const int*>(chunk_counts), L.chunks, experts, BM, tile_expert, tile_start,
+                       tile_count, ntiles, nvalid, ids, P, top_k, pos_of_pair, src_token);
     if ((status = launch_status()) != Q3X_HIP_OK) return status;
 
     const size_t gu_row = static_cast<size_t>(H / kBlock) * BB;
