@@ -369,7 +369,8 @@ def cpu_matvecs(cpu, mats, seconds):
 def gemm_entry(torch, q3x, mats, X, H, Ys, count, ms_plain, flops, replays):
     """A GEMM config's line: q3x_hip_gemm_ws with the workspace its plan asks
     for (K split over workgroups where few tiles meet a long K) when any
-    matrix splits, q3x_hip_gemm beside it; otherwise q3x_hip_gemm alone."""
+    matrix splits, q3x_hip_gemm beside it; otherwise q3x_hip_gemm alone.
+    replays: (calls per graph, replays) as the plain timing used."""
     plain = {"TFLOPs": flops / (ms_plain * 1e-3) / 1e12, "ms": ms_plain,
              "frac_x3_peak": flops / (ms_plain * 1e-3) / 1e12 / X3_PEAK_TFLOPS}
     need = max(q3x.gemm_workspace_bytes(mm.linear, count) for mm in mats)
@@ -380,7 +381,7 @@ def gemm_entry(torch, q3x, mats, X, H, Ys, count, ms_plain, flops, replays):
     def run(i):
         for mm in mats:
             q3x.batch_mv_ws(mm.linear, H if mm.name == "down" else X, Ys[mm.name], count, ws)
-    ms = time_graph(torch, run, 1, replays)
+    ms = time_graph(torch, run, *replays)
     del ws
     return {"TFLOPs": flops / (ms * 1e-3) / 1e12, "ms": ms, "frac_x3_peak": flops / (ms * 1e-3) / 1e12 / X3_PEAK_TFLOPS,
             "workspace_bytes": need, "split_k": {mm.name: q3x.gemm_workspace_bytes(mm.linear, count) > 0 for mm in mats},
@@ -419,10 +420,12 @@ def extra_configs(torch, q3x, wl, only=None, cpu=False):
             def run(i):
                 for mm in mats:
                     q3x.batch_mv(mm.linear, H if mm.name == "down" else X, Ys[mm.name], count)
-            ms = time_graph(torch, run, 1, 4 if count == 4096 else 10)
+            # Several calls to a graph replay where a call is short, so that the
+            # replay's own launch is a small share of the timed span.
+            shape = (1, 4) if count == 4096 else (4, 3)
+            ms = time_graph(torch, run, *shape)
             flops = sum(2.0 * count * mm.rows * mm.cols for mm in mats)
-            out[f"cfg2_q8_gemm_N{count}"] = gemm_entry(torch, q3x, mats, X, H, Ys, count, ms, flops,
-                                                       4 if count == 4096 else 10)
+            out[f"cfg2_q8_gemm_N{count}"] = gemm_entry(torch, q3x, mats, X, H, Ys, count, ms, flops, shape)
             del X, H, Ys
         if ref_cpu:
             # one token through gate, up and down, the reference's prefill unit
@@ -482,9 +485,9 @@ def extra_configs(torch, q3x, wl, only=None, cpu=False):
         def run_gemm(i):
             for mm in mats:
                 q3x.batch_mv(mm.linear, H if mm.name == "down" else X, Ys[mm.name], 512)
-        ms = time_graph(torch, run_gemm, 1, 10)
+        ms = time_graph(torch, run_gemm, 4, 3)
         flops = sum(2.0 * 512 * mm.rows * mm.cols for mm in mats)
-        out["cfg3_q4_gemm_N512"] = gemm_entry(torch, q3x, mats, X, H, Ys, 512, ms, flops, 10)
+        out["cfg3_q4_gemm_N512"] = gemm_entry(torch, q3x, mats, X, H, Ys, 512, ms, flops, (4, 3))
         if ref_cpu:
             t, reps = cpu_matvecs(ref_cpu, mats, 2.0)
             out["cfg3_q4_mv_27b_ffn"]["cpu_baseline"] = ref_cpu.entry(
@@ -512,7 +515,7 @@ def extra_configs(torch, q3x, wl, only=None, cpu=False):
             def run_moe(i):
                 q3x.moe_routed_logits(moe.gate_up_linear, moe.down_linear, X, T, logits, k, ids, wts, Y,
                                       workspace=wsb)
-            ms = time_graph(torch, run_moe, 20 if T == 1 else 1, 10 if T == 1 else 5)
+            ms = time_graph(torch, run_moe, 20 if T == 1 else 4, 10 if T == 1 else 3)
             router_ms = time_graph(torch, lambda i: q3x.router_top_k(logits, T, moe.experts, k, ids, wts), 20, 5)
             if T == 1:
                 per_expert = (moe.gate_up.numel() + moe.down.numel()) // moe.experts
@@ -600,8 +603,8 @@ def extra_configs(torch, q3x, wl, only=None, cpu=False):
             X = wl.activations(4, T, H, salt=9)
             Y = torch.empty((T, H), dtype=torch.float32, device="cuda")
             wsl = torch.empty(q3x.moe_layer_workspace_bytes(layer, T), dtype=torch.uint8, device="cuda")
-            ms = time_graph(torch, lambda i: q3x.moe_layer(layer, X, T, Y, workspace=wsl), 20 if T == 1 else 1,
-                            10 if T == 1 else 5)
+            ms = time_graph(torch, lambda i: q3x.moe_layer(layer, X, T, Y, workspace=wsl), 20 if T == 1 else 4,
+                            10 if T == 1 else 3)
             if T == 1:
                 per_expert = (moe.gate_up.numel() + moe.down.numel()) // moe.experts
                 alg = 2 * (E + 1) * H + k * per_expert + shared_bytes
