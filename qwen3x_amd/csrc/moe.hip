@@ -910,16 +910,20 @@ template <uint32_t QT>
 int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
                 int tokens, const int* ids, const float* weights, int top_k, float* Y, int accumulate,
                 uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
-    // 64 pairs x 256 weight rows on 8 waves of 32x64: 64 pairs (an expert's
-    // average at 2048 tokens x top 8 of 256 experts) keep the padding of an
-    // expert's short last tile low, and the wide wave tile gives each
-    // activation split and scale fold twice the matrix work of a 32x32 one.
-    // At config 4 (T = 2048), alternating runs of one box: 162-180 TFLOP/s
-    // against 145-160 for 64 x 128 on 32x32 waves; 64 x 512 on 8 waves of
-    // 64x64, 64 x 256 on 8 waves of 64x32 or on 4 of 64x64, 64 x 512 on 8
-    // waves of 32x128, 64 x 128 on 4 waves of 32x64 and 64 x 256 on 16
-    // waves of 32x32 all fell between the two.
-    return moe_grouped_tiles<QT, 2, 4, 2, 4>(gate_up, down, experts, H, I, X, tokens, ids, weights, top_k, Y,
+    // 80 pairs x 256 weight rows on 8 waves of 80x32.  At 2048 tokens x top
+    // 8 of 256 experts an expert averages 64 pairs (standard deviation about
+    // 8): 64-pair tiles give about half of the experts a second, nearly
+    // empty tile that brings the expert's weight rows into the CU again (378
+    // tiles for 256 experts at config 4), 80-pair tiles give 261, and the
+    // 80x32 wave tile keeps the register count at 128, so two workgroups
+    // still share a CU.  Alternating runs of one box at config 4: 197-201
+    // TFLOP/s against 188-192 for 64 x 256 on 8 waves of 32x64; 96 x 256 on
+    // 12 waves of 32x64 (one workgroup a CU) 191-193, on 8 waves of 48x64
+    // (164 registers) 182.  Earlier, with 64-pair tiles: 64 x 128 on 32x32
+    // waves, 64 x 512 on 8 waves of 64x64 or 32x128, 64 x 256 on 8 waves of
+    // 64x32, on 4 of 64x64 or on 16 of 32x32, and 64 x 128 on 4 waves of
+    // 32x64 all ran slower than 64 x 256 on 32x64 waves.
+    return moe_grouped_tiles<QT, 1, 8, 5, 2>(gate_up, down, experts, H, I, X, tokens, ids, weights, top_k, Y,
                                              accumulate, ws, L, stream);
 }
 
