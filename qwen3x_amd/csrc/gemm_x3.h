@@ -394,10 +394,12 @@ __global__ __launch_bounds__(KS * WM * WN * kWave) void gemm_x3_kernel(Policy po
 // The stores of a split launch, one output value per thread: value f (in
 // the units' layout, f = v * NT + t for value v of thread t) of tile
 // blockIdx.x / (BM * BN / 256), its units added in K order (unit 0 first),
-// stored where gemm_x3_kernel's thread t would store its value v.
+// stored where gemm_x3_kernel's thread t would store its value v.  With
+// kPaired columns the thread of an even column block stores the pair, its
+// partner's value (column block j + 1, the same lane, row and e) summed the
+// same way, and the thread of the odd block stores nothing.
 template <int WM, int WN, int SM, int SN, class Policy>
 __global__ __launch_bounds__(256) void gemm_x3_fixup_kernel(Policy pol, int rows) {
-    static_assert(!Policy::kPairedColumns, "split launches store single columns");
     constexpr int NT = WM * WN * kWave;
     constexpr int BM = WM * SM * 16, BN = WN * SN * 16;
     constexpr int U = static_cast<int>(x3_unit_floats<WM, WN, SM, SN>());  // BM * BN
@@ -409,15 +411,24 @@ __global__ __launch_bounds__(256) void gemm_x3_fixup_kernel(Policy pol, int rows
     if (!pol.tile(t / pol.tiles_x, BM, tile)) return;
     const int S = pol.ksplit;
     const float* units = pol.part + static_cast<size_t>(t) * S * U;
-    float sum = units[f];
-    for (int u = 1; u < S; ++u) sum += units[static_cast<size_t>(u) * U + f];
+    auto unit_sum = [&](int g) {
+        float sum = units[g];
+        for (int u = 1; u < S; ++u) sum += units[static_cast<size_t>(u) * U + g];
+        return sum;
+    };
     const int v = f / NT, tid = f % NT;
     const int i = v / (SN * 4), j = (v / 4) % SN, e = v % 4;
     const int lane = tid & (kWave - 1), wave = tid / kWave;
     const int wm = wave / WN, wn = wave % WN, l16 = lane & 15, g16 = lane >> 4;
     const int m = 16 * (i * WM + wm) + 4 * g16 + e;
     const int n = (t % pol.tiles_x) * BN + (wn * SN + j) * 16 + l16;
-    if (m < tile.mcount && n < rows) pol.store(tile, m, n, sum);
+    if (m >= tile.mcount || n >= rows) return;
+    if constexpr (Policy::kPairedColumns) {
+        static_assert(SN % 2 == 0, "paired columns need column blocks in pairs");
+        if (j % 2 == 0) pol.store_pair(tile, m, n, unit_sum(f), unit_sum(f + 4 * NT));
+    } else {
+        pol.store(tile, m, n, unit_sum(f));
+    }
 }
 
 // Tile shapes of the launches: 128 A rows x 256 weight rows on 8 waves of
@@ -557,8 +568,12 @@ int launch_x3_tiles(P pol, int rows, int count, int cols, hipStream_t stream, in
     const long long tiles = static_cast<long long>(pol.tiles_x) * ((count + BM - 1) / BM);
     if (tiles * split > 0x7fffffffLL || (split > 1 && tiles * (BM * BN / 256) > 0x7fffffffLL))
         return Q3X_HIP_EINVAL;
-    if constexpr (HasKSplit<P>::value) pol.ksplit = split;
-    else if (split != 1) return Q3X_HIP_EINVAL;
+    if constexpr (HasKSplit<P>::value) {
+        if (split > 1 && pol.part == nullptr) return Q3X_HIP_EINVAL;  // the units' sums need a workspace
+        pol.ksplit = split;
+    } else if (split != 1) {
+        return Q3X_HIP_EINVAL;
+    }
     hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, P, PF, CF, KS>),
                        dim3(static_cast<unsigned>(tiles * split)), dim3(KS * WM * WN * kWave), 0, stream, pol, rows,
                        cols);

@@ -997,7 +997,9 @@ __global__ __launch_bounds__(256) void router_gemv_bf16_kernel(const uint16_t* _
 }
 
 // Dense GEMM policies over the tokens X[count, cols] (1-D grid, tiles of BM
-// tokens); each adds its weight rows and its store.
+// tokens); each adds its weight rows and its store.  Given a workspace
+// (part), a launch may split K over workgroups (gemm_x3_fixup_kernel adds
+// the units in K order and stores).
 struct TokenTiles {
     static constexpr bool kLinearGrid = true;
     static constexpr bool kPairedColumns = false;
@@ -1006,6 +1008,8 @@ struct TokenTiles {
     const float* X;
     int cols;
     int count;
+    int ksplit = 1;         // units per tile over K (set by the launch)
+    float* part = nullptr;  // their partial sums
     __device__ bool tile(int ty, int bm, GemmTile& t) const {
         t.m0 = ty * bm;
         t.mcount = min(bm, count - t.m0);
@@ -1086,9 +1090,17 @@ struct SharedDownAdd : TokenTiles {
     }
 };
 
+// part / part_bytes: the K split's workspace (none: no split).  Calls that
+// share it must be ordered, as calls on one stream are.
 template <uint32_t QT, class P>
-int launch_token_gemm(const P& pol, int rows, hipStream_t stream) {
-    return launch_x3<QT>(pol, rows, pol.count, pol.cols, stream);
+int launch_token_gemm(P pol, int rows, hipStream_t stream, float* part = nullptr, size_t part_bytes = 0) {
+    pol.part = part;
+    return launch_x3<QT>(pol, rows, pol.count, pol.cols, stream, part ? part_bytes : 0);
+}
+
+// Workspace bytes of the K split launch_x3 plans for a token GEMM.
+inline size_t token_gemm_part_bytes(int rows, int count, int cols, bool paired) {
+    return x3_plan(rows, count, cols, paired, static_cast<size_t>(-1)).workspace_bytes();
 }
 
 inline int launch_router_topk(const float* logits, int tokens, int experts, int top_k, int* ids, float* weights,
@@ -1105,7 +1117,7 @@ inline int launch_router_topk(const float* logits, int tokens, int experts, int 
 }
 
 struct MoeLayerLayout {
-    size_t logits, gate, ids, weights, gu_s, h_s, routed, total;
+    size_t logits, gate, ids, weights, gu_s, h_s, part, part_bytes, routed, total;
     MoeLayout R;
 };
 
@@ -1120,6 +1132,16 @@ inline MoeLayerLayout moe_layer_layout(int tokens, int experts, int top_k, int H
     L.weights = take(sizeof(float) * T * top_k);
     L.gu_s = take(sizeof(float) * T * 2 * shared_I);
     L.h_s = take(sizeof(float) * T * shared_I);
+    // The K split of the prefill's token GEMMs (router, shared expert), one
+    // at a time on the layer's stream.
+    L.part_bytes = 0;
+    if (tokens > 1) {
+        L.part_bytes = std::max({token_gemm_part_bytes(experts + 1, tokens, H, false),
+                                 token_gemm_part_bytes(2 * shared_I, tokens, H, shared_I % 64 == 0),
+                                 token_gemm_part_bytes(shared_I, tokens, H, false),
+                                 token_gemm_part_bytes(H, tokens, shared_I, false)});
+    }
+    L.part = take(L.part_bytes);
     L.R = moe_layout(tokens, experts, top_k, H, I);
     L.routed = take(L.R.total);
     L.total = off;
@@ -1139,6 +1161,7 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
     int* sel = ids ? ids : reinterpret_cast<int*>(ws + L.ids);
     float* wts = weights ? weights : reinterpret_cast<float*>(ws + L.weights);
     uint8_t* rws = ws + L.routed;
+    float* part = L.part_bytes ? reinterpret_cast<float*>(ws + L.part) : nullptr;
     const auto* router = static_cast<const uint8_t*>(w.router);
     const auto* gate_row = static_cast<const uint8_t*>(w.shared_scale);
     const auto* gate_up = static_cast<const uint8_t*>(w.gate_up);
@@ -1167,7 +1190,7 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
         g.X = X; g.cols = H; g.count = tokens;
         g.router = router; g.gate_row = gate_row; g.row_bytes = static_cast<size_t>(H) * 2; g.experts = E;
         g.logits = logits; g.gate_logit = gate;
-        status = launch_token_gemm<Q3X_HIP_MATRIX_BF16>(g, E + 1, stream);
+        status = launch_token_gemm<Q3X_HIP_MATRIX_BF16>(g, E + 1, stream, part, L.part_bytes);
     }
     if (status != Q3X_HIP_OK) return status;
 
@@ -1191,7 +1214,7 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
         PairedGateUpGemm g{};
         g.X = X; g.cols = H; g.count = tokens;
         g.gate = sg; g.up = su; g.row_bytes = gu_row; g.I = SI; g.h = h_s;
-        status = launch_token_gemm<QT>(g, 2 * SI, stream);
+        status = launch_token_gemm<QT>(g, 2 * SI, stream, part, L.part_bytes);
         if (status != Q3X_HIP_OK) return status;
     } else {
         float* gu_s = reinterpret_cast<float*>(ws + L.gu_s);
@@ -1199,9 +1222,9 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
         g.X = X; g.cols = H; g.count = tokens;
         g.row_bytes = gu_row; g.out = gu_s; g.out_stride = 2 * SI;
         g.w = sg; g.col0 = 0;
-        if ((status = launch_token_gemm<QT>(g, SI, stream)) != Q3X_HIP_OK) return status;
+        if ((status = launch_token_gemm<QT>(g, SI, stream, part, L.part_bytes)) != Q3X_HIP_OK) return status;
         g.w = su; g.col0 = SI;
-        if ((status = launch_token_gemm<QT>(g, SI, stream)) != Q3X_HIP_OK) return status;
+        if ((status = launch_token_gemm<QT>(g, SI, stream, part, L.part_bytes)) != Q3X_HIP_OK) return status;
         const size_t n = static_cast<size_t>(tokens) * SI;
         hipLaunchKernelGGL(swiglu_kernel, dim3(static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 65536))),
                            dim3(256), 0, stream, gu_s, h_s, SI, tokens, nullptr);
@@ -1210,7 +1233,7 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
     SharedDownAdd g{};
     g.X = h_s; g.cols = SI; g.count = tokens;
     g.w = sd; g.row_bytes = sd_row; g.Y = Y; g.H = H; g.gate_logit = gate;
-    return launch_token_gemm<QT>(g, H, stream);
+    return launch_token_gemm<QT>(g, H, stream, part, L.part_bytes);
 }
 
 }  // namespace q3x
