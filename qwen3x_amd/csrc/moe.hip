@@ -219,10 +219,15 @@ __device__ __forceinline__ bool router_select_by_exp(const float* __restrict__ r
 }
 
 // One wavefront per token (router_topk_wave); lane s < top_k writes slot s.
+// With ext_ids, the token's pairs also go to ext_ids / ext_weights [tokens,
+// top_k + 1], slot top_k being the shared expert: id `experts`, weight
+// sigmoid(shared_logit[token]) (engine.cpp:427-429).
 template <int PER>
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int tokens,
                                                           int experts, int top_k, int* __restrict__ ids,
-                                                          float* __restrict__ weights) {
+                                                          float* __restrict__ weights, int* __restrict__ ext_ids,
+                                                          float* __restrict__ ext_weights,
+                                                          const float* __restrict__ shared_logit) {
     __shared__ __attribute__((aligned(16))) float probs[4][kRouterMaxExperts];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -234,6 +239,11 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
     if (lane < top_k) {
         ids[static_cast<size_t>(token) * top_k + lane] = id;
         weights[static_cast<size_t>(token) * top_k + lane] = weight;
+    }
+    if (ext_ids && lane <= top_k) {
+        const size_t at = static_cast<size_t>(token) * (top_k + 1) + lane;
+        ext_ids[at] = lane < top_k ? id : experts;
+        ext_weights[at] = lane < top_k ? weight : sigmoid_ref(shared_logit[token]);
     }
 }
 
@@ -455,6 +465,11 @@ struct GroupedGemm {
     const int* ntiles;
     float* out;
     int out_cols;
+    // A shared expert grouped as expert shared_group: its own matrix
+    // (shared_rows; for the gate_up GEMM the gate, shared_up the up).
+    int shared_group = -1;
+    const uint8_t* shared_rows = nullptr;
+    const uint8_t* shared_up = nullptr;
     __device__ int linear_total() const { return *ntiles * tiles_x; }
     __device__ bool tile(int ty, int, GemmTile& t) const {
         if (ty >= *ntiles) return false;
@@ -469,6 +484,7 @@ struct GroupedGemm {
         return A + static_cast<size_t>(row) * a_cols;
     }
     __device__ const uint8_t* b_row(const GemmTile& t, int n) const {
+        if (t.group == shared_group) return shared_rows + static_cast<size_t>(n) * row_bytes;
         return pool + static_cast<size_t>(t.group) * expert_bytes + static_cast<size_t>(n) * row_bytes;
     }
     __device__ void store(const GemmTile& t, int m, int n, float v) const {
@@ -489,6 +505,7 @@ struct GroupedGateUp : GroupedGemm {
     __device__ static int out_col(int n) { return 64 * (n >> 7) + 16 * ((n >> 5) & 3) + (n & 15); }
     __device__ const uint8_t* b_row(const GemmTile& t, int n) const {
         const int j = out_col(n);
+        if (t.group == shared_group) return ((n & 16) ? shared_up : shared_rows) + static_cast<size_t>(j) * row_bytes;
         const int row = (n & 16) ? I + j : j;
         return pool + static_cast<size_t>(t.group) * expert_bytes + static_cast<size_t>(row) * row_bytes;
     }
@@ -833,10 +850,19 @@ int moe_decode(const uint8_t* gate_up, const uint8_t* down, int experts, int H, 
     return Q3X_HIP_ENOTSUP;
 }
 
+// A shared expert that the grouped GEMMs take as group `group` (its gate,
+// up and down matrices of the routed experts' shapes); group -1: none.
+struct GroupedShared {
+    int group = -1;
+    const uint8_t* gate = nullptr;
+    const uint8_t* up = nullptr;
+    const uint8_t* down = nullptr;
+};
+
 template <uint32_t QT, int WM, int WN, int SM, int SN>
 int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
                 int tokens, const int* ids, const float* weights, int top_k, float* Y, int accumulate,
-                uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
+                uint8_t* ws, const MoeLayout& L, hipStream_t stream, const GroupedShared& shared) {
     constexpr int BB = QT == Q3X_HIP_MATRIX_Q8_0 ? kQ8Bytes : kQ4Bytes;
     constexpr int BM = WM * SM * 16, BN = WN * SN * 16, NT = WM * WN * kWave;
     static_assert(BM >= kGrpBM, "the workspace bounds the tile count for kGrpBM-pair tiles");
@@ -873,10 +899,14 @@ int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, 
                                                     tile_expert, tile_start, tile_count, ntiles, nullptr, 0};
         g1.I = I;
         g1.h = h;
+        g1.shared_group = shared.group;
+        g1.shared_rows = shared.gate;
+        g1.shared_up = shared.up;
         hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, GroupedGateUp>), dim3(nx * tiles_bound), dim3(NT), 0,
                            stream, g1, 2 * I, H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
     } else {
+        if (shared.group >= 0) return Q3X_HIP_ENOTSUP;  // a shared group needs the paired gate_up
         const int nx = (2 * I + BN - 1) / BN;
         GroupedGemm g1{nx, X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
                        ntiles, gu, 2 * I};
@@ -892,6 +922,8 @@ int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, 
     const int nx2 = (H + BN - 1) / BN;
     GroupedGemm g2{nx2, h, I, nullptr, down, down_row * H, down_row, tile_expert, tile_start, tile_count,
                    ntiles, d, H};
+    g2.shared_group = shared.group;
+    g2.shared_rows = shared.down;
     hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, GroupedGemm>), dim3(nx2 * tiles_bound), dim3(NT), 0,
                        stream, g2, H, I);
     if ((status = launch_status()) != Q3X_HIP_OK) return status;
@@ -909,7 +941,7 @@ int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, 
 template <uint32_t QT>
 int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H, int I, const float* X,
                 int tokens, const int* ids, const float* weights, int top_k, float* Y, int accumulate,
-                uint8_t* ws, const MoeLayout& L, hipStream_t stream) {
+                uint8_t* ws, const MoeLayout& L, hipStream_t stream, const GroupedShared& shared = {}) {
     // 80 pairs x 256 weight rows on 8 waves of 80x32.  At 2048 tokens x top
     // 8 of 256 experts an expert averages 64 pairs (standard deviation about
     // 8): 64-pair tiles give about half of the experts a second, nearly
@@ -924,7 +956,7 @@ int moe_grouped(const uint8_t* gate_up, const uint8_t* down, int experts, int H,
     // 64x32, on 4 of 64x64 or on 16 of 32x32, and 64 x 128 on 4 waves of
     // 32x64 all ran slower than 64 x 256 on 32x64 waves.
     return moe_grouped_tiles<QT, 1, 8, 5, 2>(gate_up, down, experts, H, I, X, tokens, ids, weights, top_k, Y,
-                                             accumulate, ws, L, stream);
+                                             accumulate, ws, L, stream, shared);
 }
 
 // ------------------------------------------------------------ MoE layer ----
@@ -1104,20 +1136,19 @@ inline size_t token_gemm_part_bytes(int rows, int count, int cols, bool paired) 
 }
 
 inline int launch_router_topk(const float* logits, int tokens, int experts, int top_k, int* ids, float* weights,
-                              hipStream_t stream) {
+                              hipStream_t stream, int* ext_ids = nullptr, float* ext_weights = nullptr,
+                              const float* shared_logit = nullptr) {
     const dim3 grid((tokens + 3) / 4), block(256);
-    if (experts <= 4 * kWave)
-        hipLaunchKernelGGL(router_topk_kernel<4>, grid, block, 0, stream, logits, tokens, experts, top_k, ids, weights);
-    else if (experts <= 8 * kWave)
-        hipLaunchKernelGGL(router_topk_kernel<8>, grid, block, 0, stream, logits, tokens, experts, top_k, ids, weights);
-    else
-        hipLaunchKernelGGL(router_topk_kernel<16>, grid, block, 0, stream, logits, tokens, experts, top_k, ids,
-                           weights);
+    auto kernel = experts <= 4 * kWave ? router_topk_kernel<4> : experts <= 8 * kWave ? router_topk_kernel<8>
+                                                                                      : router_topk_kernel<16>;
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, logits, tokens, experts, top_k, ids, weights, ext_ids,
+                       ext_weights, shared_logit);
     return launch_status();
 }
 
 struct MoeLayerLayout {
-    size_t logits, gate, ids, weights, gu_s, h_s, part, part_bytes, routed, total;
+    size_t logits, gate, ids, weights, gu_s, h_s, part, part_bytes, pair_ids, pair_weights, routed, total;
+    bool fold;  // the prefill groups the shared expert with the routed ones
     MoeLayout R;
 };
 
@@ -1142,7 +1173,16 @@ inline MoeLayerLayout moe_layer_layout(int tokens, int experts, int top_k, int H
                                  token_gemm_part_bytes(H, tokens, shared_I, false)});
     }
     L.part = take(L.part_bytes);
-    L.R = moe_layout(tokens, experts, top_k, H, I);
+    // Where the shared expert has the routed experts' shape, the prefill
+    // runs it as group `experts` of the grouped GEMMs: every token's pair
+    // top_k, weighted by the sigmoid of its gate logit (pair_ids /
+    // pair_weights [tokens, top_k + 1]).
+    const long long pairs1 = static_cast<long long>(tokens) * (top_k + 1);
+    L.fold = tokens > 1 && shared_I == I && I % 64 == 0 && experts + 1 <= kRouterMaxExperts &&
+             pairs1 / kGrpBM + std::min<long long>(experts + 1, pairs1) + 1 <= 65535;
+    L.pair_ids = take(L.fold ? sizeof(int) * pairs1 : 0);
+    L.pair_weights = take(L.fold ? sizeof(float) * pairs1 : 0);
+    L.R = L.fold ? moe_layout(tokens, experts + 1, top_k + 1, H, I) : moe_layout(tokens, experts, top_k, H, I);
     L.routed = take(L.R.total);
     L.total = off;
     return L;
@@ -1201,6 +1241,24 @@ int moe_layer_run(const q3x_hip_moe_layer_weights& w, const float* X, int tokens
         status = moe_decode<QT>(gate_up, down, E, H, I, X, sel, wts, K, Y, accumulate ? 1 : 0, rws, L.R, shared,
                                 stream, norm_w, logits, sel, wts);
         if (status != Q3X_HIP_ENOTSUP || accumulate) return status;
+    }
+    if (L.fold) {
+        // Prefill: the shared expert as group E of the grouped GEMMs, its
+        // pair last in every token's combine: Y = fma(sigmoid(gate logit),
+        // shared, routed sum) (engine.cpp:426-429), as the separate shared
+        // GEMMs below add it.
+        int* pair_ids = reinterpret_cast<int*>(ws + L.pair_ids);
+        float* pair_wts = reinterpret_cast<float*>(ws + L.pair_weights);
+        if ((status = launch_router_topk(logits, tokens, E, K, sel, wts, stream, pair_ids, pair_wts, gate)) !=
+            Q3X_HIP_OK)
+            return status;
+        GroupedShared shared;
+        shared.group = E;
+        shared.gate = sg;
+        shared.up = su;
+        shared.down = sd;
+        return moe_grouped<QT>(gate_up, down, E + 1, H, I, X, tokens, pair_ids, pair_wts, K + 1, Y, 0, rws, L.R,
+                               stream, shared);
     }
     if ((status = launch_router_topk(logits, tokens, E, K, sel, wts, stream)) != Q3X_HIP_OK) return status;
     // Prefill (or an unaligned decode): the grouped routed experts write Y,
