@@ -15,7 +15,7 @@
 //     combines the slots in order (moe_down_combine_kernel);
 //   prefill (tokens > 1): the (token, slot) pairs are grouped by expert with
 //     a stable counting sort (deterministic positions), each expert's group is
-//     cut into tiles of 64 or 128 pairs, and one grouped GEMM launch
+//     cut into tiles of 80 pairs, and one grouped GEMM launch
 //     (gemm_x3.h: bf16 matrix cores, three exact products per FP32 product)
 //     runs gate_up for every tile of every expert with SwiGLU in its
 //     epilogue, then one runs down; a combine sums the slots of each token

@@ -95,7 +95,7 @@ CASES = [
     (Q4_0, 16, 256, 64, 64, 4, 1),       # unaligned down rows: decode through the grouped path
     (Q8_0, 16, 256, 256, 32, 4, 1),      # shared_I % 64 != 0: two strided GEMMs + SwiGLU
     (Q8_0, 16, 256, 256, 32, 4, 9),
-    (Q4_0, 8, 512, 128, 128, 4, 160),    # 80 pairs per expert: 128-pair grouped tiles
+    (Q4_0, 8, 512, 128, 128, 4, 160),    # 80 pairs per expert: whole 80-pair grouped tiles
 ]
 
 

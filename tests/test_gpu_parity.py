@@ -569,8 +569,8 @@ def moe_bound(gu, dn, type_, E, H, I, X, ids, wts):
     (Q4_0, 4, 32, 32, 2, 1), (Q4_0, 4, 32, 32, 2, 3), (Q4_0, 16, 256, 64, 4, 1), (Q4_0, 16, 256, 64, 4, 50),
     (Q8_0, 8, 512, 256, 2, 1), (Q8_0, 8, 512, 256, 2, 70), (Q4_0, 64, 2048, 512, 8, 1),
     (Q4_0, 64, 2048, 512, 8, 40),
-    # 32+ pairs per expert: the 128-pair tiles (one partial tile per expert;
-    # two tiles per expert, the second short)
+    # 100 and 150 pairs per expert: two and three 80-pair tiles per expert,
+    # the last one short
     (Q4_0, 8, 256, 64, 4, 200), (Q8_0, 4, 512, 128, 2, 300)])
 def test_moe_routed_parity(type_, E, H, I, top_k, tokens):
     torch = _torch()
