@@ -96,6 +96,7 @@ CASES = [
     (Q8_0, 16, 256, 256, 32, 4, 1),      # shared_I % 64 != 0: two strided GEMMs + SwiGLU
     (Q8_0, 16, 256, 256, 32, 4, 9),
     (Q4_0, 8, 512, 128, 128, 4, 160),    # 80 pairs per expert: whole 80-pair grouped tiles
+    (Q4_0, 32, 2048, 512, 256, 8, 40),   # prefill, shared expert narrower: its paired GEMM, K split
 ]
 
 
