@@ -395,7 +395,7 @@ __global__ __launch_bounds__(KS * WM * WN * kWave) void gemm_x3_kernel(Policy po
 // the units' layout, f = v * NT + t for value v of thread t) of tile
 // blockIdx.x / (BM * BN / 256), its units added in K order (unit 0 first),
 // stored where gemm_x3_kernel's thread t would store its value v.  With
-// kPaired columns the thread of an even column block stores the pair, its
+// kPairedColumns the thread of an even column block stores the pair, its
 // partner's value (column block j + 1, the same lane, row and e) summed the
 // same way, and the thread of the odd block stores nothing.
 template <int WM, int WN, int SM, int SN, class Policy>
