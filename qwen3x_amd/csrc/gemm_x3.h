@@ -42,7 +42,8 @@
 // before stage kb + 1's conversion instead, so the scheduler places the
 // split and the weight conversion in the matrix instructions' shadow; with
 // two stages of loads ahead it measures 1-4% slower on 64x64 wave tiles and
-// with smaller ones it costs a wave of occupancy, so no launch uses it.
+// on 32x32 ones it costs a wave of occupancy; the grouped MoE GEMMs' 80x32
+// wave tiles keep their occupancy with it and use it.
 //
 // A policy supplies the tiles and the operand rows: tile(ty, BM, tile)
 // (false: no such tile), a_row(tile, m) (an FP32 A row), b_row(tile, n) (a

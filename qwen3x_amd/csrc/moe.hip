@@ -37,6 +37,11 @@ constexpr int kChunk = 1024;               // pairs per grouping chunk
 // Grouped GEMM tiles (gemm_x3_kernel): at least kGrpBM pairs, which bounds
 // the tile count the workspace holds.
 constexpr int kGrpBM = 64;
+// The grouped GEMMs issue a stage's matrix instructions before the next
+// stage's conversion (gemm_x3_kernel's CF), which keeps their 80x32 wave
+// tiles at two workgroups per CU: in kernel traces of one box gate_up
+// 327-330 us against 334-336, down 166-168 against 168-171 (config 4).
+constexpr bool kGrpCF = true;
 
 // ---------------------------------------------------------------- router ----
 
@@ -902,7 +907,7 @@ int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, 
         g1.shared_group = shared.group;
         g1.shared_rows = shared.gate;
         g1.shared_up = shared.up;
-        hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, GroupedGateUp>), dim3(nx * tiles_bound), dim3(NT), 0,
+        hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, GroupedGateUp, 1, kGrpCF>), dim3(nx * tiles_bound), dim3(NT), 0,
                            stream, g1, 2 * I, H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
     } else {
@@ -910,7 +915,7 @@ int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, 
         const int nx = (2 * I + BN - 1) / BN;
         GroupedGemm g1{nx, X, H, src_token, gate_up, gu_row * 2 * I, gu_row, tile_expert, tile_start, tile_count,
                        ntiles, gu, 2 * I};
-        hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, GroupedGemm>), dim3(nx * tiles_bound), dim3(NT), 0,
+        hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, GroupedGemm, 1, kGrpCF>), dim3(nx * tiles_bound), dim3(NT), 0,
                            stream, g1, 2 * I, H);
         if ((status = launch_status()) != Q3X_HIP_OK) return status;
         const size_t sw = static_cast<size_t>(P) * I;
@@ -924,7 +929,7 @@ int moe_grouped_tiles(const uint8_t* gate_up, const uint8_t* down, int experts, 
                    ntiles, d, H};
     g2.shared_group = shared.group;
     g2.shared_rows = shared.down;
-    hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, GroupedGemm>), dim3(nx2 * tiles_bound), dim3(NT), 0,
+    hipLaunchKernelGGL((gemm_x3_kernel<QT, WM, WN, SM, SN, GroupedGemm, 1, kGrpCF>), dim3(nx2 * tiles_bound), dim3(NT), 0,
                        stream, g2, H, I);
     if ((status = launch_status()) != Q3X_HIP_OK) return status;
     const size_t outs = static_cast<size_t>(tokens) * H;
