@@ -172,29 +172,37 @@ __global__ __launch_bounds__(kConvThreads) void delta_conv_kernel(float* __restr
 #pragma unroll
     for (int i = 0; i < kMaxConv; ++i)
         if (i == CK - 1) last = wt[i];
-    constexpr int kAhead = 8;  // tokens whose inputs are requested together
-    float xs[kAhead];
-    for (int t = t0; t < t1; ++t) {
-        if ((t - t0) % kAhead == 0) {
+    // The run in batches of kAhead tokens, the next batch's inputs requested
+    // before the current batch is convolved (its rows are this run's own and
+    // not yet written), so one batch's loads are in flight while another
+    // computes.
+    constexpr int kAhead = 8;
+    float xs[kAhead], xn[kAhead];
+    auto fetch = [&](int b, float (&dst)[kAhead]) {
 #pragma unroll
-            for (int u = 0; u < kAhead; ++u)
-                xs[u] = t + u < t1 ? qkv[static_cast<size_t>(t + u) * channels + c] : 0.0f;
+        for (int u = 0; u < kAhead; ++u) dst[u] = b + u < t1 ? qkv[static_cast<size_t>(b + u) * channels + c] : 0.0f;
+    };
+    fetch(t0, xs);
+    for (int b = t0; b < t1; b += kAhead) {
+        fetch(b + kAhead, xn);
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u) {
+            if (b + u >= t1) break;
+            const float x = xs[u];
+            float sum = x * last;
+#pragma unroll
+            for (int i = 0; i < kMaxConv - 1; ++i)
+                if (i < CK - 1) sum = fmaf(past[i], wt[i], sum);
+#pragma unroll
+            for (int i = 0; i < kMaxConv - 2; ++i)
+                if (i < CK - 2) past[i] = past[i + 1];
+#pragma unroll
+            for (int i = 0; i < kMaxConv - 1; ++i)
+                if (i == CK - 2) past[i] = x;
+            qkv[static_cast<size_t>(b + u) * channels + c] = silu_ref(sum);
         }
-        float x = 0.0f;
 #pragma unroll
-        for (int u = 0; u < kAhead; ++u)
-            if (u == (t - t0) % kAhead) x = xs[u];
-        float sum = x * last;
-#pragma unroll
-        for (int i = 0; i < kMaxConv - 1; ++i)
-            if (i < CK - 1) sum = fmaf(past[i], wt[i], sum);
-#pragma unroll
-        for (int i = 0; i < kMaxConv - 2; ++i)
-            if (i < CK - 2) past[i] = past[i + 1];
-#pragma unroll
-        for (int i = 0; i < kMaxConv - 1; ++i)
-            if (i == CK - 2) past[i] = x;
-        qkv[static_cast<size_t>(t) * channels + c] = silu_ref(sum);
+        for (int u = 0; u < kAhead; ++u) xs[u] = xn[u];
     }
     if (t0 < t1 && t1 == count) {
 #pragma unroll
