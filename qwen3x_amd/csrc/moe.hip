@@ -336,20 +336,24 @@ inline MoeLayout moe_layout(int tokens, int experts, int top_k, int H, int I) {
 
 // ------------------------------------------------------------- grouping ----
 
-// Inclusive-to-exclusive block scan of v over kGroupThreads threads.
+// Exclusive scan of v over the kGroupThreads threads of the workgroup
+// (integers, so exact in any order): a shuffle scan inside each wave, then
+// each wave adds the totals of the waves before it (buf: kGroupThreads /
+// kWave ints of LDS).  Two barriers; the second frees buf for the next call.
 __device__ int block_exclusive_scan(int v, int* buf) {
-    const int t = threadIdx.x;
-    buf[t] = v;
-    __syncthreads();
-    for (int offset = 1; offset < kGroupThreads; offset <<= 1) {
-        const int add = t >= offset ? buf[t - offset] : 0;
-        __syncthreads();
-        buf[t] += add;
-        __syncthreads();
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    int x = v;
+#pragma unroll
+    for (int offset = 1; offset < kWave; offset <<= 1) {
+        const int y = __shfl_up(x, offset);
+        if (lane >= offset) x += y;
     }
-    const int inclusive = buf[t];
+    if (lane == kWave - 1) buf[wave] = x;
     __syncthreads();
-    return inclusive - v;
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += buf[w];
+    __syncthreads();
+    return before + x - v;
 }
 
 // Stable counting sort of the (token, slot) pairs by expert, in two
